@@ -1,0 +1,308 @@
+/*
+ * prichs_hip.h -- C ABI of libprichs_hip.so, the MI355X (gfx950) MoE
+ * feed-forward hot path of PRICHS.
+ *
+ * Reference paths below are relative to the PRICHS source tree.
+ *
+ * Three groups of entry points:
+ *
+ *  1. Legacy launchers with the exact signatures of the reference's CUDA
+ *     launchers (crates/prichs-cuda/src/kernels.cu; Rust extern block at
+ *     crates/prichs-cuda/src/engine.rs:89-272), so the existing Rust extern
+ *     declarations link against this library unchanged.  Like the originals
+ *     they return void; failures are recorded in prichs_last_error().
+ *
+ *  2. Stage entry points of the device-resident MoE forward (router + top-k,
+ *     permutation, grouped expert GEMMs, combine) and the memory-bound
+ *     RMSNorm / RoPE kernels.  They replace the host-side routing and the
+ *     per-expert cuBLAS loop of crates/prichs-model/src/model.rs:1125-1177.
+ *
+ *  3. An engine handle that owns packed weights and workspace and runs the
+ *     whole MoELayer forward (crates/prichs-model/src/moe.rs:93-225) on one
+ *     stream with no host round trip and no allocation per call.
+ *
+ * Conventions:
+ *  - Every non-legacy entry point returns PRICHS_OK (0) or a negative status.
+ *    The message of the last failure on the calling thread is available from
+ *    prichs_last_error().  Argument checks run before any HIP call, so invalid
+ *    arguments are reported even on a machine without a GPU.
+ *  - Pointers named dev_* or documented as device memory are device pointers.
+ *    `stream` is a hipStream_t (NULL = the default stream).  Calls are
+ *    asynchronous on that stream unless stated otherwise.
+ *  - Weights are accepted in the reference layouts: f32 row-major [K, N]
+ *    ("x @ W" form): gate/up [d, f], down [f, d], router [d, E]
+ *    (crates/prichs-model/src/moe.rs:16-18, 74).
+ *  - dtype codes: PRICHS_DTYPE_F32 (IEEE binary32) and PRICHS_DTYPE_BF16
+ *    (bfloat16 bit patterns in uint16 storage).
+ *  - Results of every entry point are deterministic: no floating-point
+ *    atomics on any path except the legacy launch_moe_scatter_add, which
+ *    keeps the reference's atomicAdd semantics.
+ */
+#ifndef PRICHS_HIP_H
+#define PRICHS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* Status codes, dtypes, diagnostics                                       */
+/* ---------------------------------------------------------------------- */
+enum {
+  PRICHS_OK = 0,
+  PRICHS_ERR_INVALID_ARGUMENT = -1, /* null pointer, bad shape, bad E/k   */
+  PRICHS_ERR_CAPACITY = -2,         /* exceeds a preallocated capacity    */
+  PRICHS_ERR_HIP = -3,              /* a HIP runtime call failed          */
+  PRICHS_ERR_UNSUPPORTED = -4,      /* valid but unsupported shape/dtype  */
+  PRICHS_ERR_STATE = -5             /* e.g. forward before weights upload */
+};
+
+enum { PRICHS_DTYPE_F32 = 0, PRICHS_DTYPE_BF16 = 1 };
+
+/* Limits of the stage kernels. */
+#define PRICHS_MAX_EXPERTS 64 /* routed experts E                       */
+#define PRICHS_MAX_TOPK 8     /* k                                      */
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char *prichs_last_error(void);
+/* Clears the calling thread's last error. */
+void prichs_clear_error(void);
+/* ABI version of this header (major * 10000 + minor * 100 + patch). */
+int prichs_abi_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* 1. Legacy launchers (identical signatures to the reference)             */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces launch_rmsnorm_forward (crates/prichs-cuda/src/kernels.cu:403-419,
+ * kernel 329-362).  Per row: rstd = 1/sqrt(mean(x^2) + eps),
+ * out = (x * rstd) * w; writes rstd[t].  f32 [seq_len, hidden_dim]. */
+void launch_rmsnorm_forward(const float *dev_x, const float *dev_weight,
+                            float *dev_out, float *dev_rstd_out, size_t seq_len,
+                            size_t hidden_dim, float eps, void *stream);
+
+/* Replaces launch_swiglu_forward (kernels.cu:482-496, kernel 444-457).
+ * out = silu(g) * u with silu(g) = g / (1 + exp(-g)) (the CPU formula of
+ * crates/prichs-core/src/ops.rs:137-140). */
+void launch_swiglu_forward(const float *dev_gate, const float *dev_up,
+                           float *dev_out, size_t total_elements, void *stream);
+
+/* Replaces launch_rope (kernels.cu:554-572, kernel 520-552).  In-place
+ * rotation of interleaved pairs of [seq_len, num_heads, head_dim] by
+ * cos/sin[t * head_dim/2 + i]; backward_sign (+1/-1) multiplies sin.  Like the
+ * original it has no position offset; prichs_rope_forward has one. */
+void launch_rope(float *dev_q_or_k, const float *dev_cos_cache,
+                 const float *dev_sin_cache, size_t seq_len, size_t num_heads,
+                 size_t head_dim, int backward_sign, void *stream);
+
+/* Replaces launch_moe_gather (kernels.cu:993-1007, kernel 888-904).
+ * out[i, :] = in[token_indices[i], :]. */
+void launch_moe_gather(const float *dev_in, const int *dev_token_indices,
+                       float *dev_out, size_t n_tokens, size_t hidden_dim,
+                       void *stream);
+
+/* Replaces launch_moe_scatter_add (kernels.cu:1009-1024, kernel 906-924).
+ * accum[token_indices[i], :] += weights[i] * exp_out[i, :] (atomic add, as in
+ * the reference; with distinct indices -- the reference's only use -- the
+ * result is deterministic). */
+void launch_moe_scatter_add(const float *dev_exp_out,
+                            const int *dev_token_indices,
+                            const float *dev_weights, float *dev_accum_out,
+                            size_t n_tokens, size_t hidden_dim, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* 2. Stage entry points                                                   */
+/* ---------------------------------------------------------------------- */
+
+/* Number of token blocks the router uses for T tokens and E experts; the
+ * block_counts workspace of prichs_router_topk holds blocks * E int32. */
+size_t prichs_router_num_blocks(size_t T, size_t E);
+
+/* Router + top-k gating.  Replaces forward_gemm(router) + the host loop
+ * (crates/prichs-cuda/src/engine.rs:757-826; crates/prichs-model/src/
+ * model.rs:1136-1151) and restates moe.rs:113-142 / ops.rs:219-248 on device:
+ *   raw[t,e] = sum_k x[t,k] * W[k,e]   (k ascending, no FMA: bit-exact with
+ *                                        the reference CPU GEMM),
+ *   adj = (raw + router_bias[e]) (+ concept_bias[e] for e < n_concept),
+ *   top-k by a stable descending order of adj (ties -> lower expert index),
+ *   weights = softmax of the RAW logits of the selected experts,
+ *   w = e_i / (sum e + 1e-9).
+ * x: [T, d] of x_dtype (device).  w_router: f32 [d, E] (device).
+ * router_bias: f32 [E] (device).  concept_bias: f32 [n_concept] (device, may
+ * be NULL).  Outputs (device): logits f32 [T, E] (may be NULL), topk_idx int32
+ * [T, k], topk_w f32 [T, k], block_counts int32 [prichs_router_num_blocks*E]
+ * (per-block expert histogram consumed by prichs_permute).
+ * Limits: 1 <= E <= PRICHS_MAX_EXPERTS, 1 <= k <= min(E, PRICHS_MAX_TOPK). */
+int prichs_router_topk(const void *x, int x_dtype, const float *w_router,
+                       const float *router_bias, const float *concept_bias,
+                       size_t n_concept, size_t T, size_t d, size_t E, size_t k,
+                       float *logits, int32_t *topk_idx, float *topk_w,
+                       int32_t *block_counts, void *stream);
+
+/* Token permutation (stable counting sort by expert id).  Restates the
+ * binning of crates/prichs-model/src/moe.rs:121, 137-141, 149-164: rows are
+ * ordered by (expert ascending, token ascending).  Outputs (device):
+ *   offsets   int32 [E + 2]: rows of routed expert e are
+ *             [offsets[e], offsets[e+1]); offsets[E] = T*k; the shared
+ *             expert's rows are [T*k, offsets[E+1] = T*k + T).
+ *   row_token int32 [T*k + T]: token of each row (shared rows: t -> t).
+ *   row_weight f32 [T*k]: gate weight of each routed row.
+ *   token_row int32 [T*k]: row of (token t, slot s) at t*k + s.
+ * block_counts comes from prichs_router_topk with the same T, E. */
+int prichs_permute(const int32_t *topk_idx, const float *topk_w,
+                   const int32_t *block_counts, size_t T, size_t E, size_t k,
+                   int32_t *offsets, int32_t *row_token, float *row_weight,
+                   int32_t *token_row, void *stream);
+
+/* Packed expert-weight layouts used by the grouped GEMMs (host functions,
+ * no GPU needed).  `il` selects the gate/up interleave of the kernel that
+ * will consume the buffer; pass prichs_gate_up_interleave(dtype).
+ *
+ * gate/up, one expert: packed [Np, K = d] with K contiguous,
+ *   Np = 2 * roundup(f, 2 * il); packed row p = 2*il*b + q holds column
+ *   il*b + q of gate (q < il) or column il*b + q - il of up (q >= il),
+ *   zero when that column is >= f.
+ * down, one expert: packed [roundup(d, 256), K = f] = W_down^T, zero rows
+ *   past d.
+ * Element type: dtype (bf16 by round-to-nearest-even from f32). */
+size_t prichs_gate_up_interleave(int dtype);
+size_t prichs_packed_gate_up_elems(size_t d, size_t f, int dtype);
+size_t prichs_packed_down_elems(size_t d, size_t f, int dtype);
+int prichs_pack_gate_up(const float *gate, const float *up, size_t d, size_t f,
+                        int dtype, void *packed_out);
+int prichs_pack_down(const float *down, size_t d, size_t f, int dtype,
+                     void *packed_out);
+
+/* Grouped gate/up GEMM with the SwiGLU epilogue fused.  Replaces the gate and
+ * up SGEMMs plus launch_swiglu_forward of gpu_moe_forward_shared /
+ * gpu_moe_forward_expert (crates/prichs-cuda/src/engine.rs:1957-1999,
+ * 2112-2153); math of crates/prichs-model/src/moe.rs:166-169 and 103-105.
+ * For every row r of group g (rows [offsets[g], offsets[g+1])):
+ *   act[r, :] = silu(x[row_token[r]] @ Wg_g) * (x[row_token[r]] @ Wu_g).
+ * Groups 0..G-1 use packed weights w_packed + g * prichs_packed_gate_up_elems.
+ * With the offsets/row_token of prichs_permute, G = E + 1 covers the routed
+ * experts (g < E) and the shared expert (g = E, its weights packed last).
+ * x [T, d], act [offsets[G], f] and the weights share `dtype`; fp32
+ * accumulation.  Requires d % 64 == 0 and f % 64 == 0 for bf16, d % 16 == 0
+ * and f % 16 == 0 for f32.  max_rows bounds offsets[G] (sizes the launch). */
+int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_token,
+                                  const int32_t *offsets, size_t G,
+                                  size_t max_rows, const void *w_packed,
+                                  size_t d, size_t f, int dtype, void *act,
+                                  void *stream);
+
+/* Grouped down GEMM: y[r, :] = act[r, :] @ Wd_g for the rows of each group.
+ * Replaces the down SGEMMs (engine.rs:2002-2017, 2156-2171; moe.rs:170,106).
+ * act [offsets[G], f], y [offsets[G], d] of `dtype`; fp32 accumulation. */
+int prichs_grouped_down(const void *act, const int32_t *offsets, size_t G,
+                        size_t max_rows, const void *w_packed, size_t d,
+                        size_t f, int dtype, void *y, void *stream);
+
+/* Deterministic combine.  Replaces launch_moe_scatter_add + the shared
+ * initialisation (kernels.cu:906-924; engine.rs:2002-2017, 2226-2239) and
+ * restates moe.rs:146, 177-184: per token,
+ *   out = shared_y[t]; then for its experts in ASCENDING expert id:
+ *   out = out + w * y[row]   (product rounded, then sum).
+ * y [T*k + T*has_shared, d] of y_dtype laid out as by prichs_permute (shared
+ * rows last), out [T, d] of out_dtype. */
+int prichs_moe_combine(const void *y, int y_dtype, const int32_t *topk_idx,
+                       const float *topk_w, const int32_t *token_row,
+                       size_t T, size_t d, size_t k, int has_shared, void *out,
+                       int out_dtype, void *stream);
+
+/* RMSNorm (memory-bound).  crates/prichs-core/src/ops.rs:109-135:
+ * out = (x * inv) * w, inv = 1/sqrt(sum(x^2)/d + eps); rstd[t] = inv
+ * (rstd may be NULL).  x/out dtypes independent; w is f32 [d]. */
+int prichs_rmsnorm_forward(const void *x, int x_dtype, const float *w,
+                           void *out, int out_dtype, float *rstd, size_t T,
+                           size_t d, float eps, void *stream);
+
+/* RoPE (memory-bound, in place).  crates/prichs-core/src/backward.rs:160-188
+ * for `batch` independent sequences: qk [batch, seq_len, n_heads, head_dim],
+ * position of row s = s + pos_offset, cache f32 [*, head_dim/2] from the
+ * host (backward.rs:136-157); sign = +1 forward, -1 inverse rotation.
+ * cache_rows bounds the positions (seq_len + pos_offset <= cache_rows). */
+int prichs_rope_forward(void *qk, int dtype, const float *cos_cache,
+                        const float *sin_cache, size_t cache_rows, size_t batch,
+                        size_t seq_len, size_t n_heads, size_t head_dim,
+                        size_t pos_offset, int sign, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* 3. MoE engine (owns packed weights + workspace; replaces the MoE part of */
+/*    GpuModelEngine: engine.rs:363-649, 668-689, 1917-2239)               */
+/* ---------------------------------------------------------------------- */
+typedef struct prichs_moe_engine prichs_moe_engine;
+
+/* Creates an engine for one MoE layer on the current HIP device.
+ * n_shared is 0 or 1 (the reference has 1, moe.rs:61).  dtype is the
+ * arithmetic type of the expert GEMMs and activations (F32 or BF16).
+ * max_tokens is the largest T a forward may use; all workspace is
+ * allocated here (forward allocates nothing). */
+int prichs_moe_engine_create(size_t d, size_t f, size_t E, size_t k,
+                             size_t n_shared, int dtype, size_t max_tokens,
+                             prichs_moe_engine **out);
+int prichs_moe_engine_destroy(prichs_moe_engine *eng);
+
+/* Uploads weights given in the reference layouts (host f32): router [d, E],
+ * router_bias [E] (may be NULL = zeros, moe.rs:75), and arrays of
+ * n_shared + E pointers (shared expert first, then routed 0..E-1) to
+ * gate [d, f], up [d, f], down [f, d].  Synchronous.  Replaces
+ * upload_weights (engine.rs:668-689) for one layer; packs to the kernels'
+ * layouts. */
+int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_router,
+                             const float *router_bias,
+                             const float *const *gate, const float *const *up,
+                             const float *const *down);
+
+/* Replaces the host-side aux-free bias (moe.rs:60, 228-245): host f32 [E]. */
+int prichs_moe_engine_set_router_bias(prichs_moe_engine *eng,
+                                      const float *router_bias);
+
+/* Full MoELayer forward (moe.rs:93-225) on device: x [T, d] of the engine's
+ * dtype (device), optional concept bias f32 [n_concept] (device, may be
+ * NULL), out [T, d] of out_dtype (device).  T <= max_tokens. */
+int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, size_t T,
+                              const float *concept_bias, size_t n_concept,
+                              void *out, int out_dtype, void *stream);
+
+/* Device views of the last forward's intermediates (the reference's MoEStash,
+ * moe.rs:32-53): router logits f32 [T, E], selected experts int32 [T, k],
+ * gate weights f32 [T, k], offsets int32 [E + 2], row_token int32 [T*k + T],
+ * row_weight f32 [T*k], token_row int32 [T*k], act [T*k + T, f] and
+ * y [T*k + T, d] of the engine dtype (routed rows in permuted order, shared
+ * rows last).  Valid until the next forward. */
+typedef struct prichs_moe_stash {
+  size_t T;
+  const float *router_logits;
+  const int32_t *selected_experts;
+  const float *gating_weights;
+  const int32_t *offsets;
+  const int32_t *row_token;
+  const float *row_weight;
+  const int32_t *token_row;
+  const void *act;
+  const void *y;
+} prichs_moe_stash;
+int prichs_moe_engine_stash(const prichs_moe_engine *eng,
+                            prichs_moe_stash *out);
+
+/* Stage timing.  set_timing(eng, n) creates events for n forwards (0 turns
+ * timing off); each following forward, up to n of them, records HIP events
+ * on its stream between its stages, with no host synchronisation.
+ * stage_ms waits for those forwards and writes the AVERAGE milliseconds of:
+ * [0] router, [1] permute, [2] gate/up GEMM, [3] down GEMM, [4] combine,
+ * [5] whole forward; *n_forwards (may be NULL) gets the number averaged.
+ * It then re-arms recording for another n forwards. */
+#define PRICHS_NUM_STAGES 6
+int prichs_moe_engine_set_timing(prichs_moe_engine *eng, int max_forwards);
+int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
+                               int *n_forwards);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRICHS_HIP_H */

@@ -1,0 +1,201 @@
+"""ctypes front end of the CPU oracle (oracle/prichs_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as the
+checker, and by bench.py's cpu_baseline leg.  The product (prichs_amd) never
+imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile (gcc, OpenMP)."""
+    if force or not os.path.exists(_LIB_PATH) or (
+        os.path.getmtime(_LIB_PATH) < os.path.getmtime(os.path.join(_HERE, "prichs_oracle.c"))
+    ):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "liboracle.so"],
+                       check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        sz = C.c_size_t
+        L.orc_matmul_2d.argtypes = [_f32p, _f32p, _f32p, sz, sz, sz]
+        L.orc_matmul_2d.restype = None
+        L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, sz, sz, C.c_float]
+        L.orc_rms_norm.restype = None
+        L.orc_silu.argtypes = [C.c_float]
+        L.orc_silu.restype = C.c_float
+        L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, sz]
+        L.orc_swiglu.restype = None
+        L.orc_add_tensors.argtypes = [_f32p, _f32p, _f32p, sz]
+        L.orc_add_tensors.restype = None
+        L.orc_top_k_gating_unbiased.argtypes = [_f32p, _f32p, sz, sz, _i32p, _f32p]
+        L.orc_top_k_gating_unbiased.restype = C.c_int
+        L.orc_route.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, sz, sz, sz, sz, sz,
+                                _f32p, _i32p, _f32p]
+        L.orc_route.restype = C.c_int
+        L.orc_bin_tokens.argtypes = [_i32p, _f32p, sz, sz, sz, _i32p, _i32p, _f32p, _i32p]
+        L.orc_bin_tokens.restype = None
+        L.orc_moe_forward.argtypes = [_f32p, sz, sz, sz, sz, sz, sz, _f32p, _f32p, C.c_void_p, sz,
+                                      C.c_void_p, C.c_void_p, C.c_void_p, _f32p,
+                                      _f32p, _i32p, _f32p, _i32p, _i32p, _f32p, _i32p]
+        L.orc_moe_forward.restype = C.c_int
+        L.orc_precompute_rope_cache.argtypes = [sz, sz, C.c_float, _f32p, _f32p]
+        L.orc_precompute_rope_cache.restype = None
+        L.orc_rope_forward_in_place.argtypes = [_f32p, _f32p, _f32p, sz, sz, sz, sz]
+        L.orc_rope_forward_in_place.restype = None
+        L.orc_num_threads.restype = C.c_int
+        L.orc_set_num_threads.argtypes = [C.c_int]
+        L.orc_set_num_threads.restype = None
+        _lib = L
+    return _lib
+
+
+def _c(a, dt=np.float32):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
+
+
+def set_num_threads(n: int) -> None:
+    lib().orc_set_num_threads(int(n))
+
+
+def matmul_2d(a, b):
+    a, b = _c(a), _c(b)
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    out = np.empty((m, n), np.float32)
+    lib().orc_matmul_2d(a, b, out, m, k, n)
+    return out
+
+
+def rms_norm(x, w, eps=1e-5):
+    x, w = _c(x), _c(w)
+    out = np.empty_like(x)
+    d = x.shape[-1]
+    lib().orc_rms_norm(x, w, out, x.size // d, d, eps)
+    return out
+
+
+def silu(v: float) -> float:
+    return lib().orc_silu(float(v))
+
+
+def swiglu(g, u):
+    g, u = _c(g), _c(u)
+    out = np.empty_like(g)
+    lib().orc_swiglu(g, u, out, g.size)
+    return out
+
+
+def add_tensors(a, b):
+    a, b = _c(a), _c(b)
+    out = np.empty_like(a)
+    lib().orc_add_tensors(a, b, out, a.size)
+    return out
+
+
+def top_k_gating_unbiased(raw, adj, k):
+    raw, adj = _c(raw), _c(adj)
+    E = raw.size
+    idx = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    rc = lib().orc_top_k_gating_unbiased(raw, adj, E, k, idx, w)
+    if rc != 0:
+        raise ValueError("bad top-k arguments")
+    return idx, w
+
+
+def route(x, w_router, router_bias, k, concept_bias=None):
+    x, w_router, router_bias = _c(x), _c(w_router), _c(router_bias)
+    T, d = x.shape
+    E = w_router.shape[1]
+    logits = np.empty((T, E), np.float32)
+    sel = np.empty((T, k), np.int32)
+    gw = np.empty((T, k), np.float32)
+    cb = None if concept_bias is None else _c(concept_bias)
+    rc = lib().orc_route(x, w_router, router_bias, None if cb is None else cb.ctypes.data,
+                         0 if cb is None else cb.size, T, d, E, k, logits, sel, gw)
+    if rc != 0:
+        raise ValueError("bad routing arguments")
+    return logits, sel, gw
+
+
+def bin_tokens(sel, gw, E):
+    sel, gw = _c(sel, np.int32), _c(gw)
+    T, k = sel.shape
+    offsets = np.empty(E + 1, np.int32)
+    row_token = np.empty(T * k, np.int32)
+    row_weight = np.empty(T * k, np.float32)
+    token_row = np.empty(T * k, np.int32)
+    lib().orc_bin_tokens(sel, gw, T, E, k, offsets, row_token, row_weight, token_row)
+    return offsets, row_token, row_weight, token_row
+
+
+def moe_forward(inp, concept_bias=None):
+    """MoELayer::forward_train (moe.rs:93-212) on a synth.MoEInputs; returns a dict."""
+    T, d, f, E, k, S = inp.T, inp.d, inp.f, inp.E, inp.k, inp.n_shared
+    x = _c(inp.x)
+    gates = [_c(a) for a in inp.gate]
+    ups = [_c(a) for a in inp.up]
+    downs = [_c(a) for a in inp.down]
+    arr_t = C.c_void_p * (S + E)
+    pg = arr_t(*[a.ctypes.data for a in gates])
+    pu = arr_t(*[a.ctypes.data for a in ups])
+    pd = arr_t(*[a.ctypes.data for a in downs])
+    out = np.empty((T, d), np.float32)
+    logits = np.empty((T, E), np.float32)
+    sel = np.empty((T, k), np.int32)
+    gw = np.empty((T, k), np.float32)
+    offsets = np.empty(E + 1, np.int32)
+    row_token = np.empty(max(T * k, 1), np.int32)
+    row_weight = np.empty(max(T * k, 1), np.float32)
+    token_row = np.empty(max(T * k, 1), np.int32)
+    cb = None if concept_bias is None else _c(concept_bias)
+    rc = lib().orc_moe_forward(x, T, d, f, E, k, S, _c(inp.w_router), _c(inp.router_bias),
+                               None if cb is None else cb.ctypes.data, 0 if cb is None else cb.size,
+                               C.cast(pg, C.c_void_p), C.cast(pu, C.c_void_p), C.cast(pd, C.c_void_p),
+                               out, logits, sel, gw, offsets, row_token, row_weight, token_row)
+    if rc != 0:
+        raise RuntimeError("oracle moe_forward failed")
+    return dict(out=out, logits=logits, sel=sel, gw=gw, offsets=offsets,
+                row_token=row_token[: T * k], row_weight=row_weight[: T * k],
+                token_row=token_row[: T * k])
+
+
+def precompute_rope_cache(max_seq_len, head_dim, theta):
+    half = head_dim // 2
+    cos = np.empty(max_seq_len * half, np.float32)
+    sin = np.empty(max_seq_len * half, np.float32)
+    lib().orc_precompute_rope_cache(max_seq_len, head_dim, theta, cos, sin)
+    return cos, sin
+
+
+def rope_forward(t, cos, sin, pos_offset=0):
+    """Returns a rotated copy of t [seq, heads, head_dim] (backward.rs:160-188)."""
+    t = np.array(t, dtype=np.float32, copy=True, order="C")
+    S, H, hd = t.shape
+    lib().orc_rope_forward_in_place(t, _c(cos), _c(sin), S, H, hd, pos_offset)
+    return t

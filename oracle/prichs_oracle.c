@@ -1,0 +1,410 @@
+/*
+ * prichs_oracle.c -- CPU restatement of PRICHS's MoE feed-forward CPU path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * library in prichs_amd/.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it.  The product never calls it.
+ *
+ * Every function restates one function of the reference (Rust, prichs-core /
+ * prichs-model) and cites it by file:line under the reference tree.  The
+ * arithmetic order is kept exactly: each product and each sum is rounded to
+ * f32 separately (the file is compiled with -ffp-contract=off; Rust never
+ * contracts a*b+c into an FMA), loops run in the reference's order, and the
+ * transcendental calls (expf, sqrtf, powf, cosf, sinf) go to the same glibc
+ * libm that Rust's f32::{exp,sqrt,powf,cos,sin} resolve to on Linux.
+ *
+ * Row loops that the reference runs under Rayon (par_chunks_exact_mut over
+ * output rows) run here under OpenMP over the same rows: Rayon only splits
+ * rows between threads, so the per-element arithmetic order is unchanged.
+ *
+ * Pinning (what checks each function besides this restatement):
+ *   orc_matmul_2d            GEMM known-answer test (engine.rs:2881-2910),
+ *                            float64 recomputation, exact small-integer case.
+ *   orc_rms_norm             KAT row [2,2,2,2] -> 1.0 (engine.rs:3041-3053),
+ *                            float64 closed form.
+ *   orc_swiglu / orc_silu    closed form in float64, silu(0)=0, odd/limit cases.
+ *   orc_top_k_gating_unbiased  invariants (distinct, descending, ties -> lower
+ *                            index, +0 == -0), brute force over all k-subsets,
+ *                            bias changes selection only, NaN cases against an
+ *                            independent Python insertion-sort model.
+ *   orc_moe_forward          float64 re-assembly of the layer from numpy,
+ *                            permutation = stable counting sort, committed
+ *                            golden fixture for config 1.
+ *   orc_precompute_rope_cache / orc_rope_forward_in_place
+ *                            cos=1/sin=0 identity (engine.rs:2970-2972), norm
+ *                            preservation, float64 closed form.
+ *   orc_attention_forward / orc_block_forward
+ *                            float64 softmax attention recomputation, causal
+ *                            mask invariants.
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------ */
+/* GEMM: crates/prichs-core/src/ops.rs:8-61 (CPU branch ops.rs:33-58).        */
+/* out[i][j] = (((0 + a[i][0]*b[0][j]) + a[i][1]*b[1][j]) + ...)              */
+/* The m == 1 fast path (ops.rs:34-43) has the same per-element order.        */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_matmul_2d(const float *a, const float *b, float *out,
+                           size_t m, size_t k, size_t n) {
+  long long mi;
+#pragma omp parallel for schedule(static)
+  for (mi = 0; mi < (long long)m; ++mi) {
+    const float *a_row = a + (size_t)mi * k;
+    float *out_row = out + (size_t)mi * n;
+    for (size_t j = 0; j < n; ++j) out_row[j] = 0.0f;
+    for (size_t kk = 0; kk < k; ++kk) {
+      const float a_val = a_row[kk];
+      const float *b_row = b + kk * n;
+      for (size_t j = 0; j < n; ++j) {
+        float prod = a_val * b_row[j];
+        out_row[j] = out_row[j] + prod;
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm: crates/prichs-core/src/ops.rs:109-135.                            */
+/* sum_sq sequential over the row (Iterator::sum), rms = sqrt(ss/d + eps),    */
+/* inv = 1/rms, out = (x*inv)*w.                                              */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_rms_norm(const float *x, const float *w, float *out,
+                          size_t rows, size_t d, float eps) {
+  long long r;
+#pragma omp parallel for schedule(static)
+  for (r = 0; r < (long long)rows; ++r) {
+    const float *row = x + (size_t)r * d;
+    float *orow = out + (size_t)r * d;
+    float sum_sq = 0.0f;
+    for (size_t c = 0; c < d; ++c) {
+      float sq = row[c] * row[c];
+      sum_sq = sum_sq + sq;
+    }
+    float rms = sqrtf(sum_sq / (float)d + eps);
+    float inv_rms = 1.0f / rms;
+    for (size_t c = 0; c < d; ++c) {
+      float t = row[c] * inv_rms;
+      orow[c] = t * w[c];
+    }
+  }
+}
+
+/* silu: crates/prichs-core/src/ops.rs:137-140.  x / (1 + exp(-x)). */
+ORC_API float orc_silu(float x) {
+  float den = 1.0f + expf(-x);
+  return x / den;
+}
+
+/* SwiGLU: crates/prichs-core/src/ops.rs:142-159.  out = silu(g) * u. */
+ORC_API void orc_swiglu(const float *g, const float *u, float *out, size_t n) {
+  long long i;
+#pragma omp parallel for schedule(static)
+  for (i = 0; i < (long long)n; ++i) out[i] = orc_silu(g[i]) * u[i];
+}
+
+/* add_tensors: crates/prichs-core/src/ops.rs:250-267. */
+ORC_API void orc_add_tensors(const float *a, const float *b, float *out,
+                             size_t n) {
+  long long i;
+#pragma omp parallel for schedule(static)
+  for (i = 0; i < (long long)n; ++i) out[i] = a[i] + b[i];
+}
+
+/* ------------------------------------------------------------------------ */
+/* top_k_gating_unbiased: crates/prichs-core/src/ops.rs:219-248.              */
+/*                                                                            */
+/* Selection: slice::sort_by on (index, routing_logit) with comparator        */
+/* b.partial_cmp(a).unwrap_or(Equal) -- a stable descending sort.  For the    */
+/* slice lengths used here (E <= 20) Rust's stable sort is an insertion sort  */
+/* that inserts v[i] leftwards while is_less(v[i], v[j-1]) holds, where       */
+/* is_less(x, y) == (compare(x, y) == Less) == (x.val > y.val).  A NaN never  */
+/* compares Less, so the insertion sort below reproduces the reference on     */
+/* NaN inputs too; on non-NaN inputs it is the stable descending order (ties  */
+/* keep ascending index, +0 and -0 compare equal).                            */
+/*                                                                            */
+/* Weights: softmax over the RAW logits of the selected experts in slot      */
+/* order: m = fold(-inf, f32::max), e_i = exp(raw_i - m), s = sequential sum, */
+/* inv = 1/(s + 1e-9), w_i = e_i * inv.                                       */
+/* ------------------------------------------------------------------------ */
+#define ORC_MAX_E 256
+ORC_API int orc_top_k_gating_unbiased(const float *raw, const float *adj,
+                                      size_t E, size_t k, int32_t *idx_out,
+                                      float *w_out) {
+  if (E == 0 || E > ORC_MAX_E || k > E) return -1;
+  int32_t ord[ORC_MAX_E];
+  float val[ORC_MAX_E];
+  for (size_t i = 0; i < E; ++i) {
+    ord[i] = (int32_t)i;
+    val[i] = adj[i];
+  }
+  for (size_t i = 1; i < E; ++i) {
+    int32_t oi = ord[i];
+    float vi = val[i];
+    size_t j = i;
+    while (j > 0 && (vi > val[j - 1])) { /* is_less(v[i], v[j-1]) */
+      ord[j] = ord[j - 1];
+      val[j] = val[j - 1];
+      --j;
+    }
+    ord[j] = oi;
+    val[j] = vi;
+  }
+  float max_val = -INFINITY;
+  for (size_t s = 0; s < k; ++s) max_val = fmaxf(max_val, raw[ord[s]]);
+  float e_buf[ORC_MAX_E];
+  float sum_exp = 0.0f;
+  for (size_t s = 0; s < k; ++s) {
+    float diff = raw[ord[s]] - max_val;
+    float e = expf(diff);
+    e_buf[s] = e;
+    sum_exp = sum_exp + e;
+  }
+  float inv_sum = 1.0f / (sum_exp + 1e-9f);
+  for (size_t s = 0; s < k; ++s) {
+    idx_out[s] = ord[s];
+    w_out[s] = e_buf[s] * inv_sum;
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Router + gating for all tokens: crates/prichs-model/src/moe.rs:113-142.    */
+/* raw = x @ W_router (ops.rs GEMM order); adj = (raw + bias[e]) (+ c[e] for  */
+/* e < n_concept); per token top_k_gating_unbiased(raw, adj, k).              */
+/* ------------------------------------------------------------------------ */
+ORC_API int orc_route(const float *x, const float *w_router,
+                      const float *router_bias, const float *concept_bias,
+                      size_t n_concept, size_t T, size_t d, size_t E, size_t k,
+                      float *logits_out, int32_t *sel_out, float *gw_out) {
+  if (E == 0 || E > ORC_MAX_E || k > E) return -1;
+  orc_matmul_2d(x, w_router, logits_out, T, d, E);
+  long long t;
+  int bad = 0;
+#pragma omp parallel for schedule(static) reduction(| : bad)
+  for (t = 0; t < (long long)T; ++t) {
+    const float *raw = logits_out + (size_t)t * E;
+    float adj[ORC_MAX_E];
+    for (size_t e = 0; e < E; ++e) {
+      float logit = raw[e] + router_bias[e];
+      if (concept_bias != NULL && e < n_concept) logit = logit + concept_bias[e];
+      adj[e] = logit;
+    }
+    bad |= orc_top_k_gating_unbiased(raw, adj, E, k, sel_out + (size_t)t * k,
+                                     gw_out + (size_t)t * k);
+  }
+  return bad ? -1 : 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Token binning: crates/prichs-model/src/moe.rs:121, 137-141, 149-153.       */
+/* expert_assignments[e] gets (t, w) for t ascending; experts are visited in  */
+/* ascending order.  Flattened: offsets[E+1], row_token[T*k], row_weight,     */
+/* and the inverse map token_row[t*k + slot].                                 */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_bin_tokens(const int32_t *sel, const float *gw, size_t T,
+                            size_t E, size_t k, int32_t *offsets,
+                            int32_t *row_token, float *row_weight,
+                            int32_t *token_row) {
+  size_t counts[ORC_MAX_E];
+  for (size_t e = 0; e < E; ++e) counts[e] = 0;
+  for (size_t i = 0; i < T * k; ++i) counts[sel[i]]++;
+  offsets[0] = 0;
+  for (size_t e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + (int32_t)counts[e];
+  size_t cursor[ORC_MAX_E];
+  for (size_t e = 0; e < E; ++e) cursor[e] = (size_t)offsets[e];
+  for (size_t t = 0; t < T; ++t) {
+    for (size_t s = 0; s < k; ++s) {
+      int32_t e = sel[t * k + s];
+      size_t r = cursor[e]++;
+      row_token[r] = (int32_t)t;
+      row_weight[r] = gw[t * k + s];
+      if (token_row) token_row[t * k + s] = (int32_t)r;
+    }
+  }
+}
+
+/* Expert::forward shape: G = X Wg, U = X Wu, A = swiglu(G, U), Y = A Wd.
+ * crates/prichs-model/src/moe.rs:22-28 and 166-170. */
+static int orc_expert_ffn(const float *xin, size_t m, size_t d, size_t f,
+                          const float *wg, const float *wu, const float *wd,
+                          float *y) {
+  float *g = (float *)malloc(sizeof(float) * m * f);
+  float *u = (float *)malloc(sizeof(float) * m * f);
+  if (!g || !u) {
+    free(g);
+    free(u);
+    return -1;
+  }
+  orc_matmul_2d(xin, wg, g, m, d, f);
+  orc_matmul_2d(xin, wu, u, m, d, f);
+  orc_swiglu(g, u, g, m * f);
+  orc_matmul_2d(g, wd, y, m, f, d);
+  free(g);
+  free(u);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MoELayer::forward_train: crates/prichs-model/src/moe.rs:93-212.            */
+/*                                                                            */
+/* 1. shared expert on all rows (moe.rs:103-106);                             */
+/* 2. router logits + per-token gating (moe.rs:113-142);                      */
+/* 3. total_out = shared_out (moe.rs:146);                                    */
+/* 4. for e ascending with a non-empty bin: gather rows, expert FFN, then     */
+/*    out[t] += w * y row by row (moe.rs:149-184).                            */
+/*                                                                            */
+/* Weights: gate/up [d,f], down [f,d] row-major (moe.rs:16-18); the shared    */
+/* expert comes first in the arrays (n_shared = 0 or 1), then routed 0..E-1.  */
+/* Optional outputs (NULL to skip): logits [T,E], sel [T,k], gw [T,k],        */
+/* offsets [E+1], row_token [T*k], row_weight [T*k], token_row [T*k].         */
+/* ------------------------------------------------------------------------ */
+ORC_API int orc_moe_forward(const float *x, size_t T, size_t d, size_t f,
+                            size_t E, size_t k, size_t n_shared,
+                            const float *w_router, const float *router_bias,
+                            const float *concept_bias, size_t n_concept,
+                            const float *const *w_gate,
+                            const float *const *w_up,
+                            const float *const *w_down, float *out,
+                            float *logits, int32_t *sel, float *gw,
+                            int32_t *offsets, int32_t *row_token,
+                            float *row_weight, int32_t *token_row) {
+  if (E == 0 || E > ORC_MAX_E || k > E || n_shared > 1) return -1;
+  int rc = 0;
+  float *lg = logits ? logits : (float *)malloc(sizeof(float) * (T * E + 1));
+  int32_t *sl = sel ? sel : (int32_t *)malloc(sizeof(int32_t) * (T * k + 1));
+  float *gwt = gw ? gw : (float *)malloc(sizeof(float) * (T * k + 1));
+  int32_t *off = offsets ? offsets : (int32_t *)malloc(sizeof(int32_t) * (E + 1));
+  int32_t *rt = row_token ? row_token : (int32_t *)malloc(sizeof(int32_t) * (T * k + 1));
+  float *rw = row_weight ? row_weight : (float *)malloc(sizeof(float) * (T * k + 1));
+  if (!lg || !sl || !gwt || !off || !rt || !rw) rc = -1;
+
+  /* 1. shared expert, written straight into out (total_out = shared_out). */
+  if (rc == 0) {
+    if (n_shared == 1) {
+      rc = orc_expert_ffn(x, T, d, f, w_gate[0], w_up[0], w_down[0], out);
+    } else {
+      memset(out, 0, sizeof(float) * T * d);
+    }
+  }
+  /* 2. routing. */
+  if (rc == 0)
+    rc = orc_route(x, w_router, router_bias, concept_bias, n_concept, T, d, E, k,
+                   lg, sl, gwt);
+  if (rc == 0) orc_bin_tokens(sl, gwt, T, E, k, off, rt, rw, token_row);
+
+  /* 3./4. routed experts in ascending order, scatter-add row by row. */
+  for (size_t e = 0; rc == 0 && e < E; ++e) {
+    size_t n_tok = (size_t)(off[e + 1] - off[e]);
+    if (n_tok == 0) continue;
+    float *xb = (float *)malloc(sizeof(float) * n_tok * d);
+    float *yb = (float *)malloc(sizeof(float) * n_tok * d);
+    if (!xb || !yb) {
+      free(xb);
+      free(yb);
+      rc = -1;
+      break;
+    }
+    for (size_t i = 0; i < n_tok; ++i)
+      memcpy(xb + i * d, x + (size_t)rt[off[e] + i] * d, sizeof(float) * d);
+    rc = orc_expert_ffn(xb, n_tok, d, f, w_gate[n_shared + e],
+                        w_up[n_shared + e], w_down[n_shared + e], yb);
+    if (rc == 0) {
+      /* Rows of one bin belong to distinct tokens, so rows can be updated in
+       * parallel without changing any element's order of additions. */
+      long long i;
+#pragma omp parallel for schedule(static)
+      for (i = 0; i < (long long)n_tok; ++i) {
+        size_t r = (size_t)off[e] + (size_t)i;
+        float wgt = rw[r];
+        float *orow = out + (size_t)rt[r] * d;
+        const float *yrow = yb + (size_t)i * d;
+        for (size_t c = 0; c < d; ++c) {
+          float prod = wgt * yrow[c];
+          orow[c] = orow[c] + prod;
+        }
+      }
+    }
+    free(xb);
+    free(yb);
+  }
+
+  if (!logits) free(lg);
+  if (!sel) free(sl);
+  if (!gw) free(gwt);
+  if (!offsets) free(off);
+  if (!row_token) free(rt);
+  if (!row_weight) free(rw);
+  return rc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* RoPE cache: crates/prichs-core/src/backward.rs:136-157.                    */
+/* freq_i = 1 / theta^((2i)/hd) (f32 powf), angle = (t as f32) * freq_i.      */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_precompute_rope_cache(size_t max_seq_len, size_t head_dim,
+                                       float theta, float *cos_cache,
+                                       float *sin_cache) {
+  size_t half = head_dim / 2;
+  for (size_t i = 0; i < half; ++i) {
+    float exponent = (float)(2 * i) / (float)head_dim;
+    float freq = 1.0f / powf(theta, exponent);
+    for (size_t t = 0; t < max_seq_len; ++t) {
+      float angle = (float)t * freq;
+      size_t off = t * half + i;
+      cos_cache[off] = cosf(angle);
+      sin_cache[off] = sinf(angle);
+    }
+  }
+}
+
+/* RoPE rotation: crates/prichs-core/src/backward.rs:160-188.
+ * Interleaved pairs (2i, 2i+1) at position t + pos_offset. */
+ORC_API void orc_rope_forward_in_place(float *tensor, const float *cos_cache,
+                                       const float *sin_cache, size_t seq_len,
+                                       size_t n_heads, size_t head_dim,
+                                       size_t pos_offset) {
+  size_t half = head_dim / 2;
+  for (size_t t = 0; t < seq_len; ++t) {
+    size_t trig = (t + pos_offset) * half;
+    for (size_t h = 0; h < n_heads; ++h) {
+      size_t base = (t * n_heads + h) * head_dim;
+      for (size_t i = 0; i < half; ++i) {
+        float c = cos_cache[trig + i];
+        float s = sin_cache[trig + i];
+        float q0 = tensor[base + 2 * i];
+        float q1 = tensor[base + 2 * i + 1];
+        float a0 = q0 * c, b0 = q1 * s;
+        float a1 = q0 * s, b1 = q1 * c;
+        tensor[base + 2 * i] = a0 - b0;
+        tensor[base + 2 * i + 1] = a1 + b1;
+      }
+    }
+  }
+}
+
+/* Number of OpenMP threads the oracle will use (1 without OpenMP). */
+ORC_API int orc_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+ORC_API void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}

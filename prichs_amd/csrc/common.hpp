@@ -1,0 +1,94 @@
+// common.hpp -- shared helpers of libprichs_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "prichs_hip.h"
+
+namespace prichs {
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Returns `code` after recording the message (for `return fail(...)`).
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Checks a HIP call; on failure records "<what>: <hip error>" and returns
+// PRICHS_ERR_HIP from the enclosing int function.
+#define PRICHS_HIP_TRY(expr, what)                                            \
+  do {                                                                         \
+    hipError_t _e = (expr);                                                    \
+    if (_e != hipSuccess)                                                      \
+      return ::prichs::fail(PRICHS_ERR_HIP, "%s: %s", (what),                 \
+                            hipGetErrorString(_e));                            \
+  } while (0)
+
+// After a kernel launch: reports launch-configuration errors.
+#define PRICHS_LAUNCH_CHECK(what) PRICHS_HIP_TRY(hipGetLastError(), (what))
+
+#define PRICHS_REQUIRE(cond, ...)                                              \
+  do {                                                                         \
+    if (!(cond)) return ::prichs::fail(PRICHS_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// ------------------------------------------------------------------ bf16 --
+typedef uint16_t bf16_t;
+
+__host__ __device__ inline float bf16_to_f32(bf16_t b) {
+  union {
+    uint32_t u;
+    float f;
+  } v;
+  v.u = static_cast<uint32_t>(b) << 16;
+  return v.f;
+}
+
+// Round to nearest even; NaN stays a (quiet) NaN.
+__host__ __device__ inline bf16_t f32_to_bf16(float f) {
+  union {
+    uint32_t u;
+    float f;
+  } v;
+  v.f = f;
+  uint32_t u = v.u;
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))
+    return static_cast<bf16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int dtype = PRICHS_DTYPE_F32;
+  __device__ static float load(const float *p) { return *p; }
+  __device__ static void store(float *p, float v) { *p = v; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int dtype = PRICHS_DTYPE_BF16;
+  __device__ static float load(const bf16_t *p) { return bf16_to_f32(*p); }
+  __device__ static void store(bf16_t *p, float v) { *p = f32_to_bf16(v); }
+};
+
+inline size_t dtype_size(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? 2 : 4; }
+inline bool dtype_ok(int dtype) {
+  return dtype == PRICHS_DTYPE_F32 || dtype == PRICHS_DTYPE_BF16;
+}
+
+inline size_t roundup(size_t a, size_t b) { return (a + b - 1) / b * b; }
+inline size_t cdiv(size_t a, size_t b) { return (a + b - 1) / b; }
+
+// Device-side silu of the reference CPU path (crates/prichs-core/src/ops.rs:
+// 137-140): x / (1 + exp(-x)).
+__device__ inline float silu_ref(float x) { return x / (1.0f + expf(-x)); }
+
+}  // namespace prichs

@@ -1,0 +1,442 @@
+// elementwise.hip -- HBM-bound kernels: combine, RMSNorm, RoPE, and the
+// legacy f32 launchers with the reference's signatures.
+//
+// All loads/stores are 16-byte vectors along the contiguous dimension where
+// the shape allows it (one wave64 sweeps 1 KiB per instruction), with scalar
+// fallbacks for ragged shapes.
+#include "common.hpp"
+
+namespace prichs {
+namespace {
+
+// ------------------------------------------------------------- vectors --
+struct V8 {
+  float v[8];
+};
+
+__device__ inline V8 ld8(const float *p) {
+  V8 r;
+  const float4 a = *reinterpret_cast<const float4 *>(p);
+  const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+  r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+  r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+  return r;
+}
+__device__ inline V8 ld8(const bf16_t *p) {
+  V8 r;
+  const uint4 a = *reinterpret_cast<const uint4 *>(p);
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r.v[2 * i] = __uint_as_float(w[i] << 16);
+    r.v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+  return r;
+}
+__device__ inline void st8(float *p, const V8 &r) {
+  *reinterpret_cast<float4 *>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+  *reinterpret_cast<float4 *>(p + 4) = make_float4(r.v[4], r.v[5], r.v[6], r.v[7]);
+}
+__device__ inline void st8(bf16_t *p, const V8 &r) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (uint32_t)f32_to_bf16(r.v[2 * i]) | ((uint32_t)f32_to_bf16(r.v[2 * i + 1]) << 16);
+  *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <typename T> bool aligned16(const T *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+// ------------------------------------------------------------- combine --
+// out[t] = shared[t] (or 0); then for the token's experts in ascending id:
+// out = out + w * y[row]  (crates/prichs-model/src/moe.rs:146, 149, 177-184).
+template <typename YT, typename OT, bool VEC>
+__global__ __launch_bounds__(256) void combine_kernel(
+    const YT *__restrict__ y, const int32_t *__restrict__ topk_idx,
+    const float *__restrict__ topk_w, const int32_t *__restrict__ token_row, int T, int d,
+    int k, int has_shared, OT *__restrict__ out) {
+#pragma clang fp contract(off)
+  const int per_tok = VEC ? d / 8 : d;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (long long)T * per_tok) return;
+  const int t = (int)(gid / per_tok);
+  const int c = (int)(gid - (long long)t * per_tok) * (VEC ? 8 : 1);
+
+  int ex[PRICHS_MAX_TOPK], rows[PRICHS_MAX_TOPK];
+  float wt[PRICHS_MAX_TOPK];
+#pragma unroll
+  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+    if (s < k) {
+      ex[s] = topk_idx[(size_t)t * k + s];
+      rows[s] = token_row[(size_t)t * k + s];
+      wt[s] = topk_w[(size_t)t * k + s];
+    } else {
+      ex[s] = 0x7fffffff;
+      rows[s] = 0;
+      wt[s] = 0.f;
+    }
+  }
+  // Ascending expert id (k <= 8: a fixed compare-exchange network would do,
+  // but k is runtime; a bubble pass over registers stays in registers).
+#pragma unroll
+  for (int a = 0; a < PRICHS_MAX_TOPK - 1; ++a)
+#pragma unroll
+    for (int b = 0; b < PRICHS_MAX_TOPK - 1 - a; ++b)
+      if (ex[b] > ex[b + 1]) {
+        int te = ex[b]; ex[b] = ex[b + 1]; ex[b + 1] = te;
+        int tr = rows[b]; rows[b] = rows[b + 1]; rows[b + 1] = tr;
+        float tw = wt[b]; wt[b] = wt[b + 1]; wt[b + 1] = tw;
+      }
+
+  const size_t shared_row = (size_t)T * k + t;
+  if (VEC) {
+    V8 acc;
+    if (has_shared) {
+      acc = ld8(y + shared_row * d + c);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc.v[j] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+      if (s < k) {
+        const V8 yv = ld8(y + (size_t)rows[s] * d + c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = wt[s] * yv.v[j];
+          acc.v[j] = acc.v[j] + p;
+        }
+      }
+    }
+    st8(out + (size_t)t * d + c, acc);
+  } else {
+    float acc = has_shared ? Elem<YT>::load(y + shared_row * d + c) : 0.f;
+    for (int s = 0; s < k; ++s) {
+      const float p = wt[s] * Elem<YT>::load(y + (size_t)rows[s] * d + c);
+      acc = acc + p;
+    }
+    Elem<OT>::store(out + (size_t)t * d + c, acc);
+  }
+}
+
+// ------------------------------------------------------------- RMSNorm --
+// One wave64 per row (crates/prichs-core/src/ops.rs:109-135):
+// inv = 1/sqrt(sum(x^2)/d + eps), out = (x * inv) * w.
+template <typename XT, typename OT, bool VEC>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const XT *__restrict__ x,
+                                                      const float *__restrict__ w,
+                                                      OT *__restrict__ out,
+                                                      float *__restrict__ rstd, int T, int d,
+                                                      float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const XT *xr = x + (size_t)row * d;
+  OT *orow = out + (size_t)row * d;
+  float ss = 0.f;
+  if (VEC) {
+    for (int c = lane * 8; c < d; c += 512) {
+      const V8 v = ld8(xr + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = ss + v.v[j] * v.v[j];
+    }
+  } else {
+    for (int c = lane; c < d; c += 64) {
+      const float v = Elem<XT>::load(xr + c);
+      ss = ss + v * v;
+    }
+  }
+  ss = wave_sum(ss);
+  const float rms = sqrtf(ss / (float)d + eps);
+  const float inv = 1.0f / rms;
+  if (rstd != nullptr && lane == 0) rstd[row] = inv;
+  if (VEC) {
+    for (int c = lane * 8; c < d; c += 512) {
+      V8 v = ld8(xr + c);
+      const V8 wv = ld8(w + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = v.v[j] * inv;
+        v.v[j] = a * wv.v[j];
+      }
+      st8(orow + c, v);
+    }
+  } else {
+    for (int c = lane; c < d; c += 64) {
+      const float a = Elem<XT>::load(xr + c) * inv;
+      Elem<OT>::store(orow + c, a * w[c]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- RoPE --
+// crates/prichs-core/src/backward.rs:160-188: pairs (2i, 2i+1) at position
+// p -> (q0 c - q1 s, q0 s + q1 c), c/s = cache[p * hd/2 + i]; sign * s for
+// the inverse rotation.  One thread rotates 4 pairs (8 elements).
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void rope_kernel(T *__restrict__ qk, const float *__restrict__ cs,
+                                                   const float *__restrict__ sn, long long rows,
+                                                   int seq_len, int H, int hd, int pos_offset,
+                                                   float sign) {
+#pragma clang fp contract(off)
+  const int half = hd / 2;
+  const int per_row = VEC ? half / 4 : half;  // threads per (row, head)
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long total = rows * H * per_row;
+  if (gid >= total) return;
+  const long long rh = gid / per_row;
+  const int q = (int)(gid - rh * per_row);
+  const long long row = rh / H;
+  const int pos = (int)(row % seq_len) + pos_offset;
+  T *base = qk + rh * hd;
+  const float *cr = cs + (size_t)pos * half;
+  const float *sr = sn + (size_t)pos * half;
+  if (VEC) {
+    const int i0 = q * 4;
+    V8 v = ld8(base + 2 * i0);
+    const float4 c4 = *reinterpret_cast<const float4 *>(cr + i0);
+    const float4 s4 = *reinterpret_cast<const float4 *>(sr + i0);
+    const float c[4] = {c4.x, c4.y, c4.z, c4.w};
+    const float s[4] = {sign * s4.x, sign * s4.y, sign * s4.z, sign * s4.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q0 = v.v[2 * j], q1 = v.v[2 * j + 1];
+      const float a0 = q0 * c[j], b0 = q1 * s[j];
+      const float a1 = q0 * s[j], b1 = q1 * c[j];
+      v.v[2 * j] = a0 - b0;
+      v.v[2 * j + 1] = a1 + b1;
+    }
+    st8(base + 2 * i0, v);
+  } else {
+    const float c = cr[q], s = sign * sr[q];
+    const float q0 = Elem<T>::load(base + 2 * q), q1 = Elem<T>::load(base + 2 * q + 1);
+    const float a0 = q0 * c, b0 = q1 * s;
+    const float a1 = q0 * s, b1 = q1 * c;
+    Elem<T>::store(base + 2 * q, a0 - b0);
+    Elem<T>::store(base + 2 * q + 1, a1 + b1);
+  }
+}
+
+// ------------------------------------------------------- legacy kernels --
+__global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ g,
+                                                     const float *__restrict__ u,
+                                                     float *__restrict__ out, size_t n) {
+#pragma clang fp contract(off)
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = silu_ref(g[i]) * u[i];
+}
+
+__global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ in,
+                                                     const int *__restrict__ idx,
+                                                     float *__restrict__ out, size_t n_tok,
+                                                     size_t d) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_tok * d) return;
+  const size_t r = i / d, c = i - r * d;
+  out[i] = in[(size_t)idx[r] * d + c];
+}
+
+__global__ __launch_bounds__(256) void scatter_add_kernel(const float *__restrict__ y,
+                                                          const int *__restrict__ idx,
+                                                          const float *__restrict__ w,
+                                                          float *__restrict__ acc, size_t n_tok,
+                                                          size_t d) {
+#pragma clang fp contract(off)
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_tok * d) return;
+  const size_t r = i / d, c = i - r * d;
+  const float p = w[r] * y[i];
+  atomicAdd(acc + (size_t)idx[r] * d + c, p);
+}
+
+unsigned grid_for(size_t n, unsigned block = 256) { return (unsigned)((n + block - 1) / block); }
+
+template <typename XT, typename OT>
+void launch_rmsnorm_t(const void *x, const float *w, void *out, float *rstd, size_t T, size_t d,
+                      float eps, hipStream_t s) {
+  const bool vec = d % 8 == 0 && aligned16(static_cast<const XT *>(x)) &&
+                   aligned16(static_cast<OT *>(out)) && aligned16(w);
+  auto kern = vec ? rmsnorm_kernel<XT, OT, true> : rmsnorm_kernel<XT, OT, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s,
+                     static_cast<const XT *>(x), w, static_cast<OT *>(out), rstd, (int)T, (int)d,
+                     eps);
+}
+
+template <typename YT, typename OT>
+void launch_combine_t(const void *y, const int32_t *idx, const float *w, const int32_t *tr,
+                      size_t T, size_t d, size_t k, int has_shared, void *out, hipStream_t s) {
+  const bool vec =
+      d % 8 == 0 && aligned16(static_cast<const YT *>(y)) && aligned16(static_cast<OT *>(out));
+  const size_t n = T * (vec ? d / 8 : d);
+  auto kern = vec ? combine_kernel<YT, OT, true> : combine_kernel<YT, OT, false>;
+  hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(256), 0, s, static_cast<const YT *>(y), idx, w,
+                     tr, (int)T, (int)d, (int)k, has_shared, static_cast<OT *>(out));
+}
+
+template <typename T>
+void launch_rope_t(void *qk, const float *cs, const float *sn, size_t batch, size_t seq, size_t H,
+                   size_t hd, size_t pos_off, float sign, hipStream_t s) {
+  const size_t half = hd / 2;
+  const bool vec = half % 4 == 0 && aligned16(static_cast<T *>(qk)) && aligned16(cs) &&
+                   aligned16(sn);
+  const long long rows = (long long)(batch * seq);
+  const size_t n = (size_t)rows * H * (vec ? half / 4 : half);
+  auto kern = vec ? rope_kernel<T, true> : rope_kernel<T, false>;
+  hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(256), 0, s, static_cast<T *>(qk), cs, sn, rows,
+                     (int)seq, (int)H, (int)hd, (int)pos_off, sign);
+}
+
+}  // namespace
+}  // namespace prichs
+
+using namespace prichs;
+
+// ------------------------------------------------------------ entry points --
+extern "C" int prichs_moe_combine(const void *y, int y_dtype, const int32_t *topk_idx,
+                                  const float *topk_w, const int32_t *token_row, size_t T,
+                                  size_t d, size_t k, int has_shared, void *out, int out_dtype,
+                                  void *stream) {
+  PRICHS_REQUIRE(dtype_ok(y_dtype) && dtype_ok(out_dtype), "combine: bad dtype");
+  PRICHS_REQUIRE(k >= 1 && k <= PRICHS_MAX_TOPK, "combine: k=%zu outside [1, %d]", k,
+                 PRICHS_MAX_TOPK);
+  PRICHS_REQUIRE(d >= 1 && d <= (size_t)INT32_MAX, "combine: bad d=%zu", d);
+  PRICHS_REQUIRE(T <= (size_t)INT32_MAX / (k + 1), "combine: T=%zu too large", T);
+  if (T == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(y && topk_idx && topk_w && token_row && out, "combine: null pointer argument");
+  hipStream_t s = as_stream(stream);
+  const int hs = has_shared ? 1 : 0;
+  if (y_dtype == PRICHS_DTYPE_BF16) {
+    if (out_dtype == PRICHS_DTYPE_BF16)
+      launch_combine_t<bf16_t, bf16_t>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+    else
+      launch_combine_t<bf16_t, float>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+  } else {
+    if (out_dtype == PRICHS_DTYPE_BF16)
+      launch_combine_t<float, bf16_t>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+    else
+      launch_combine_t<float, float>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+  }
+  PRICHS_LAUNCH_CHECK("combine launch");
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_rmsnorm_forward(const void *x, int x_dtype, const float *w, void *out,
+                                      int out_dtype, float *rstd, size_t T, size_t d, float eps,
+                                      void *stream) {
+  PRICHS_REQUIRE(dtype_ok(x_dtype) && dtype_ok(out_dtype), "rmsnorm: bad dtype");
+  PRICHS_REQUIRE(d >= 1 && d <= (size_t)INT32_MAX && T <= (size_t)INT32_MAX,
+                 "rmsnorm: bad shape T=%zu d=%zu", T, d);
+  if (T == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(x && w && out, "rmsnorm: null pointer argument");
+  hipStream_t s = as_stream(stream);
+  if (x_dtype == PRICHS_DTYPE_BF16) {
+    if (out_dtype == PRICHS_DTYPE_BF16)
+      launch_rmsnorm_t<bf16_t, bf16_t>(x, w, out, rstd, T, d, eps, s);
+    else
+      launch_rmsnorm_t<bf16_t, float>(x, w, out, rstd, T, d, eps, s);
+  } else {
+    if (out_dtype == PRICHS_DTYPE_BF16)
+      launch_rmsnorm_t<float, bf16_t>(x, w, out, rstd, T, d, eps, s);
+    else
+      launch_rmsnorm_t<float, float>(x, w, out, rstd, T, d, eps, s);
+  }
+  PRICHS_LAUNCH_CHECK("rmsnorm launch");
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_rope_forward(void *qk, int dtype, const float *cos_cache,
+                                   const float *sin_cache, size_t cache_rows, size_t batch,
+                                   size_t seq_len, size_t n_heads, size_t head_dim,
+                                   size_t pos_offset, int sign, void *stream) {
+  PRICHS_REQUIRE(dtype_ok(dtype), "rope: bad dtype %d", dtype);
+  PRICHS_REQUIRE(head_dim >= 2 && head_dim % 2 == 0, "rope: head_dim=%zu must be even",
+                 head_dim);
+  PRICHS_REQUIRE(sign == 1 || sign == -1, "rope: sign must be +1 or -1");
+  PRICHS_REQUIRE(seq_len + pos_offset <= cache_rows,
+                 "rope: positions up to %zu exceed the cache (%zu rows)", seq_len + pos_offset,
+                 cache_rows);
+  PRICHS_REQUIRE(cache_rows <= (size_t)INT32_MAX && n_heads <= (size_t)INT32_MAX,
+                 "rope: shape too large");
+  if (batch == 0 || seq_len == 0 || n_heads == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(qk && cos_cache && sin_cache, "rope: null pointer argument");
+  hipStream_t s = as_stream(stream);
+  if (dtype == PRICHS_DTYPE_BF16)
+    launch_rope_t<bf16_t>(qk, cos_cache, sin_cache, batch, seq_len, n_heads, head_dim, pos_offset,
+                          (float)sign, s);
+  else
+    launch_rope_t<float>(qk, cos_cache, sin_cache, batch, seq_len, n_heads, head_dim, pos_offset,
+                         (float)sign, s);
+  PRICHS_LAUNCH_CHECK("rope launch");
+  return PRICHS_OK;
+}
+
+// ---------------------------------------------------------- legacy ABI --
+// void launchers: failures go to the last-error slot only, like the
+// reference's unchecked launchers.
+extern "C" void launch_rmsnorm_forward(const float *dev_x, const float *dev_weight, float *dev_out,
+                                       float *dev_rstd_out, size_t seq_len, size_t hidden_dim,
+                                       float eps, void *stream) {
+  (void)prichs_rmsnorm_forward(dev_x, PRICHS_DTYPE_F32, dev_weight, dev_out, PRICHS_DTYPE_F32,
+                               dev_rstd_out, seq_len, hidden_dim, eps, stream);
+}
+
+extern "C" void launch_swiglu_forward(const float *dev_gate, const float *dev_up, float *dev_out,
+                                      size_t total_elements, void *stream) {
+  if (total_elements == 0) return;
+  if (!dev_gate || !dev_up || !dev_out) {
+    set_error("launch_swiglu_forward: null pointer argument");
+    return;
+  }
+  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(total_elements)), dim3(256), 0,
+                     as_stream(stream), dev_gate, dev_up, dev_out, total_elements);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("launch_swiglu_forward: %s", hipGetErrorString(e));
+}
+
+extern "C" void launch_rope(float *dev_q_or_k, const float *dev_cos_cache,
+                            const float *dev_sin_cache, size_t seq_len, size_t num_heads,
+                            size_t head_dim, int backward_sign, void *stream) {
+  (void)prichs_rope_forward(dev_q_or_k, PRICHS_DTYPE_F32, dev_cos_cache, dev_sin_cache, seq_len,
+                            1, seq_len, num_heads, head_dim, 0, backward_sign >= 0 ? 1 : -1,
+                            stream);
+}
+
+extern "C" void launch_moe_gather(const float *dev_in, const int *dev_token_indices,
+                                  float *dev_out, size_t n_tokens, size_t hidden_dim,
+                                  void *stream) {
+  const size_t n = n_tokens * hidden_dim;
+  if (n == 0) return;
+  if (!dev_in || !dev_token_indices || !dev_out) {
+    set_error("launch_moe_gather: null pointer argument");
+    return;
+  }
+  hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), dev_in,
+                     dev_token_indices, dev_out, n_tokens, hidden_dim);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("launch_moe_gather: %s", hipGetErrorString(e));
+}
+
+extern "C" void launch_moe_scatter_add(const float *dev_exp_out, const int *dev_token_indices,
+                                       const float *dev_weights, float *dev_accum_out,
+                                       size_t n_tokens, size_t hidden_dim, void *stream) {
+  const size_t n = n_tokens * hidden_dim;
+  if (n == 0) return;
+  if (!dev_exp_out || !dev_token_indices || !dev_weights || !dev_accum_out) {
+    set_error("launch_moe_scatter_add: null pointer argument");
+    return;
+  }
+  hipLaunchKernelGGL(scatter_add_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream),
+                     dev_exp_out, dev_token_indices, dev_weights, dev_accum_out, n_tokens,
+                     hidden_dim);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("launch_moe_scatter_add: %s", hipGetErrorString(e));
+}

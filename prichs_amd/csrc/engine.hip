@@ -1,0 +1,346 @@
+// engine.hip -- the MoE layer engine: packed weights + workspace + forward.
+//
+// Replaces the MoE part of the reference's GpuModelEngine
+// (crates/prichs-cuda/src/engine.rs:363-649 allocation, 668-689 upload,
+// 1917-2239 forward) and the host routing of crates/prichs-model/src/
+// model.rs:1125-1177.  All memory is allocated at creation for max_tokens;
+// a forward is five launches on one stream with no host synchronisation:
+//
+//   router_topk -> permute -> grouped gate/up+SwiGLU -> grouped down -> combine
+//
+// Row space of act / y: routed rows (expert ascending, token ascending), then
+// the shared expert's T rows (group E).
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "common.hpp"
+
+struct prichs_moe_engine {
+  int device = 0;
+  size_t d = 0, f = 0, E = 0, k = 0, S = 0, max_tokens = 0;
+  int dtype = PRICHS_DTYPE_BF16;
+  bool uploaded = false;
+
+  void *arena = nullptr;  // one allocation for weights + workspace
+  float *w_router = nullptr;
+  float *router_bias = nullptr;
+  void *w_gate_up = nullptr;
+  void *w_down = nullptr;
+  float *logits = nullptr;
+  int32_t *topk_idx = nullptr;
+  float *topk_w = nullptr;
+  int32_t *block_counts = nullptr;
+  int32_t *offsets = nullptr;
+  int32_t *row_token = nullptr;
+  float *row_weight = nullptr;
+  int32_t *token_row = nullptr;
+  void *act = nullptr;
+  void *y = nullptr;
+  size_t gu_elems = 0, dn_elems = 0;  // packed elements per expert
+  size_t last_T = 0;
+
+  // Stage timing: `slots` sets of PRICHS_NUM_STAGES events, filled in turn
+  // by timed forwards (created by set_timing, never inside forward).
+  int slots = 0;
+  int recorded = 0;
+  std::vector<hipEvent_t> ev;
+};
+
+namespace prichs {
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) {
+      ok = false;
+      return;
+    }
+    if (prev != dev && hipSetDevice(dev) != hipSuccess) ok = false;
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+struct Carve {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t at = off;
+    off = roundup(off + bytes, 256);
+    return at;
+  }
+};
+
+}  // namespace
+}  // namespace prichs
+
+using namespace prichs;
+
+extern "C" int prichs_moe_engine_create(size_t d, size_t f, size_t E, size_t k, size_t n_shared,
+                                        int dtype, size_t max_tokens, prichs_moe_engine **out) {
+  PRICHS_REQUIRE(out != nullptr, "engine_create: null output handle");
+  *out = nullptr;
+  PRICHS_REQUIRE(dtype_ok(dtype), "engine_create: bad dtype %d", dtype);
+  PRICHS_REQUIRE(E >= 1 && E <= PRICHS_MAX_EXPERTS, "engine_create: E=%zu outside [1, %d]", E,
+                 PRICHS_MAX_EXPERTS);
+  PRICHS_REQUIRE(k >= 1 && k <= E && k <= PRICHS_MAX_TOPK,
+                 "engine_create: k=%zu invalid for E=%zu", k, E);
+  PRICHS_REQUIRE(n_shared <= 1, "engine_create: n_shared=%zu (0 or 1 supported)", n_shared);
+  PRICHS_REQUIRE(max_tokens >= 1 && max_tokens <= (size_t)INT32_MAX / (k + 1),
+                 "engine_create: max_tokens=%zu outside [1, %zu]", max_tokens,
+                 (size_t)INT32_MAX / (k + 1));
+  const size_t gu = prichs_packed_gate_up_elems(d, f, dtype);
+  const size_t dn = prichs_packed_down_elems(d, f, dtype);
+  {
+    // Shape support is the grouped GEMMs' (multiples of their K tile).
+    if (d == 0 || f == 0) return fail(PRICHS_ERR_UNSUPPORTED, "engine_create: d and f must be >0");
+    const size_t q = dtype == PRICHS_DTYPE_BF16 ? 64 : 16;
+    if (d % q || f % q)
+      return fail(PRICHS_ERR_UNSUPPORTED,
+                  "engine_create: d=%zu and f=%zu must be multiples of %zu for this dtype", d, f,
+                  q);
+  }
+  const size_t es = dtype_size(dtype);
+  const size_t G = E + n_shared;
+  const size_t Tm = max_tokens;
+  const size_t rows = Tm * k + n_shared * Tm;
+  const size_t nb = prichs_router_num_blocks(Tm, E);
+
+  prichs_moe_engine *eng = new (std::nothrow) prichs_moe_engine();
+  if (!eng) return fail(PRICHS_ERR_CAPACITY, "engine_create: out of host memory");
+  eng->d = d;
+  eng->f = f;
+  eng->E = E;
+  eng->k = k;
+  eng->S = n_shared;
+  eng->dtype = dtype;
+  eng->max_tokens = Tm;
+  eng->gu_elems = gu;
+  eng->dn_elems = dn;
+
+  Carve c;
+  const size_t o_router = c.take(sizeof(float) * d * E);
+  const size_t o_bias = c.take(sizeof(float) * E);
+  const size_t o_gu = c.take(es * gu * G);
+  const size_t o_dn = c.take(es * dn * G);
+  const size_t o_logits = c.take(sizeof(float) * Tm * E);
+  const size_t o_idx = c.take(sizeof(int32_t) * Tm * k);
+  const size_t o_w = c.take(sizeof(float) * Tm * k);
+  const size_t o_bc = c.take(sizeof(int32_t) * nb * E);
+  const size_t o_off = c.take(sizeof(int32_t) * (E + 2));
+  const size_t o_rt = c.take(sizeof(int32_t) * (Tm * k + Tm));
+  const size_t o_rw = c.take(sizeof(float) * Tm * k);
+  const size_t o_tr = c.take(sizeof(int32_t) * Tm * k);
+  const size_t o_act = c.take(es * rows * f);
+  const size_t o_y = c.take(es * rows * d);
+
+  int rc = PRICHS_OK;
+  if (hipGetDevice(&eng->device) != hipSuccess) {
+    rc = fail(PRICHS_ERR_HIP, "engine_create: no HIP device");
+  } else {
+    hipError_t e = hipMalloc(&eng->arena, c.off);
+    if (e != hipSuccess) {
+      eng->arena = nullptr;
+      rc = fail(PRICHS_ERR_CAPACITY, "engine_create: hipMalloc(%zu bytes): %s", c.off,
+                hipGetErrorString(e));
+    }
+  }
+  if (rc != PRICHS_OK) {
+    prichs_moe_engine_destroy(eng);
+    return rc;
+  }
+  char *base = static_cast<char *>(eng->arena);
+  eng->w_router = reinterpret_cast<float *>(base + o_router);
+  eng->router_bias = reinterpret_cast<float *>(base + o_bias);
+  eng->w_gate_up = base + o_gu;
+  eng->w_down = base + o_dn;
+  eng->logits = reinterpret_cast<float *>(base + o_logits);
+  eng->topk_idx = reinterpret_cast<int32_t *>(base + o_idx);
+  eng->topk_w = reinterpret_cast<float *>(base + o_w);
+  eng->block_counts = reinterpret_cast<int32_t *>(base + o_bc);
+  eng->offsets = reinterpret_cast<int32_t *>(base + o_off);
+  eng->row_token = reinterpret_cast<int32_t *>(base + o_rt);
+  eng->row_weight = reinterpret_cast<float *>(base + o_rw);
+  eng->token_row = reinterpret_cast<int32_t *>(base + o_tr);
+  eng->act = base + o_act;
+  eng->y = base + o_y;
+  *out = eng;
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_destroy(prichs_moe_engine *eng) {
+  if (!eng) return PRICHS_OK;
+  int rc = PRICHS_OK;
+  {
+    DeviceGuard g(eng->device);
+    for (hipEvent_t e : eng->ev)
+      if (e) (void)hipEventDestroy(e);
+    if (eng->arena && hipFree(eng->arena) != hipSuccess)
+      rc = fail(PRICHS_ERR_HIP, "engine_destroy: hipFree failed");
+  }
+  delete eng;
+  return rc;
+}
+
+extern "C" int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_router,
+                                        const float *router_bias, const float *const *gate,
+                                        const float *const *up, const float *const *down) {
+  PRICHS_REQUIRE(eng != nullptr, "engine_upload: null engine");
+  PRICHS_REQUIRE(w_router && gate && up && down, "engine_upload: null pointer argument");
+  const size_t G = eng->E + eng->S;
+  for (size_t i = 0; i < G; ++i)
+    PRICHS_REQUIRE(gate[i] && up[i] && down[i], "engine_upload: null weight for expert slot %zu",
+                   i);
+  const size_t es = dtype_size(eng->dtype);
+  std::vector<char> gu(es * eng->gu_elems * G), dn(es * eng->dn_elems * G);
+  // Reference order is [shared, routed 0..E-1]; packed order is
+  // [routed 0..E-1, shared] so the shared group follows the routed rows.
+  for (size_t slot = 0; slot < G; ++slot) {
+    const size_t grp = slot < eng->S ? eng->E : slot - eng->S;
+    int rc = prichs_pack_gate_up(gate[slot], up[slot], eng->d, eng->f, eng->dtype,
+                                 gu.data() + es * eng->gu_elems * grp);
+    if (rc) return rc;
+    rc = prichs_pack_down(down[slot], eng->d, eng->f, eng->dtype,
+                          dn.data() + es * eng->dn_elems * grp);
+    if (rc) return rc;
+  }
+  std::vector<float> bias(eng->E, 0.0f);
+  if (router_bias) std::memcpy(bias.data(), router_bias, sizeof(float) * eng->E);
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_upload: cannot select device %d", eng->device);
+  PRICHS_HIP_TRY(hipMemcpy(eng->w_router, w_router, sizeof(float) * eng->d * eng->E,
+                           hipMemcpyHostToDevice),
+                 "engine_upload: router");
+  PRICHS_HIP_TRY(hipMemcpy(eng->router_bias, bias.data(), sizeof(float) * eng->E,
+                           hipMemcpyHostToDevice),
+                 "engine_upload: router bias");
+  PRICHS_HIP_TRY(hipMemcpy(eng->w_gate_up, gu.data(), gu.size(), hipMemcpyHostToDevice),
+                 "engine_upload: gate/up");
+  PRICHS_HIP_TRY(hipMemcpy(eng->w_down, dn.data(), dn.size(), hipMemcpyHostToDevice),
+                 "engine_upload: down");
+  PRICHS_HIP_TRY(hipDeviceSynchronize(), "engine_upload: synchronize");
+  eng->uploaded = true;
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_set_router_bias(prichs_moe_engine *eng, const float *router_bias) {
+  PRICHS_REQUIRE(eng && router_bias, "engine_set_router_bias: null pointer argument");
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_set_router_bias: cannot select device");
+  PRICHS_HIP_TRY(hipMemcpy(eng->router_bias, router_bias, sizeof(float) * eng->E,
+                           hipMemcpyHostToDevice),
+                 "engine_set_router_bias");
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, size_t T,
+                                         const float *concept_bias, size_t n_concept, void *out,
+                                         int out_dtype, void *stream) {
+  PRICHS_REQUIRE(eng != nullptr, "engine_forward: null engine");
+  PRICHS_REQUIRE(dtype_ok(out_dtype), "engine_forward: bad out dtype %d", out_dtype);
+  if (!eng->uploaded) return fail(PRICHS_ERR_STATE, "engine_forward: weights not uploaded");
+  if (T > eng->max_tokens)
+    return fail(PRICHS_ERR_CAPACITY, "engine_forward: T=%zu exceeds max_tokens=%zu", T,
+                eng->max_tokens);
+  if (T == 0) {
+    eng->last_T = 0;
+    return PRICHS_OK;
+  }
+  PRICHS_REQUIRE(x && out, "engine_forward: null pointer argument");
+  PRICHS_REQUIRE(concept_bias != nullptr || n_concept == 0,
+                 "engine_forward: concept_bias is NULL but n_concept=%zu", n_concept);
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_forward: cannot select device");
+  hipStream_t s = as_stream(stream);
+  const bool tm = eng->slots > 0 && eng->recorded < eng->slots;
+  hipEvent_t *ev = tm ? &eng->ev[(size_t)eng->recorded * PRICHS_NUM_STAGES] : nullptr;
+  const size_t G = eng->E + eng->S;
+  const size_t rows = T * eng->k + eng->S * T;
+  int rc;
+  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[0], s), "engine_forward: event");
+  rc = prichs_router_topk(x, eng->dtype, eng->w_router, eng->router_bias, concept_bias, n_concept,
+                          T, eng->d, eng->E, eng->k, eng->logits, eng->topk_idx, eng->topk_w,
+                          eng->block_counts, stream);
+  if (rc) return rc;
+  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[1], s), "engine_forward: event");
+  rc = prichs_permute(eng->topk_idx, eng->topk_w, eng->block_counts, T, eng->E, eng->k,
+                      eng->offsets, eng->row_token, eng->row_weight, eng->token_row, stream);
+  if (rc) return rc;
+  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[2], s), "engine_forward: event");
+  rc = prichs_grouped_gate_up_swiglu(x, eng->row_token, eng->offsets, G, rows, eng->w_gate_up,
+                                     eng->d, eng->f, eng->dtype, eng->act, stream);
+  if (rc) return rc;
+  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[3], s), "engine_forward: event");
+  rc = prichs_grouped_down(eng->act, eng->offsets, G, rows, eng->w_down, eng->d, eng->f,
+                           eng->dtype, eng->y, stream);
+  if (rc) return rc;
+  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[4], s), "engine_forward: event");
+  rc = prichs_moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T,
+                          eng->d, eng->k, (int)eng->S, out, out_dtype, stream);
+  if (rc) return rc;
+  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[5], s), "engine_forward: event");
+  if (tm) ++eng->recorded;
+  eng->last_T = T;
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_stash(const prichs_moe_engine *eng, prichs_moe_stash *out) {
+  PRICHS_REQUIRE(eng && out, "engine_stash: null pointer argument");
+  out->T = eng->last_T;
+  out->router_logits = eng->logits;
+  out->selected_experts = eng->topk_idx;
+  out->gating_weights = eng->topk_w;
+  out->offsets = eng->offsets;
+  out->row_token = eng->row_token;
+  out->row_weight = eng->row_weight;
+  out->token_row = eng->token_row;
+  out->act = eng->act;
+  out->y = eng->y;
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_set_timing(prichs_moe_engine *eng, int max_forwards) {
+  PRICHS_REQUIRE(eng != nullptr, "engine_set_timing: null engine");
+  PRICHS_REQUIRE(max_forwards >= 0 && max_forwards <= 1 << 16,
+                 "engine_set_timing: max_forwards=%d outside [0, 65536]", max_forwards);
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_set_timing: cannot select device");
+  const size_t need = (size_t)max_forwards * PRICHS_NUM_STAGES;
+  while (eng->ev.size() < need) {
+    hipEvent_t e = nullptr;
+    PRICHS_HIP_TRY(hipEventCreate(&e), "engine_set_timing: hipEventCreate");
+    eng->ev.push_back(e);
+  }
+  eng->slots = max_forwards;
+  eng->recorded = 0;
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
+                                          int *n_forwards) {
+  PRICHS_REQUIRE(eng && ms_out, "engine_stage_ms: null pointer argument");
+  if (eng->recorded == 0)
+    return fail(PRICHS_ERR_STATE, "engine_stage_ms: no timed forward since set_timing");
+  DeviceGuard g(eng->device);
+  double acc[PRICHS_NUM_STAGES] = {0};
+  for (int f = 0; f < eng->recorded; ++f) {
+    hipEvent_t *ev = &eng->ev[(size_t)f * PRICHS_NUM_STAGES];
+    PRICHS_HIP_TRY(hipEventSynchronize(ev[PRICHS_NUM_STAGES - 1]), "engine_stage_ms: sync");
+    float ms = 0.f;
+    for (int i = 0; i + 1 < PRICHS_NUM_STAGES; ++i) {
+      PRICHS_HIP_TRY(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "engine_stage_ms: elapsed");
+      acc[i] += ms;
+    }
+    PRICHS_HIP_TRY(hipEventElapsedTime(&ms, ev[0], ev[PRICHS_NUM_STAGES - 1]),
+                   "engine_stage_ms: elapsed");
+    acc[PRICHS_NUM_STAGES - 1] += ms;
+  }
+  for (int i = 0; i < PRICHS_NUM_STAGES; ++i) ms_out[i] = (float)(acc[i] / eng->recorded);
+  if (n_forwards) *n_forwards = eng->recorded;
+  eng->recorded = 0;
+  return PRICHS_OK;
+}

@@ -1,0 +1,522 @@
+// gemm.hip -- grouped expert GEMMs on CDNA4 MFMA.
+//
+// Both GEMMs of the MoE FFN run over one "row space": routed rows in the
+// permutation order of prichs_permute, then the shared expert's rows.  Group
+// g owns rows [offsets[g], offsets[g+1]) and its own weight matrix, so the
+// routed experts and the always-on shared expert (a dense group of T rows)
+// are one persistent launch: every workgroup walks a global list of
+// (group, M-tile, N-tile) tiles, which absorbs skewed routing without
+// per-expert launches.
+//
+//   gate/up:  act[r] = silu(x[row_token[r]] @ Wg) * (x[row_token[r]] @ Wu)
+//             (crates/prichs-model/src/moe.rs:166-169, 103-105); the A rows
+//             are gathered straight from x, and the gate and up columns of
+//             one output column sit in the same lane's accumulators (packed
+//             weight interleave), so SwiGLU is applied in the epilogue.
+//   down:     y[r] = act[r] @ Wd  (moe.rs:170, 106).
+//
+// bf16 kernel: 256x256x64 tiles, 4 wave64s in a 2x2 grid each owning a
+// 128x128 sub-tile of v_mfma_f32_16x16x32_bf16 accumulators (fp32), A and B
+// staged through double-buffered LDS with an XOR swizzle of 16-byte chunks.
+// f32 kernel: 128x128x16 tiles on v_mfma_f32_16x16x4_f32 (the fp32-checked
+// mode; accumulates in fp32 like the reference CPU path).
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "common.hpp"
+
+namespace prichs {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxGroups = PRICHS_MAX_EXPERTS + 1;
+constexpr int kPadRowsDown = 256;  // packed down weights: rows padded to this
+
+// ------------------------------------------------------------------------
+// Tile scheduler shared by both kernels.
+// ------------------------------------------------------------------------
+struct TileMap {
+  int prefix[kMaxGroups + 1];  // first global M-tile of each group
+};
+
+__device__ inline void build_tile_map(TileMap &tm, const int32_t *offsets, int G, int BM) {
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int g = 0; g < G; ++g) {
+      tm.prefix[g] = run;
+      const int mg = offsets[g + 1] - offsets[g];
+      run += mg > 0 ? (mg + BM - 1) / BM : 0;
+    }
+    tm.prefix[G] = run;
+  }
+  __syncthreads();
+}
+
+__device__ inline int find_group(const TileMap &tm, int G, int mt) {
+  int g = 0;
+  while (g + 1 < G && tm.prefix[g + 1] <= mt) ++g;
+  return g;
+}
+
+// ------------------------------------------------------------------------
+// bf16 kernel
+// ------------------------------------------------------------------------
+namespace bf {
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int kThreads = 256;
+constexpr int WM = 128, WN = 128;
+constexpr int MI = WM / 16, NJ = WN / 16;
+constexpr int kIl = 64;  // gate/up interleave: packed blocks [64 gate | 64 up]
+constexpr int kStageElems = (BM + BN) * BK;
+constexpr size_t kLdsBytes = 2 * kStageElems * sizeof(bf16_t);
+static_assert(WN == 2 * kIl, "a wave's N sub-tile must hold one gate/up block");
+static_assert(BN == 4 * kIl, "packed gate/up rows are padded to a multiple of 4 * il");
+
+// LDS element offset of (row, 16-byte chunk) in a [rows][BK] tile.
+__device__ inline int lds_off(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
+
+template <bool GATEUP>
+__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
+    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
+    const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
+    bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
+    int G) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  __shared__ TileMap tm;
+  build_tile_map(tm, offsets, G, BM);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n_tiles = Np / BN;
+  const int total = tm.prefix[G] * n_tiles;
+  const int KT = K / BK;
+
+  // Global-load assignment: rows (tid>>3) + 32*i, 16-byte chunk tid&7.
+  const int ld_row = tid >> 3;
+  const int ld_chunk = tid & 7;
+  const int st_off = lds_off(ld_row, ld_chunk);  // + 32*i*BK per i (row&7 fixed)
+
+  // Fragment read offsets (row&7 == lane&7 for every fragment row).
+  const int fr_row = lane & 15;
+  int a_rd[2], b_rd[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int ch = ks * 4 + (lane >> 4);
+    a_rd[ks] = lds_off(wm * WM + fr_row, ch);
+    b_rd[ks] = lds_off(wn * WN + fr_row, ch);
+  }
+
+  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+    const int mt = tile / n_tiles;
+    const int nt = tile - mt * n_tiles;
+    const int g = find_group(tm, G, mt);
+    const int row0 = offsets[g];
+    const int mg = offsets[g + 1] - row0;
+    const int m0 = (mt - tm.prefix[g]) * BM;
+    const int n0 = nt * BN;
+
+    const bf16_t *a_ptr[8];
+    const bf16_t *b_ptr[8];
+    const bf16_t *Bg = B + (long long)g * b_group_stride;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int lr = m0 + ld_row + 32 * i;
+      lr = lr < mg ? lr : mg - 1;
+      const int vr = row0 + lr;
+      const int src = a_rows ? a_rows[vr] : vr;
+      a_ptr[i] = A + (long long)src * lda + ld_chunk * 8;
+      b_ptr[i] = Bg + (long long)(n0 + ld_row + 32 * i) * K + ld_chunk * 8;
+    }
+
+    f32x4 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint4 ra[8], rb[8];
+    auto gload = [&](int k0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ra[i] = *reinterpret_cast<const uint4 *>(a_ptr[i] + k0);
+        rb[i] = *reinterpret_cast<const uint4 *>(b_ptr[i] + k0);
+      }
+    };
+    auto lstore = [&](int buf) {
+      bf16_t *as = lds + buf * kStageElems;
+      bf16_t *bs = as + BM * BK;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        *reinterpret_cast<uint4 *>(as + st_off + 32 * i * BK) = ra[i];
+        *reinterpret_cast<uint4 *>(bs + st_off + 32 * i * BK) = rb[i];
+      }
+    };
+    auto compute = [&](int buf) {
+      const bf16_t *as = lds + buf * kStageElems;
+      const bf16_t *bs = as + BM * BK;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        bf16x8 af[MI], bfr[NJ];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd[ks] + i * 16 * BK);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          bfr[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd[ks] + j * 16 * BK);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      const bool more = kt + 1 < KT;
+      if (more) gload((kt + 1) * BK);
+      compute(kt & 1);
+      if (more) lstore((kt + 1) & 1);
+      __syncthreads();
+    }
+
+    // Epilogue.  Lane holds rows 4*(lane>>4)+r, column lane&15 of each block.
+    const int rbase = m0 + wm * WM + 4 * (lane >> 4);
+    if (GATEUP) {
+      const int cbase = (n0 / (2 * kIl) + wn) * kIl + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int lr = rbase + i * 16 + r;
+          if (lr < mg) {
+            bf16_t *crow = C + (long long)(row0 + lr) * ldc;
+#pragma unroll
+            for (int j = 0; j < NJ / 2; ++j) {
+              const int col = cbase + j * 16;
+              if (col < n_store) {
+                const float gv = acc[i][j][r];
+                const float uv = acc[i][j + NJ / 2][r];
+                crow[col] = f32_to_bf16(silu_ref(gv) * uv);
+              }
+            }
+          }
+        }
+      }
+    } else {
+      const int cbase = n0 + wn * WN + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int lr = rbase + i * 16 + r;
+          if (lr < mg) {
+            bf16_t *crow = C + (long long)(row0 + lr) * ldc;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const int col = cbase + j * 16;
+              if (col < n_store) crow[col] = f32_to_bf16(acc[i][j][r]);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+}  // namespace bf
+
+// ------------------------------------------------------------------------
+// f32 kernel (fp32-checked mode)
+// ------------------------------------------------------------------------
+namespace fp {
+constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int kThreads = 256;
+constexpr int WM = 64, WN = 64;
+constexpr int MI = WM / 16, NJ = WN / 16;
+constexpr int kIl = 32;
+constexpr int kLd = BK + 1;  // padded LDS row (floats)
+constexpr int kStage = (BM + BN) * kLd;
+constexpr size_t kLdsBytes = 2 * kStage * sizeof(float);
+static_assert(WN == 2 * kIl, "a wave's N sub-tile must hold one gate/up block");
+static_assert(BN == 4 * kIl, "packed gate/up rows are padded to a multiple of 4 * il");
+
+template <bool GATEUP>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
+    const float *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
+    const float *__restrict__ B, long long b_group_stride, int Np, int K,
+    float *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets, int G) {
+  extern __shared__ float ldsf[];
+  __shared__ TileMap tm;
+  build_tile_map(tm, offsets, G, BM);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n_tiles = Np / BN;
+  const int total = tm.prefix[G] * n_tiles;
+  const int KT = K / BK;
+  const int ld_row = tid >> 2;  // + 64*i
+  const int ld_c4 = (tid & 3) * 4;
+
+  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+    const int mt = tile / n_tiles;
+    const int nt = tile - mt * n_tiles;
+    const int g = find_group(tm, G, mt);
+    const int row0 = offsets[g];
+    const int mg = offsets[g + 1] - row0;
+    const int m0 = (mt - tm.prefix[g]) * BM;
+    const int n0 = nt * BN;
+    const float *Bg = B + (long long)g * b_group_stride;
+    const float *a_ptr[2];
+    const float *b_ptr[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int lr = m0 + ld_row + 64 * i;
+      lr = lr < mg ? lr : mg - 1;
+      const int vr = row0 + lr;
+      const int src = a_rows ? a_rows[vr] : vr;
+      a_ptr[i] = A + (long long)src * lda + ld_c4;
+      b_ptr[i] = Bg + (long long)(n0 + ld_row + 64 * i) * K + ld_c4;
+    }
+    f32x4 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    float4 ra[2], rb[2];
+    auto gload = [&](int k0) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ra[i] = *reinterpret_cast<const float4 *>(a_ptr[i] + k0);
+        rb[i] = *reinterpret_cast<const float4 *>(b_ptr[i] + k0);
+      }
+    };
+    auto lstore = [&](int buf) {
+      float *as = ldsf + buf * kStage;
+      float *bs = as + BM * kLd;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        float *pa = as + (ld_row + 64 * i) * kLd + ld_c4;
+        float *pb = bs + (ld_row + 64 * i) * kLd + ld_c4;
+        pa[0] = ra[i].x; pa[1] = ra[i].y; pa[2] = ra[i].z; pa[3] = ra[i].w;
+        pb[0] = rb[i].x; pb[1] = rb[i].y; pb[2] = rb[i].z; pb[3] = rb[i].w;
+      }
+    };
+    auto compute = [&](int buf) {
+      const float *as = ldsf + buf * kStage;
+      const float *bs = as + BM * kLd;
+#pragma unroll
+      for (int ks = 0; ks < BK / 4; ++ks) {
+        const int kk = ks * 4 + (lane >> 4);
+        float af[MI], bfr[NJ];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) af[i] = as[(wm * WM + i * 16 + (lane & 15)) * kLd + kk];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) bfr[j] = bs[(wn * WN + j * 16 + (lane & 15)) * kLd + kk];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      const bool more = kt + 1 < KT;
+      if (more) gload((kt + 1) * BK);
+      compute(kt & 1);
+      if (more) lstore((kt + 1) & 1);
+      __syncthreads();
+    }
+
+    const int rbase = m0 + wm * WM + 4 * (lane >> 4);
+    if (GATEUP) {
+      const int cbase = (n0 / (2 * kIl) + wn) * kIl + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int lr = rbase + i * 16 + r;
+          if (lr < mg) {
+            float *crow = C + (long long)(row0 + lr) * ldc;
+#pragma unroll
+            for (int j = 0; j < NJ / 2; ++j) {
+              const int col = cbase + j * 16;
+              if (col < n_store) crow[col] = silu_ref(acc[i][j][r]) * acc[i][j + NJ / 2][r];
+            }
+          }
+        }
+    } else {
+      const int cbase = n0 + wn * WN + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int lr = rbase + i * 16 + r;
+          if (lr < mg) {
+            float *crow = C + (long long)(row0 + lr) * ldc;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const int col = cbase + j * 16;
+              if (col < n_store) crow[col] = acc[i][j][r];
+            }
+          }
+        }
+    }
+  }
+}
+}  // namespace fp
+
+size_t il_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)bf::kIl : (size_t)fp::kIl; }
+
+int check_gemm_shape(size_t d, size_t f, int dtype, const char *who) {
+  if (!dtype_ok(dtype)) return fail(PRICHS_ERR_INVALID_ARGUMENT, "%s: bad dtype %d", who, dtype);
+  const size_t q = dtype == PRICHS_DTYPE_BF16 ? (size_t)bf::BK : (size_t)fp::BK;
+  if (d == 0 || f == 0 || d % q || f % q)
+    return fail(PRICHS_ERR_UNSUPPORTED, "%s: d=%zu and f=%zu must be positive multiples of %zu",
+                who, d, f, q);
+  if (d > (1u << 20) || f > (1u << 20))
+    return fail(PRICHS_ERR_UNSUPPORTED, "%s: d=%zu or f=%zu too large", who, d, f);
+  return PRICHS_OK;
+}
+
+template <typename T> void put(void *out, size_t i, float v);
+template <> void put<float>(void *out, size_t i, float v) { static_cast<float *>(out)[i] = v; }
+template <> void put<bf16_t>(void *out, size_t i, float v) {
+  static_cast<bf16_t *>(out)[i] = f32_to_bf16(v);
+}
+
+// Packed gate/up rows: 2 * roundup(f, 2 * il) (a multiple of the kernel's BN).
+size_t gate_up_np(size_t f, size_t il) { return 2 * roundup(f, 2 * il); }
+
+template <typename T>
+void pack_gate_up_impl(const float *gate, const float *up, size_t d, size_t f, size_t il,
+                       void *out) {
+  const size_t np = gate_up_np(f, il);
+  for (size_t p = 0; p < np; ++p) {
+    const size_t b = p / (2 * il), q = p % (2 * il);
+    const float *src = q < il ? gate : up;
+    const size_t col = il * b + (q < il ? q : q - il);
+    for (size_t k = 0; k < d; ++k) put<T>(out, p * d + k, col < f ? src[k * f + col] : 0.0f);
+  }
+}
+
+template <typename T> void pack_down_impl(const float *down, size_t d, size_t f, void *out) {
+  const size_t np = roundup(d, kPadRowsDown);
+  for (size_t n = 0; n < np; ++n)
+    for (size_t k = 0; k < f; ++k) put<T>(out, n * f + k, n < d ? down[k * d + n] : 0.0f);
+}
+
+int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, const void *B,
+                   long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
+                   const int32_t *offsets, int G, size_t max_rows, int dtype, hipStream_t s) {
+  const int cus = device_cu_count();
+  if (cus <= 0) return fail(PRICHS_ERR_HIP, "grouped gemm: cannot query the device");
+  if (dtype == PRICHS_DTYPE_BF16) {
+    const size_t ub = (max_rows / bf::BM + G) * (size_t)(Np / bf::BN);
+    const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus));
+    auto kern = gateup ? bf::grouped_gemm_kernel<true> : bf::grouped_gemm_kernel<false>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[gateup]) {
+      PRICHS_HIP_TRY(hipFuncSetAttribute((const void *)kern,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)bf::kLdsBytes),
+                     "grouped gemm: set LDS size");
+      attr_set[gateup] = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(bf::kThreads), bf::kLdsBytes, s,
+                       static_cast<const bf16_t *>(A), a_rows, lda,
+                       static_cast<const bf16_t *>(B), b_stride, Np, K,
+                       static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G);
+  } else {
+    const size_t ub = (max_rows / fp::BM + G) * (size_t)(Np / fp::BN);
+    const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus * 4));
+    auto kern = gateup ? fp::grouped_gemm_kernel<true> : fp::grouped_gemm_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(fp::kThreads), fp::kLdsBytes, s,
+                       static_cast<const float *>(A), a_rows, lda,
+                       static_cast<const float *>(B), b_stride, Np, K,
+                       static_cast<float *>(Cp), ldc, n_store, offsets, G);
+  }
+  PRICHS_LAUNCH_CHECK("grouped gemm launch");
+  return PRICHS_OK;
+}
+
+}  // namespace
+}  // namespace prichs
+
+using namespace prichs;
+
+extern "C" size_t prichs_gate_up_interleave(int dtype) { return dtype_ok(dtype) ? il_of(dtype) : 0; }
+
+extern "C" size_t prichs_packed_gate_up_elems(size_t d, size_t f, int dtype) {
+  if (!dtype_ok(dtype)) return 0;
+  return gate_up_np(f, il_of(dtype)) * d;
+}
+
+extern "C" size_t prichs_packed_down_elems(size_t d, size_t f, int dtype) {
+  if (!dtype_ok(dtype)) return 0;
+  return roundup(d, kPadRowsDown) * f;
+}
+
+extern "C" int prichs_pack_gate_up(const float *gate, const float *up, size_t d, size_t f,
+                                   int dtype, void *packed_out) {
+  if (int rc = check_gemm_shape(d, f, dtype, "pack_gate_up")) return rc;
+  PRICHS_REQUIRE(gate && up && packed_out, "pack_gate_up: null pointer argument");
+  if (dtype == PRICHS_DTYPE_BF16)
+    pack_gate_up_impl<bf16_t>(gate, up, d, f, il_of(dtype), packed_out);
+  else
+    pack_gate_up_impl<float>(gate, up, d, f, il_of(dtype), packed_out);
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_pack_down(const float *down, size_t d, size_t f, int dtype,
+                                void *packed_out) {
+  if (int rc = check_gemm_shape(d, f, dtype, "pack_down")) return rc;
+  PRICHS_REQUIRE(down && packed_out, "pack_down: null pointer argument");
+  if (dtype == PRICHS_DTYPE_BF16)
+    pack_down_impl<bf16_t>(down, d, f, packed_out);
+  else
+    pack_down_impl<float>(down, d, f, packed_out);
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_token,
+                                             const int32_t *offsets, size_t G, size_t max_rows,
+                                             const void *w_packed, size_t d, size_t f, int dtype,
+                                             void *act, void *stream) {
+  if (int rc = check_gemm_shape(d, f, dtype, "gate_up")) return rc;
+  PRICHS_REQUIRE(G >= 1 && G <= (size_t)kMaxGroups, "gate_up: G=%zu outside [1, %d]", G,
+                 kMaxGroups);
+  PRICHS_REQUIRE(x && row_token && offsets && w_packed && act, "gate_up: null pointer argument");
+  PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX, "gate_up: max_rows too large");
+  const size_t np = gate_up_np(f, il_of(dtype));
+  return launch_grouped(true, x, row_token, (int)d, w_packed, (long long)(np * d), (int)np,
+                        (int)d, act, (int)f, (int)f, offsets, (int)G, max_rows, dtype,
+                        as_stream(stream));
+}
+
+extern "C" int prichs_grouped_down(const void *act, const int32_t *offsets, size_t G,
+                                   size_t max_rows, const void *w_packed, size_t d, size_t f,
+                                   int dtype, void *y, void *stream) {
+  if (int rc = check_gemm_shape(d, f, dtype, "down")) return rc;
+  PRICHS_REQUIRE(G >= 1 && G <= (size_t)kMaxGroups, "down: G=%zu outside [1, %d]", G,
+                 kMaxGroups);
+  PRICHS_REQUIRE(act && offsets && w_packed && y, "down: null pointer argument");
+  PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX, "down: max_rows too large");
+  const size_t np = roundup(d, kPadRowsDown);
+  return launch_grouped(false, act, nullptr, (int)f, w_packed, (long long)(np * f), (int)np,
+                        (int)f, y, (int)d, (int)d, offsets, (int)G, max_rows, dtype,
+                        as_stream(stream));
+}

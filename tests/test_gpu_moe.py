@@ -1,0 +1,242 @@
+"""GPU parity of the MoE hot path against the CPU oracle, through the C ABI.
+
+Bars (written in each test):
+* routing (logits, selected experts) and the permutation: bit-exact;
+* gate weights: within 1e-6 relative (GPU expf vs glibc expf);
+* fp32 configurations: max |gpu - ref| / max |ref| <= 1e-4;
+* bf16 configurations: max |gpu - ref| / max |ref| <= 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from prichs_amd import _lib as L
+from prichs_amd import moe, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "bf16": 2e-2}
+
+
+def dev(a, dtype="f32"):
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda")
+    return t.to(torch.bfloat16) if dtype == "bf16" else t
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy() if t.dtype == torch.bfloat16 else t.cpu().numpy()
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+# ----------------------------------------------------------------- router --
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+def test_router_bit_exact(cuda, orc, cfg):
+    over = {"T": 4096} if cfg == 3 else {}
+    inp = synth.config_inputs(cfg, **over)
+    say("router", cfg, inp.T, inp.d)
+    logits, idx, w, _ = ops.router_topk(dev(inp.x, inp.dtype), dev(inp.w_router),
+                                        dev(inp.router_bias), inp.k)
+    rl, rs, rw = orc.route(inp.x, inp.w_router, inp.router_bias, inp.k)
+    np.testing.assert_array_equal(host(logits).view(np.uint32), rl.view(np.uint32))
+    np.testing.assert_array_equal(host(idx), rs)
+    assert rel_err(host(w), rw) <= 1e-6
+
+
+@pytest.mark.parametrize("E,k,T,d", [(4, 2, 77, 64), (8, 1, 33, 96), (16, 3, 200, 128),
+                                     (64, 8, 129, 40), (3, 3, 5, 8), (1, 1, 9, 16)])
+def test_router_shapes(cuda, orc, E, k, T, d):
+    rng = np.random.default_rng(E * 100 + k)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    wr = (0.1 * rng.standard_normal((d, E))).astype(np.float32)
+    b = (0.05 * rng.standard_normal(E)).astype(np.float32)
+    logits, idx, w, _ = ops.router_topk(dev(x), dev(wr), dev(b), k)
+    rl, rs, rw = orc.route(x, wr, b, k)
+    np.testing.assert_array_equal(host(logits).view(np.uint32), rl.view(np.uint32))
+    np.testing.assert_array_equal(host(idx), rs)
+    assert rel_err(host(w), rw) <= 1e-6
+
+
+def test_router_ties_nan_and_concept_bias(cuda, orc):
+    T, d, E, k = 64, 16, 8, 2
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    x[:16] = 0.0  # raw logits exactly +0: selection decided by the bias, with ties
+    wr = (0.2 * rng.standard_normal((d, E))).astype(np.float32)
+    wr_nan = wr.copy()
+    wr_nan[3, 5] = np.nan  # every token gets a NaN logit on expert 5
+    b = np.array([0.5, 0.5, -0.0, 0.0, 0.5, 0.1, -1, 0.5], np.float32)
+    cb = np.array([0.0, 0.0, 0.25], np.float32)
+    for w_r in (wr, wr_nan):
+        for concept in (None, cb):
+            logits, idx, w, _ = ops.router_topk(dev(x), dev(w_r), dev(b), k,
+                                                None if concept is None else dev(concept))
+            rl, rs, rw = orc.route(x, w_r, b, k, concept_bias=concept)
+            np.testing.assert_array_equal(host(logits).view(np.uint32), rl.view(np.uint32))
+            np.testing.assert_array_equal(host(idx), rs)
+            gw = host(w)
+            assert np.array_equal(np.isnan(gw), np.isnan(rw))
+            ok = ~np.isnan(rw)
+            assert np.abs(gw[ok] - rw[ok]).max() <= 1e-6
+
+
+# ------------------------------------------------------------ permutation --
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+def test_permutation_bit_exact(cuda, orc, cfg):
+    over = {"T": 16384} if cfg == 3 else {}
+    inp = synth.config_inputs(cfg, **over)
+    say("permute", cfg, inp.T)
+    _, idx, w, bc = ops.router_topk(dev(inp.x, inp.dtype), dev(inp.w_router),
+                                    dev(inp.router_bias), inp.k)
+    off, rt, rw, tr = ops.permute(idx, w, bc, inp.E)
+    _, rs, rgw = orc.route(inp.x, inp.w_router, inp.router_bias, inp.k)
+    o_off, o_rt, o_rw, o_tr = orc.bin_tokens(rs, host(w), inp.E)
+    T, k = inp.T, inp.k
+    np.testing.assert_array_equal(host(off)[: inp.E + 1], o_off)
+    assert host(off)[inp.E + 1] == T * k + T
+    np.testing.assert_array_equal(host(rt)[: T * k], o_rt)
+    np.testing.assert_array_equal(host(rt)[T * k:], np.arange(T))
+    np.testing.assert_array_equal(host(rw), o_rw)
+    np.testing.assert_array_equal(host(tr), o_tr)
+
+
+# ------------------------------------------------------------------ GEMMs --
+def _stage_inputs(inp):
+    x = dev(inp.x, inp.dtype)
+    _, idx, w, bc = ops.router_topk(x, dev(inp.w_router), dev(inp.router_bias), inp.k)
+    off, rt, rw, tr = ops.permute(idx, w, bc, inp.E)
+    order = list(range(inp.n_shared, inp.n_shared + inp.E)) + list(range(inp.n_shared))
+    gu = ops.to_device_packed([ops.pack_gate_up(inp.gate[j], inp.up[j], inp.dtype) for j in order],
+                              inp.dtype)
+    dn = ops.to_device_packed([ops.pack_down(inp.down[j], inp.dtype) for j in order], inp.dtype)
+    return x, idx, w, off, rt, tr, gu, dn, order
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 4])
+def test_grouped_gemms_against_oracle(cuda, orc, cfg):
+    inp = synth.config_inputs(cfg)
+    say("gemm", cfg)
+    T, k, E, d, f = inp.T, inp.k, inp.E, inp.d, inp.f
+    x, idx, w, off, rt, tr, gu, dn, order = _stage_inputs(inp)
+    G, rows = E + inp.n_shared, T * k + T
+    act = ops.grouped_gate_up_swiglu(x, rt, off, G, rows, gu, d, f)
+    y = ops.grouped_down(act, off, G, rows, dn, d, f)
+    h_off, h_rt = host(off), host(rt)
+    h_act, h_y = host(act), host(y)
+    tol = TOL[inp.dtype]
+    rng = np.random.default_rng(0)
+    for g in range(G):
+        r0, r1 = h_off[g], h_off[g + 1]
+        if r1 == r0:
+            continue
+        sel = np.arange(r0, r1)
+        if sel.size > 256:
+            sel = np.sort(rng.choice(sel, 256, replace=False))
+        j = order[g]
+        xr = inp.x[h_rt[sel]]
+        ga = orc.matmul_2d(xr, inp.gate[j])
+        ua = orc.matmul_2d(xr, inp.up[j])
+        a_ref = orc.swiglu(ga, ua)
+        assert rel_err(h_act[sel], a_ref) <= tol, ("act", g)
+        # down GEMM on the GPU's own act rows isolates the second GEMM's error
+        y_ref = orc.matmul_2d(h_act[sel], inp.down[j])
+        assert rel_err(h_y[sel], y_ref) <= tol, ("y", g)
+
+
+# ------------------------------------------------------------- full layer --
+@pytest.mark.parametrize("cfg", [1, 2, 4])
+def test_moe_layer_full_against_oracle(cuda, orc, cfg):
+    inp = synth.config_inputs(cfg)
+    say("layer", cfg, inp.T)
+    layer = moe.MoELayer.from_inputs(inp)
+    out, stash = layer.forward_train(inp.x)
+    r = orc.moe_forward(inp)
+    np.testing.assert_array_equal(stash.selected_experts, r["sel"])
+    np.testing.assert_array_equal(stash.router_logits.view(np.uint32), r["logits"].view(np.uint32))
+    np.testing.assert_array_equal(stash.expert_offsets, r["offsets"])
+    np.testing.assert_array_equal(stash.row_token, r["row_token"])
+    assert rel_err(stash.gating_weights, r["gw"]) <= 1e-6
+    assert rel_err(out, r["out"]) <= TOL[inp.dtype]
+    layer.engine.close()
+
+
+def test_moe_layer_skewed_config3_sampled_rows(cuda, orc):
+    # Full size (16384 tokens, ~60% of rows on experts 0-1).  Routing and the
+    # permutation are checked on every token; outputs on 384 sampled tokens
+    # (per-token results do not depend on the rest of the batch).
+    inp = synth.config_inputs(3)
+    say("layer skew", inp.T)
+    layer = moe.MoELayer.from_inputs(inp)
+    out, stash = layer.forward_train(inp.x)
+    _, rs, _ = orc.route(inp.x, inp.w_router, inp.router_bias, inp.k)
+    np.testing.assert_array_equal(stash.selected_experts, rs)
+    cnt = np.bincount(rs.reshape(-1), minlength=inp.E)
+    assert 0.59 <= (cnt[0] + cnt[1]) / rs.size <= 0.61
+    o_off, o_rt, _, _ = orc.bin_tokens(rs, stash.gating_weights, inp.E)
+    np.testing.assert_array_equal(stash.expert_offsets, o_off)
+    np.testing.assert_array_equal(stash.row_token, o_rt)
+    rows = np.sort(np.random.default_rng(3).choice(inp.T, 384, replace=False))
+    sub = synth.MoEInputs(**{**inp.__dict__, "x": inp.x[rows], "T": len(rows)})
+    r = orc.moe_forward(sub)
+    assert rel_err(out[rows], r["out"]) <= TOL["bf16"]
+    layer.engine.close()
+
+
+def test_moe_forward_deterministic_and_ragged(cuda, orc):
+    inp = synth.config_inputs(2, T=1000)  # ragged: not a multiple of any tile
+    eng = moe.MoEEngine(inp.d, inp.f, inp.E, inp.k, 1, "bf16", max_tokens=inp.T)
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    x = dev(inp.x, "bf16")
+    o1 = eng.forward(x, out_dtype=torch.float32)
+    o2 = eng.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)  # no atomics: bitwise reproducible
+    r = orc.moe_forward(inp)
+    assert rel_err(host(o1), r["out"]) <= TOL["bf16"]
+    # smaller batches reuse the same workspace; T = 1 and an empty batch
+    for T in (1, 17, 0):
+        sub = synth.MoEInputs(**{**inp.__dict__, "x": inp.x[:T], "T": T})
+        o = eng.forward(dev(inp.x[:T], "bf16"), out_dtype=torch.float32)
+        if T:
+            assert rel_err(host(o), orc.moe_forward(sub)["out"]) <= TOL["bf16"]
+    # capacity errors are reported, not faulted
+    with pytest.raises(L.PrichsError) as e:
+        eng.forward(dev(np.zeros((inp.T + 1, inp.d), np.float32), "bf16"))
+    assert e.value.status == L.PRICHS_ERR_CAPACITY
+    eng.close()
+
+
+def test_moe_bf16_output_and_aux_bias(cuda, orc):
+    inp = synth.config_inputs(4)
+    layer = moe.MoELayer.from_inputs(inp)
+    x = dev(inp.x, "bf16")
+    ob = layer.engine.forward(x, out_dtype=torch.bfloat16)
+    r = orc.moe_forward(inp)
+    assert rel_err(host(ob), r["out"]) <= TOL["bf16"]
+    # aux-loss-free bias update (moe.rs:228-245) changes routing on the device.
+    counts = np.bincount(r["sel"].reshape(-1), minlength=inp.E)
+    layer.update_aux_free_bias(counts, inp.T, 5.0)
+    out2, st2 = layer.forward_train(inp.x)
+    inp2 = synth.MoEInputs(**{**inp.__dict__, "router_bias": layer.router_bias.copy()})
+    r2 = orc.moe_forward(inp2)
+    np.testing.assert_array_equal(st2.selected_experts, r2["sel"])
+    assert rel_err(out2, r2["out"]) <= TOL["bf16"]
+    layer.engine.close()
+
+
+def test_engine_stage_timing(cuda):
+    inp = synth.config_inputs(4)
+    eng = moe.MoEEngine(inp.d, inp.f, inp.E, inp.k, 1, "bf16", max_tokens=inp.T)
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    eng.set_timing(3)
+    for _ in range(5):
+        eng.forward(dev(inp.x, "bf16"))
+    ms = eng.stage_ms()
+    assert ms["n"] == 3
+    assert all(v >= 0 for v in ms.values())
+    assert ms["total"] >= max(ms["gate_up"], ms["down"])
+    eng.close()

@@ -1,0 +1,128 @@
+"""GPU parity of RMSNorm, RoPE and the legacy f32 launchers, through the C ABI.
+
+Bars: RoPE is bit-exact (same separately rounded products and sums as
+backward.rs:175-184); RMSNorm within 2e-6 relative (parallel sum of squares);
+legacy launchers as their reference tests or closed forms state.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from prichs_amd import _lib as L
+from prichs_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda").to(dtype)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr())
+
+
+@pytest.mark.parametrize("T,d", [(8192, 1536), (7, 100), (33, 1536), (1, 8)])
+def test_rmsnorm_against_oracle(cuda, orc, T, d):
+    rng = np.random.default_rng(T + d)
+    x = (2 * rng.standard_normal((T, d))).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(d)).astype(np.float32)
+    ref = orc.rms_norm(x, w, 1e-5)
+    out, rstd = ops.rmsnorm(dev(x), dev(w), 1e-5)
+    assert rel_err(host(out), ref) <= 2e-6
+    x64 = x.astype(np.float64)
+    assert rel_err(host(rstd), 1 / np.sqrt((x64 ** 2).mean(1) + 1e-5)) <= 2e-6
+    # bf16 in / bf16 out: the input is bf16, the output is the rounded f32 result
+    xb = synth.round_bf16(x)
+    outb, _ = ops.rmsnorm(dev(xb, torch.bfloat16), dev(w), 1e-5)
+    refb = synth.round_bf16(orc.rms_norm(xb, w, 1e-5))
+    assert np.abs(host(outb) - refb).max() <= 2 ** -7 * np.abs(refb).max()
+
+
+def test_legacy_rmsnorm_known_answer(cuda):
+    # engine.rs:3041-3053: row [2,2,2,2], w = 1 -> 1.0, rstd 0.5.
+    x = dev(np.array([[1, 2, 3, 4], [2, 2, 2, 2]], np.float32))
+    w = dev(np.ones(4, np.float32))
+    out = torch.empty_like(x)
+    rstd = torch.empty(2, device="cuda")
+    lib = L.load()
+    lib.launch_rmsnorm_forward(ptr(x), ptr(w), ptr(out), ptr(rstd), 2, 4, 1e-5, None)
+    assert L.last_error() == "" or "launch" not in L.last_error()
+    o = host(out)
+    assert np.abs(o[1] - 1.0).max() < 1e-4
+    assert abs(host(rstd)[1] - 0.5) < 1e-4
+
+
+@pytest.mark.parametrize("B,S,H,hd,off", [(4, 2048, 12, 128, 0), (4, 2048, 3, 128, 0),
+                                          (1, 37, 2, 6, 5), (2, 16, 1, 10, 0)])
+def test_rope_bit_exact(cuda, orc, B, S, H, hd, off):
+    rng = np.random.default_rng(S + H + hd)
+    cos, sin = orc.precompute_rope_cache(max(S + off, 1024), hd, 500000.0)
+    rows = max(S + off, 1024)
+    q = rng.standard_normal((B, S, H, hd)).astype(np.float32)
+    ref = np.stack([orc.rope_forward(q[b], cos, sin, pos_offset=off) for b in range(B)])
+    qd = dev(q)
+    ops.rope_(qd, dev(cos), dev(sin), rows, B, S, pos_offset=off)
+    np.testing.assert_array_equal(host(qd).view(np.uint32), ref.view(np.uint32))
+    qb = synth.round_bf16(q)
+    refb = synth.round_bf16(np.stack([orc.rope_forward(qb[b], cos, sin, pos_offset=off)
+                                      for b in range(B)]))
+    qdb = dev(qb, torch.bfloat16)
+    ops.rope_(qdb, dev(cos), dev(sin), rows, B, S, pos_offset=off)
+    np.testing.assert_array_equal(host(qdb), refb)
+    # sign = -1 undoes the rotation up to rounding
+    ops.rope_(qd, dev(cos), dev(sin), rows, B, S, pos_offset=off, sign=-1)
+    assert np.abs(host(qd) - q).max() < 1e-5
+
+
+def test_legacy_rope_identity_and_sign(cuda, orc):
+    # engine.rs:2970-2972: cos = 1, sin = 0 leaves Q/K unchanged.
+    S, H, hd = 4, 2, 8
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((S, H, hd)).astype(np.float32)
+    qd = dev(q)
+    lib = L.load()
+    lib.launch_rope(ptr(qd), ptr(dev(np.ones(S * hd // 2))), ptr(dev(np.zeros(S * hd // 2))),
+                    S, H, hd, 1, None)
+    np.testing.assert_array_equal(host(qd), q)
+    cos, sin = orc.precompute_rope_cache(S, hd, 10000.0)
+    lib.launch_rope(ptr(qd), ptr(dev(cos)), ptr(dev(sin)), S, H, hd, 1, None)
+    np.testing.assert_array_equal(host(qd), orc.rope_forward(q, cos, sin))
+
+
+def test_legacy_swiglu_gather_scatter(cuda, orc):
+    rng = np.random.default_rng(2)
+    n = 10007
+    g = (4 * rng.standard_normal(n)).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    out = torch.empty(n, device="cuda")
+    lib = L.load()
+    gd, ud = dev(g), dev(u)
+    lib.launch_swiglu_forward(ptr(gd), ptr(ud), ptr(out), n, None)
+    assert rel_err(host(out), orc.swiglu(g, u)) <= 1e-6
+    T, d = 50, 24
+    src = rng.standard_normal((T, d)).astype(np.float32)
+    idx = np.array([3, 7, 7, 0, 49], np.int32)
+    idx_d = torch.from_numpy(idx).to("cuda")
+    srcd = dev(src)
+    gath = torch.empty((len(idx), d), device="cuda")
+    lib.launch_moe_gather(ptr(srcd), ptr(idx_d), ptr(gath), len(idx), d, None)
+    np.testing.assert_array_equal(host(gath), src[idx])
+    uniq = np.array([5, 1, 9], np.int32)
+    y = rng.standard_normal((3, d)).astype(np.float32)
+    wts = np.array([0.25, 0.5, 2.0], np.float32)
+    acc = dev(src)
+    lib.launch_moe_scatter_add(ptr(dev(y)), ptr(torch.from_numpy(uniq).to("cuda")), ptr(dev(wts)),
+                               ptr(acc), 3, d, None)
+    expect = src.copy()
+    for i, t in enumerate(uniq):
+        expect[t] = expect[t] + wts[i] * y[i]
+    np.testing.assert_array_equal(host(acc), expect)
