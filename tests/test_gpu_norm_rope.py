@@ -27,6 +27,9 @@ def host(t):
 
 
 def ptr(t):
+    """Raw device address of t.  The caller must keep t referenced until the
+    work that uses the address has completed: a temporary freed before the
+    launch is enqueued hands its block to the next allocation."""
     return C.c_void_p(t.data_ptr())
 
 
@@ -90,11 +93,12 @@ def test_legacy_rope_identity_and_sign(cuda, orc):
     q = rng.standard_normal((S, H, hd)).astype(np.float32)
     qd = dev(q)
     lib = L.load()
-    lib.launch_rope(ptr(qd), ptr(dev(np.ones(S * hd // 2))), ptr(dev(np.zeros(S * hd // 2))),
-                    S, H, hd, 1, None)
+    ones_d, zeros_d = dev(np.ones(S * hd // 2)), dev(np.zeros(S * hd // 2))
+    lib.launch_rope(ptr(qd), ptr(ones_d), ptr(zeros_d), S, H, hd, 1, None)
     np.testing.assert_array_equal(host(qd), q)
     cos, sin = orc.precompute_rope_cache(S, hd, 10000.0)
-    lib.launch_rope(ptr(qd), ptr(dev(cos)), ptr(dev(sin)), S, H, hd, 1, None)
+    cos_d, sin_d = dev(cos), dev(sin)
+    lib.launch_rope(ptr(qd), ptr(cos_d), ptr(sin_d), S, H, hd, 1, None)
     np.testing.assert_array_equal(host(qd), orc.rope_forward(q, cos, sin))
 
 
@@ -120,8 +124,9 @@ def test_legacy_swiglu_gather_scatter(cuda, orc):
     y = rng.standard_normal((3, d)).astype(np.float32)
     wts = np.array([0.25, 0.5, 2.0], np.float32)
     acc = dev(src)
-    lib.launch_moe_scatter_add(ptr(dev(y)), ptr(torch.from_numpy(uniq).to("cuda")), ptr(dev(wts)),
-                               ptr(acc), 3, d, None)
+    y_d, uniq_d, wts_d = dev(y), torch.from_numpy(uniq).to("cuda"), dev(wts)
+    assert uniq.min() >= 0 and uniq.max() < T  # indices address rows of acc [T, d]
+    lib.launch_moe_scatter_add(ptr(y_d), ptr(uniq_d), ptr(wts_d), ptr(acc), 3, d, None)
     expect = src.copy()
     for i, t in enumerate(uniq):
         expect[t] = expect[t] + wts[i] * y[i]
