@@ -158,13 +158,13 @@ int prichs_permute(const int32_t *topk_idx, const float *topk_w,
                    int32_t *token_row, void *stream);
 
 /* Packed expert-weight layouts used by the grouped GEMMs (host functions,
- * no GPU needed).  `il` selects the gate/up interleave of the kernel that
- * will consume the buffer; pass prichs_gate_up_interleave(dtype).
+ * no GPU needed).  il = prichs_gate_up_interleave(dtype) is the gate/up
+ * interleave of the kernel that consumes the buffer.
  *
- * gate/up, one expert: packed [Np, K = d] with K contiguous,
- *   Np = 2 * roundup(f, 2 * il); packed row p = 2*il*b + q holds column
- *   il*b + q of gate (q < il) or column il*b + q - il of up (q >= il),
- *   zero when that column is >= f.
+ * gate/up, one expert: packed [Np, K = d] with K contiguous, Np =
+ *   roundup(2 * roundup(f, il), N tile) (N tile 256 for bf16, 128 for f32);
+ *   packed row p = 2*il*b + q holds column il*b + q of gate (q < il) or
+ *   column il*b + q - il of up (q >= il), zero when that column is >= f.
  * down, one expert: packed [roundup(d, 256), K = f] = W_down^T, zero rows
  *   past d.
  * Element type: dtype (bf16 by round-to-nearest-even from f32). */

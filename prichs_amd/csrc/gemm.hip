@@ -15,9 +15,10 @@
 //             weight interleave), so SwiGLU is applied in the epilogue.
 //   down:     y[r] = act[r] @ Wd  (moe.rs:170, 106).
 //
-// bf16 kernel: 256x256x64 tiles, 4 wave64s in a 2x2 grid each owning a
-// 128x128 sub-tile of v_mfma_f32_16x16x32_bf16 accumulators (fp32), A and B
-// staged through double-buffered LDS with an XOR swizzle of 16-byte chunks.
+// bf16 kernel: 256x256x64 tiles, 8 wave64s in a 2x4 grid each owning a
+// 128x64 sub-tile of v_mfma_f32_16x16x32_bf16 accumulators (fp32, two waves
+// per SIMD), A and B staged through double-buffered LDS with an XOR swizzle
+// of 16-byte chunks, persistent workgroups walking an XCD-aware tile order.
 // f32 kernel: 128x128x16 tiles on v_mfma_f32_16x16x4_f32 (the fp32-checked
 // mode; accumulates in fp32 like the reference CPU path).
 #include <algorithm>
@@ -31,9 +32,20 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Native vector types (not HIP's struct-based uint4/uint2), so staged
+// fragments stay in registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxGroups = PRICHS_MAX_EXPERTS + 1;
 constexpr int kPadRowsDown = 256;  // packed down weights: rows padded to this
+
+#ifndef PRICHS_BF16_WGM
+#define PRICHS_BF16_WGM 2
+#endif
+#ifndef PRICHS_BF16_WGN
+#define PRICHS_BF16_WGN 4
+#endif
 
 // ------------------------------------------------------------------------
 // Tile scheduler shared by both kernels.
@@ -65,21 +77,47 @@ __device__ inline int find_group(const TileMap &tm, int G, int mt) {
 // bf16 kernel
 // ------------------------------------------------------------------------
 namespace bf {
+// Tile shape of one workgroup: BM x BN outputs, K consumed BK at a time.
+// WGM x WGN wave64s; a wave owns a WM x WN sub-tile of 16x16 MFMA blocks.
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int kThreads = 256;
-constexpr int WM = 128, WN = 128;
+constexpr int WGM = PRICHS_BF16_WGM, WGN = PRICHS_BF16_WGN;
+constexpr int kThreads = 64 * WGM * WGN;
+constexpr int WM = BM / WGM, WN = BN / WGN;
 constexpr int MI = WM / 16, NJ = WN / 16;
-constexpr int kIl = 64;  // gate/up interleave: packed blocks [64 gate | 64 up]
+constexpr int kIl = WN / 2;             // gate/up interleave: packed blocks [kIl gate | kIl up]
+constexpr int kRowsPerPass = kThreads / 8;  // 8 threads load one 128-byte row slice
+constexpr int LA = BM / kRowsPerPass;   // A chunks per thread per stage
+constexpr int LB = BN / kRowsPerPass;   // B chunks per thread per stage
 constexpr int kStageElems = (BM + BN) * BK;
 constexpr size_t kLdsBytes = 2 * kStageElems * sizeof(bf16_t);
-static_assert(WN == 2 * kIl, "a wave's N sub-tile must hold one gate/up block");
-static_assert(BN == 4 * kIl, "packed gate/up rows are padded to a multiple of 4 * il");
+constexpr int kBandM = 4;               // M-tiles per band of the tile order
+static_assert(WN % 32 == 0 && kIl % 16 == 0, "a wave's N sub-tile holds whole gate/up blocks");
+static_assert(BN % (2 * kIl) == 0, "packed gate/up rows are padded to a multiple of BN");
+static_assert(kRowsPerPass % 8 == 0, "the LDS swizzle key (row & 7) must be pass-invariant");
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a gfx950 CU");
 
-// LDS element offset of (row, 16-byte chunk) in a [rows][BK] tile.
+// LDS element offset of (row, 16-byte chunk) in a [rows][BK] tile; the XOR
+// swizzle spreads the 16 rows of one MFMA fragment read over all banks.
 __device__ inline int lds_off(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
 
+// Linear tile id -> (M-tile, N-tile): bands of kBandM M-tiles, N-tiles
+// outermost inside a band, so 32 consecutive tiles (one XCD's share of a
+// persistent round) touch kBandM A panels and 8 B panels.
+__device__ inline void tile_coords(int t, int m_tiles, int n_tiles, int &mt, int &nt) {
+  const int band_tiles = kBandM * n_tiles;
+  const int band = t / band_tiles;
+  const int r = t - band * band_tiles;
+  const int rows = min(kBandM, m_tiles - band * kBandM);
+  mt = band * kBandM + r % rows;
+  nt = r / rows;
+}
+
+// C[m, n] = sum_k A[row(m), k] * B[n, k] for the rows of each group, with
+// B = packed weights [Np, K] of group g.  The MFMA takes the weight fragment
+// as its first operand, so each lane's accumulator holds 4 consecutive
+// output columns of one row (D[n][m] of v_mfma_f32_16x16x32_bf16).
 template <bool GATEUP>
-__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
+__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
     bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
@@ -91,47 +129,49 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
   const int n_tiles = Np / BN;
-  const int total = tm.prefix[G] * n_tiles;
+  const int m_tiles = tm.prefix[G];
+  const int total = m_tiles * n_tiles;
   const int KT = K / BK;
 
-  // Global-load assignment: rows (tid>>3) + 32*i, 16-byte chunk tid&7.
   const int ld_row = tid >> 3;
   const int ld_chunk = tid & 7;
-  const int st_off = lds_off(ld_row, ld_chunk);  // + 32*i*BK per i (row&7 fixed)
+  const int st_off = lds_off(ld_row, ld_chunk);  // + kRowsPerPass * i * BK per pass i
 
-  // Fragment read offsets (row&7 == lane&7 for every fragment row).
-  const int fr_row = lane & 15;
-  int a_rd[2], b_rd[2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const int ch = ks * 4 + (lane >> 4);
-    a_rd[ks] = lds_off(wm * WM + fr_row, ch);
-    b_rd[ks] = lds_off(wn * WN + fr_row, ch);
-  }
+  const int fr = lane & 15;
+  const int a_rd0 = lds_off(wm * WM + fr, lane >> 4);
+  const int a_rd1 = lds_off(wm * WM + fr, 4 + (lane >> 4));
+  const int b_rd0 = lds_off(wn * WN + fr, lane >> 4);
+  const int b_rd1 = lds_off(wn * WN + fr, 4 + (lane >> 4));
 
-  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    const int mt = tile / n_tiles;
-    const int nt = tile - mt * n_tiles;
+  // Workgroups are dealt round-robin to the 8 XCDs; renumber them so each
+  // XCD runs a contiguous run of the tile order (shared panels in its L2).
+  const int nblk = gridDim.x;
+  const int lb = (nblk % 8 == 0) ? (int)(blockIdx.x % 8) * (nblk / 8) + (int)(blockIdx.x / 8)
+                                 : (int)blockIdx.x;
+
+  for (int t = lb; t < total; t += nblk) {
+    int mt, nt;
+    tile_coords(t, m_tiles, n_tiles, mt, nt);
     const int g = find_group(tm, G, mt);
     const int row0 = offsets[g];
     const int mg = offsets[g + 1] - row0;
     const int m0 = (mt - tm.prefix[g]) * BM;
     const int n0 = nt * BN;
 
-    const bf16_t *a_ptr[8];
-    const bf16_t *b_ptr[8];
-    const bf16_t *Bg = B + (long long)g * b_group_stride;
+    uint32_t a_off[LA];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int lr = m0 + ld_row + 32 * i;
+    for (int i = 0; i < LA; ++i) {
+      int lr = m0 + ld_row + kRowsPerPass * i;
       lr = lr < mg ? lr : mg - 1;
       const int vr = row0 + lr;
       const int src = a_rows ? a_rows[vr] : vr;
-      a_ptr[i] = A + (long long)src * lda + ld_chunk * 8;
-      b_ptr[i] = Bg + (long long)(n0 + ld_row + 32 * i) * K + ld_chunk * 8;
+      a_off[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(ld_chunk * 8);
     }
+    const bf16_t *b_base =
+        B + (long long)g * b_group_stride + (long long)(n0 + ld_row) * K + ld_chunk * 8;
+    const int b_pass = kRowsPerPass * K;
 
     f32x4 acc[MI][NJ];
 #pragma unroll
@@ -139,90 +179,99 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
 #pragma unroll
       for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    uint4 ra[8], rb[8];
-    auto gload = [&](int k0) {
+    u32x4 ra[LA], rb[LB];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        ra[i] = *reinterpret_cast<const uint4 *>(a_ptr[i] + k0);
-        rb[i] = *reinterpret_cast<const uint4 *>(b_ptr[i] + k0);
-      }
-    };
-    auto lstore = [&](int buf) {
-      bf16_t *as = lds + buf * kStageElems;
-      bf16_t *bs = as + BM * BK;
+    for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(A + a_off[i]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        *reinterpret_cast<uint4 *>(as + st_off + 32 * i * BK) = ra[i];
-        *reinterpret_cast<uint4 *>(bs + st_off + 32 * i * BK) = rb[i];
+    for (int i = 0; i < LB; ++i) rb[i] = *reinterpret_cast<const u32x4 *>(b_base + i * b_pass);
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      *reinterpret_cast<u32x4 *>(lds + st_off + kRowsPerPass * i * BK) = ra[i];
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      *reinterpret_cast<u32x4 *>(lds + BM * BK + st_off + kRowsPerPass * i * BK) = rb[i];
+    __syncthreads();
+
+    for (int kt = 0; kt < KT; ++kt) {
+      const bool more = kt + 1 < KT;
+      if (more) {
+        const int k0 = (kt + 1) * BK;
+#pragma unroll
+        for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(A + a_off[i] + k0);
+#pragma unroll
+        for (int i = 0; i < LB; ++i)
+          rb[i] = *reinterpret_cast<const u32x4 *>(b_base + i * b_pass + k0);
       }
-    };
-    auto compute = [&](int buf) {
-      const bf16_t *as = lds + buf * kStageElems;
+      const bf16_t *as = lds + (kt & 1) * kStageElems;
       const bf16_t *bs = as + BM * BK;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        bf16x8 af[MI], bfr[NJ];
+        bf16x8 af[MI], wf[NJ];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
-          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd[ks] + i * 16 * BK);
+          af[i] = *reinterpret_cast<const bf16x8 *>(as + (ks ? a_rd1 : a_rd0) + i * 16 * BK);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-          bfr[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd[ks] + j * 16 * BK);
+          wf[j] = *reinterpret_cast<const bf16x8 *>(bs + (ks ? b_rd1 : b_rd0) + j * 16 * BK);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
       }
-    };
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      const bool more = kt + 1 < KT;
-      if (more) gload((kt + 1) * BK);
-      compute(kt & 1);
-      if (more) lstore((kt + 1) & 1);
+      if (more) {
+        bf16_t *as_n = lds + ((kt + 1) & 1) * kStageElems;
+#pragma unroll
+        for (int i = 0; i < LA; ++i)
+          *reinterpret_cast<u32x4 *>(as_n + st_off + kRowsPerPass * i * BK) = ra[i];
+#pragma unroll
+        for (int i = 0; i < LB; ++i)
+          *reinterpret_cast<u32x4 *>(as_n + BM * BK + st_off + kRowsPerPass * i * BK) = rb[i];
+      }
       __syncthreads();
     }
 
-    // Epilogue.  Lane holds rows 4*(lane>>4)+r, column lane&15 of each block.
-    const int rbase = m0 + wm * WM + 4 * (lane >> 4);
+    // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
+    //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
+    const int lr = m0 + wm * WM + fr;
+    const int cq = 4 * (lane >> 4);
     if (GATEUP) {
-      const int cbase = (n0 / (2 * kIl) + wn) * kIl + (lane & 15);
+      // Packed rows [n0 + wn*WN, +WN) are one [kIl gate | kIl up] block:
+      // gate column c pairs with up column c in j + NJ/2.
+      const int cbase = (n0 + wn * WN) / 2 + cq;
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
+        const int m = lr + 16 * i;
+        if (m < mg) {
+          bf16_t *crow = C + (long long)(row0 + m) * ldc;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int lr = rbase + i * 16 + r;
-          if (lr < mg) {
-            bf16_t *crow = C + (long long)(row0 + lr) * ldc;
+          for (int j = 0; j < NJ / 2; ++j) {
+            const int col = cbase + 16 * j;
+            if (col < n_store) {
+              uint32_t h[4];
 #pragma unroll
-            for (int j = 0; j < NJ / 2; ++j) {
-              const int col = cbase + j * 16;
-              if (col < n_store) {
-                const float gv = acc[i][j][r];
-                const float uv = acc[i][j + NJ / 2][r];
-                crow[col] = f32_to_bf16(silu_ref(gv) * uv);
-              }
+              for (int r = 0; r < 4; ++r)
+                h[r] = f32_to_bf16(silu_ref(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
+              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
             }
           }
         }
       }
     } else {
-      const int cbase = n0 + wn * WN + (lane & 15);
+      const int cbase = n0 + wn * WN + cq;
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
+        const int m = lr + 16 * i;
+        if (m < mg) {
+          bf16_t *crow = C + (long long)(row0 + m) * ldc;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int lr = rbase + i * 16 + r;
-          if (lr < mg) {
-            bf16_t *crow = C + (long long)(row0 + lr) * ldc;
+          for (int j = 0; j < NJ; ++j) {
+            const int col = cbase + 16 * j;
+            if (col < n_store) {
+              uint32_t h[4];
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              const int col = cbase + j * 16;
-              if (col < n_store) crow[col] = f32_to_bf16(acc[i][j][r]);
+              for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(acc[i][j][r]);
+              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
             }
           }
         }
@@ -380,6 +429,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
 }  // namespace fp
 
 size_t il_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)bf::kIl : (size_t)fp::kIl; }
+size_t bn_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)bf::BN : (size_t)fp::BN; }
 
 int check_gemm_shape(size_t d, size_t f, int dtype, const char *who) {
   if (!dtype_ok(dtype)) return fail(PRICHS_ERR_INVALID_ARGUMENT, "%s: bad dtype %d", who, dtype);
@@ -398,13 +448,15 @@ template <> void put<bf16_t>(void *out, size_t i, float v) {
   static_cast<bf16_t *>(out)[i] = f32_to_bf16(v);
 }
 
-// Packed gate/up rows: 2 * roundup(f, 2 * il) (a multiple of the kernel's BN).
-size_t gate_up_np(size_t f, size_t il) { return 2 * roundup(f, 2 * il); }
+// Packed gate/up rows: the [il gate | il up] blocks covering f columns,
+// padded with zero rows to a multiple of the kernel's N tile.
+size_t gate_up_np(size_t f, int dtype) { return roundup(2 * roundup(f, il_of(dtype)), bn_of(dtype)); }
 
 template <typename T>
-void pack_gate_up_impl(const float *gate, const float *up, size_t d, size_t f, size_t il,
+void pack_gate_up_impl(const float *gate, const float *up, size_t d, size_t f, int dtype,
                        void *out) {
-  const size_t np = gate_up_np(f, il);
+  const size_t il = il_of(dtype);
+  const size_t np = gate_up_np(f, dtype);
   for (size_t p = 0; p < np; ++p) {
     const size_t b = p / (2 * il), q = p % (2 * il);
     const float *src = q < il ? gate : up;
@@ -462,7 +514,7 @@ extern "C" size_t prichs_gate_up_interleave(int dtype) { return dtype_ok(dtype) 
 
 extern "C" size_t prichs_packed_gate_up_elems(size_t d, size_t f, int dtype) {
   if (!dtype_ok(dtype)) return 0;
-  return gate_up_np(f, il_of(dtype)) * d;
+  return gate_up_np(f, dtype) * d;
 }
 
 extern "C" size_t prichs_packed_down_elems(size_t d, size_t f, int dtype) {
@@ -475,9 +527,9 @@ extern "C" int prichs_pack_gate_up(const float *gate, const float *up, size_t d,
   if (int rc = check_gemm_shape(d, f, dtype, "pack_gate_up")) return rc;
   PRICHS_REQUIRE(gate && up && packed_out, "pack_gate_up: null pointer argument");
   if (dtype == PRICHS_DTYPE_BF16)
-    pack_gate_up_impl<bf16_t>(gate, up, d, f, il_of(dtype), packed_out);
+    pack_gate_up_impl<bf16_t>(gate, up, d, f, dtype, packed_out);
   else
-    pack_gate_up_impl<float>(gate, up, d, f, il_of(dtype), packed_out);
+    pack_gate_up_impl<float>(gate, up, d, f, dtype, packed_out);
   return PRICHS_OK;
 }
 
@@ -501,7 +553,7 @@ extern "C" int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_t
                  kMaxGroups);
   PRICHS_REQUIRE(x && row_token && offsets && w_packed && act, "gate_up: null pointer argument");
   PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX, "gate_up: max_rows too large");
-  const size_t np = gate_up_np(f, il_of(dtype));
+  const size_t np = gate_up_np(f, dtype);
   return launch_grouped(true, x, row_token, (int)d, w_packed, (long long)(np * d), (int)np,
                         (int)d, act, (int)f, (int)f, offsets, (int)G, max_rows, dtype,
                         as_stream(stream));

@@ -134,7 +134,9 @@ def test_pack_gate_up_layout(lib, dtype):
     il = lib.prichs_gate_up_interleave(dtype)
     packed = ops.pack_gate_up(gate, up, dtype)
     np_ = packed.shape[0]
-    assert np_ == 2 * (-(-f // (2 * il)) * (2 * il))
+    # whole [il gate | il up] blocks, zero-padded to the kernel's N tile
+    assert np_ % (2 * il) == 0 and np_ >= 2 * (-(-f // il) * il)
+    assert np_ % (256 if dtype == L.DTYPE_BF16 else 128) == 0
     vals = synth.from_bf16_bits(packed) if dtype == L.DTYPE_BF16 else packed
     rnd = synth.round_bf16 if dtype == L.DTYPE_BF16 else (lambda a: a)
     for p in range(np_):
