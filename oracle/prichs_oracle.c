@@ -33,9 +33,6 @@
  *   orc_precompute_rope_cache / orc_rope_forward_in_place
  *                            cos=1/sin=0 identity (engine.rs:2970-2972), norm
  *                            preservation, float64 closed form.
- *   orc_attention_forward / orc_block_forward
- *                            float64 softmax attention recomputation, causal
- *                            mask invariants.
  */
 #include <math.h>
 #include <stddef.h>
