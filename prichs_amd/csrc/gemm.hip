@@ -40,6 +40,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kMaxGroups = PRICHS_MAX_EXPERTS + 1;
 constexpr int kPadRowsDown = 256;  // packed down weights: rows padded to this
 
+// SwiGLU of the bf16 epilogue (silu_ref is the reference formula with the
+// full-precision expf and division; silu_fast uses v_exp_f32 / v_rcp_f32).
+#ifndef PRICHS_BF16_SILU
+#define PRICHS_BF16_SILU silu_fast
+#endif
 #ifndef PRICHS_BF16_WGM
 #define PRICHS_BF16_WGM 2
 #endif
@@ -251,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
               uint32_t h[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                h[r] = f32_to_bf16(silu_ref(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
+                h[r] = f32_to_bf16(PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
               *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
             }
           }
@@ -280,6 +285,426 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
   }
 }
 }  // namespace bf
+
+// ------------------------------------------------------------------------
+// bf16 kernel, direct-to-LDS pipeline
+// ------------------------------------------------------------------------
+// Same tile, wave grid, operand order and epilogue as bf::grouped_gemm_kernel;
+// the staging differs: global_load_lds_dwordx4 writes each lane's 16 bytes
+// straight into LDS (no staging registers, no ds_write), K advances 32 at a
+// time through a ring of 4 LDS stages, and loads run 3 stages ahead.  One
+// workgroup barrier per stage; waits are explicit vmcnt counts.
+namespace bf3 {
+constexpr int BM = 256, BN = 256, BK = 32, kStages = 4;
+constexpr int WGM = 2, WGN = 4;
+constexpr int kThreads = 64 * WGM * WGN;
+constexpr int kWaves = WGM * WGN;
+constexpr int WM = BM / WGM, WN = BN / WGN;
+constexpr int MI = WM / 16, NJ = WN / 16;
+constexpr int kIl = WN / 2;
+constexpr int kRowsPerInst = 16;  // one wave instruction fills 1 KiB = 16 rows of 64 bytes
+constexpr int kInstA = BM / kRowsPerInst / kWaves;
+constexpr int kInstB = BN / kRowsPerInst / kWaves;
+constexpr int kInstPerStage = kInstA + kInstB;
+constexpr int kStageElems = (BM + BN) * BK;
+constexpr size_t kLdsBytes = (size_t)kStages * kStageElems * sizeof(bf16_t);
+static_assert(kIl == bf::kIl, "both bf16 kernels consume the same packed gate/up layout");
+static_assert(BN == bf::BN && BM == bf::BM, "tile shape shared with the register-staged kernel");
+static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
+              "the DMA instructions of one stage cover the A and B tiles exactly");
+static_assert(kInstPerStage * 2 <= 63, "vmcnt immediates");
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a gfx950 CU");
+
+// 64-byte rows of 4 16-byte chunks.  The key makes the 16 rows of one
+// fragment read hit distinct banks whether the LDS serves 8 or 16 lanes of a
+// ds_read_b128 per cycle.
+__device__ inline int swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+__device__ inline int lds_off(int row, int chunk) { return row * BK + ((chunk ^ swz(row)) << 3); }
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] at [15:14]).
+#define PRICHS_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
+
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <bool GATEUP>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
+    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
+    const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
+    bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
+    int G) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  __shared__ TileMap tm;
+  build_tile_map(tm, offsets, G, BM);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
+  const int n_tiles = Np / BN;
+  const int m_tiles = tm.prefix[G];
+  const int total = m_tiles * n_tiles;
+  const int KT = K / BK;
+
+  // DMA lane mapping: instruction i of wave w fills rows r0 = 16 (w kInst + i)
+  // .. r0 + 15; lane l lands at r0 + l/4, physical chunk l%4, so it loads the
+  // logical chunk (l%4) ^ swz(row).
+  const int dma_row = lane >> 2;
+  const int dma_chunk = (lane & 3) ^ swz(dma_row);  // swz depends on row % 8 only
+
+  const int fr = lane & 15;
+  const int a_rd = lds_off(wm * WM + fr, lane >> 4);
+  const int b_rd = lds_off(wn * WN + fr, lane >> 4);
+
+  const int nblk = gridDim.x;
+  const int lb = (nblk % 8 == 0) ? (int)(blockIdx.x % 8) * (nblk / 8) + (int)(blockIdx.x / 8)
+                                 : (int)blockIdx.x;
+
+  for (int t = lb; t < total; t += nblk) {
+    int mt, nt;
+    bf::tile_coords(t, m_tiles, n_tiles, mt, nt);
+    const int g = find_group(tm, G, mt);
+    const int row0 = offsets[g];
+    const int mg = offsets[g + 1] - row0;
+    const int m0 = (mt - tm.prefix[g]) * BM;
+    const int n0 = nt * BN;
+
+    uint32_t a_goff[kInstA], b_goff[kInstB];
+#pragma unroll
+    for (int i = 0; i < kInstA; ++i) {
+      int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
+      lr = lr < mg ? lr : mg - 1;
+      const int vr = row0 + lr;
+      const int src = a_rows ? a_rows[vr] : vr;
+      a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < kInstB; ++i) {
+      const int nr = n0 + (wave * kInstB + i) * kRowsPerInst + dma_row;
+      b_goff[i] = (uint32_t)nr * (uint32_t)K + (uint32_t)(dma_chunk * 8);
+    }
+    const bf16_t *Bg = B + (long long)g * b_group_stride;
+
+    f32x4 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // The previous tile's epilogue stores drain and every wave is past its
+    // last LDS read before the ring is refilled.
+    PRICHS_WAIT_VMCNT(0);
+    lds_barrier();
+
+#define PRICHS_ISSUE_STAGE(kt_)                                                       \
+  do {                                                                               \
+    const int k0_ = (kt_) * BK;                                                      \
+    bf16_t *st_ = lds + ((kt_) & (kStages - 1)) * kStageElems;                       \
+    _Pragma("unroll") for (int i_ = 0; i_ < kInstA; ++i_)                            \
+        __builtin_amdgcn_global_load_lds(A + a_goff[i_] + k0_,                       \
+                                         st_ + (wave * kInstA + i_) * kRowsPerInst * BK, \
+                                         16, 0, 0);                                  \
+    _Pragma("unroll") for (int i_ = 0; i_ < kInstB; ++i_)                            \
+        __builtin_amdgcn_global_load_lds(Bg + b_goff[i_] + k0_,                      \
+                                         st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK, \
+                                         16, 0, 0);                                  \
+  } while (0)
+
+    PRICHS_ISSUE_STAGE(0);
+    if (KT > 1) PRICHS_ISSUE_STAGE(1);
+    if (KT > 2) PRICHS_ISSUE_STAGE(2);
+
+    for (int kt = 0; kt < KT; ++kt) {
+      // Stages issued so far: min(kt + 3, KT); those after kt may stay in flight.
+      const int ahead = min(2, KT - 1 - kt);
+      if (ahead == 2)
+        PRICHS_WAIT_VMCNT(2 * kInstPerStage);
+      else if (ahead == 1)
+        PRICHS_WAIT_VMCNT(kInstPerStage);
+      else
+        PRICHS_WAIT_VMCNT(0);
+      lds_barrier();
+      // The slot refilled here was last read in iteration kt - 1, before the barrier.
+      if (kt + 3 < KT) PRICHS_ISSUE_STAGE(kt + 3);
+
+      const bf16_t *as = lds + (kt & (kStages - 1)) * kStageElems;
+      const bf16_t *bs = as + BM * BK;
+      bf16x8 af[MI], wf[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) wf[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+    }
+#undef PRICHS_ISSUE_STAGE
+
+    const int lr = m0 + wm * WM + fr;
+    const int cq = 4 * (lane >> 4);
+    if (GATEUP) {
+      const int cbase = (n0 + wn * WN) / 2 + cq;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = lr + 16 * i;
+        if (m < mg) {
+          bf16_t *crow = C + (long long)(row0 + m) * ldc;
+#pragma unroll
+          for (int j = 0; j < NJ / 2; ++j) {
+            const int col = cbase + 16 * j;
+            if (col < n_store) {
+              uint32_t h[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                h[r] = f32_to_bf16(PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
+              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            }
+          }
+        }
+      }
+    } else {
+      const int cbase = n0 + wn * WN + cq;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = lr + 16 * i;
+        if (m < mg) {
+          bf16_t *crow = C + (long long)(row0 + m) * ldc;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const int col = cbase + 16 * j;
+            if (col < n_store) {
+              uint32_t h[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(acc[i][j][r]);
+              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            }
+          }
+        }
+      }
+    }
+  }
+}
+}  // namespace bf3
+
+// ------------------------------------------------------------------------
+// bf16 kernel, direct-to-LDS pipeline with fragment reads hidden under MFMAs
+// ------------------------------------------------------------------------
+// Same LDS ring, DMA mapping, tile order and epilogue as bf3.  Each stage's
+// MFMAs are split in two halves around the workgroup barrier: after the
+// first half frees the A fragments of rows 0..3, the wave waits for the next
+// stage, passes the barrier, issues that stage's fragment reads (into the
+// freed registers) and the DMA of stage kt + 4, and only then runs the
+// second half, so the LDS read latency and bandwidth of one stage overlap the
+// MFMAs of the previous one.
+namespace bf4 {
+using namespace bf3;  // tile shape, swizzle, DMA layout
+static_assert(MI % 2 == 0, "two halves of A fragments");
+
+template <bool GATEUP>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
+    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
+    const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
+    bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
+    int G) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  __shared__ TileMap tm;
+  build_tile_map(tm, offsets, G, BM);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
+  const int n_tiles = Np / BN;
+  const int m_tiles = tm.prefix[G];
+  const int total = m_tiles * n_tiles;
+  const int KT = K / BK;
+
+  const int dma_row = lane >> 2;
+  const int dma_chunk = (lane & 3) ^ swz(dma_row);
+  const int fr = lane & 15;
+  const int a_rd = lds_off(wm * WM + fr, lane >> 4);
+  const int b_rd = lds_off(wn * WN + fr, lane >> 4);
+
+  const int nblk = gridDim.x;
+  const int lb = (nblk % 8 == 0) ? (int)(blockIdx.x % 8) * (nblk / 8) + (int)(blockIdx.x / 8)
+                                 : (int)blockIdx.x;
+
+  for (int t = lb; t < total; t += nblk) {
+    int mt, nt;
+    bf::tile_coords(t, m_tiles, n_tiles, mt, nt);
+    const int g = find_group(tm, G, mt);
+    const int row0 = offsets[g];
+    const int mg = offsets[g + 1] - row0;
+    const int m0 = (mt - tm.prefix[g]) * BM;
+    const int n0 = nt * BN;
+
+    uint32_t a_goff[kInstA], b_goff[kInstB];
+#pragma unroll
+    for (int i = 0; i < kInstA; ++i) {
+      int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
+      lr = lr < mg ? lr : mg - 1;
+      const int vr = row0 + lr;
+      const int src = a_rows ? a_rows[vr] : vr;
+      a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < kInstB; ++i) {
+      const int nr = n0 + (wave * kInstB + i) * kRowsPerInst + dma_row;
+      b_goff[i] = (uint32_t)nr * (uint32_t)K + (uint32_t)(dma_chunk * 8);
+    }
+    const bf16_t *Bg = B + (long long)g * b_group_stride;
+
+    f32x4 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    PRICHS_WAIT_VMCNT(0);
+    lds_barrier();
+
+#define PRICHS_ISSUE_STAGE(kt_)                                                       \
+  do {                                                                               \
+    const int k0_ = (kt_) * BK;                                                      \
+    bf16_t *st_ = lds + ((kt_) & (kStages - 1)) * kStageElems;                       \
+    _Pragma("unroll") for (int i_ = 0; i_ < kInstA; ++i_)                            \
+        __builtin_amdgcn_global_load_lds(A + a_goff[i_] + k0_,                       \
+                                         st_ + (wave * kInstA + i_) * kRowsPerInst * BK, \
+                                         16, 0, 0);                                  \
+    _Pragma("unroll") for (int i_ = 0; i_ < kInstB; ++i_)                            \
+        __builtin_amdgcn_global_load_lds(Bg + b_goff[i_] + k0_,                      \
+                                         st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK, \
+                                         16, 0, 0);                                  \
+  } while (0)
+
+    // Prologue: stages 0..3 in flight; stage 0 lands and is read.
+    PRICHS_ISSUE_STAGE(0);
+    if (KT > 1) PRICHS_ISSUE_STAGE(1);
+    if (KT > 2) PRICHS_ISSUE_STAGE(2);
+    if (KT > 3) PRICHS_ISSUE_STAGE(3);
+    {
+      const int ahead = min(3, KT - 1);  // stages issued after stage 0
+      if (ahead == 3)
+        PRICHS_WAIT_VMCNT(3 * kInstPerStage);
+      else if (ahead == 2)
+        PRICHS_WAIT_VMCNT(2 * kInstPerStage);
+      else if (ahead == 1)
+        PRICHS_WAIT_VMCNT(kInstPerStage);
+      else
+        PRICHS_WAIT_VMCNT(0);
+    }
+    lds_barrier();
+
+    bf16x8 af[MI], wf[NJ], wn_next[NJ];
+    {
+      const bf16_t *as = lds;
+      const bf16_t *bs = as + BM * BK;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) wf[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
+    }
+
+    for (int kt = 0; kt < KT; ++kt) {
+      // First half: A rows 0 .. MI/2-1 of stage kt.
+#pragma unroll
+      for (int i = 0; i < MI / 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+
+      const bool more = kt + 1 < KT;
+      if (more) {
+        // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
+        const int ahead = min(2, KT - 2 - kt);
+        if (ahead == 2)
+          PRICHS_WAIT_VMCNT(2 * kInstPerStage);
+        else if (ahead == 1)
+          PRICHS_WAIT_VMCNT(kInstPerStage);
+        else
+          PRICHS_WAIT_VMCNT(0);
+        lds_barrier();
+        // Every wave has read stage kt (in the previous iteration), so its
+        // slot takes stage kt + 4.
+        if (kt + 4 < KT) PRICHS_ISSUE_STAGE(kt + 4);
+        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
+        const bf16_t *bs = as + BM * BK;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          wn_next[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
+#pragma unroll
+        for (int i = 0; i < MI / 2; ++i)
+          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
+      }
+      // Second half: A rows MI/2 .. MI-1 of stage kt.
+#pragma unroll
+      for (int i = MI / 2; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+      if (more) {
+        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
+#pragma unroll
+        for (int i = MI / 2; i < MI; ++i)
+          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) wf[j] = wn_next[j];
+      }
+    }
+#undef PRICHS_ISSUE_STAGE
+
+    const int lr = m0 + wm * WM + fr;
+    const int cq = 4 * (lane >> 4);
+    if (GATEUP) {
+      const int cbase = (n0 + wn * WN) / 2 + cq;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = lr + 16 * i;
+        if (m < mg) {
+          bf16_t *crow = C + (long long)(row0 + m) * ldc;
+#pragma unroll
+          for (int j = 0; j < NJ / 2; ++j) {
+            const int col = cbase + 16 * j;
+            if (col < n_store) {
+              uint32_t h[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                h[r] = f32_to_bf16(PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
+              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            }
+          }
+        }
+      }
+    } else {
+      const int cbase = n0 + wn * WN + cq;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = lr + 16 * i;
+        if (m < mg) {
+          bf16_t *crow = C + (long long)(row0 + m) * ldc;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const int col = cbase + 16 * j;
+            if (col < n_store) {
+              uint32_t h[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(acc[i][j][r]);
+              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            }
+          }
+        }
+      }
+    }
+  }
+}
+}  // namespace bf4
 
 // ------------------------------------------------------------------------
 // f32 kernel (fp32-checked mode)
@@ -471,24 +896,35 @@ template <typename T> void pack_down_impl(const float *down, size_t d, size_t f,
     for (size_t k = 0; k < f; ++k) put<T>(out, n * f + k, n < d ? down[k * d + n] : 0.0f);
 }
 
+#ifndef PRICHS_GEMM_VERSION
+#define PRICHS_GEMM_VERSION 4
+#endif
+#if PRICHS_GEMM_VERSION == 4
+namespace BFK = bf4;
+#elif PRICHS_GEMM_VERSION == 3
+namespace BFK = bf3;
+#else
+namespace BFK = bf;
+#endif
+
 int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, const void *B,
                    long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
                    const int32_t *offsets, int G, size_t max_rows, int dtype, hipStream_t s) {
   const int cus = device_cu_count();
   if (cus <= 0) return fail(PRICHS_ERR_HIP, "grouped gemm: cannot query the device");
   if (dtype == PRICHS_DTYPE_BF16) {
-    const size_t ub = (max_rows / bf::BM + G) * (size_t)(Np / bf::BN);
+    const size_t ub = (max_rows / BFK::BM + G) * (size_t)(Np / BFK::BN);
     const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus));
-    auto kern = gateup ? bf::grouped_gemm_kernel<true> : bf::grouped_gemm_kernel<false>;
+    auto kern = gateup ? BFK::grouped_gemm_kernel<true> : BFK::grouped_gemm_kernel<false>;
     static bool attr_set[2] = {false, false};
     if (!attr_set[gateup]) {
       PRICHS_HIP_TRY(hipFuncSetAttribute((const void *)kern,
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)bf::kLdsBytes),
+                                         (int)BFK::kLdsBytes),
                      "grouped gemm: set LDS size");
       attr_set[gateup] = true;
     }
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(bf::kThreads), bf::kLdsBytes, s,
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(BFK::kThreads), BFK::kLdsBytes, s,
                        static_cast<const bf16_t *>(A), a_rows, lda,
                        static_cast<const bf16_t *>(B), b_stride, Np, K,
                        static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G);
