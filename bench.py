@@ -144,7 +144,7 @@ def main():
         "config": {"workload": WORKLOADS[args.config], "tokens": T, "d_model": d, "d_ffn": f,
                    "routed_experts": E, "shared_experts": S, "top_k": k},
         "roofline": {
-            "kernel": "grouped gate/up GEMM + fused SwiGLU (bf::grouped_gemm_kernel<true>)",
+            "kernel": "grouped gate/up GEMM + fused SwiGLU (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, true>)",
             "bound": "mfma",
             "achieved": gu_tflops,
             "peak": peak,

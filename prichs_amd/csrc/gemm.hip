@@ -15,10 +15,12 @@
 //             weight interleave), so SwiGLU is applied in the epilogue.
 //   down:     y[r] = act[r] @ Wd  (moe.rs:170, 106).
 //
-// bf16 kernel: 256x256x64 tiles, 8 wave64s in a 2x4 grid each owning a
-// 128x64 sub-tile of v_mfma_f32_16x16x32_bf16 accumulators (fp32, two waves
-// per SIMD), A and B staged through double-buffered LDS with an XOR swizzle
-// of 16-byte chunks, persistent workgroups walking an XCD-aware tile order.
+// bf16 kernel: 256x256 output tiles per workgroup on v_mfma_f32_16x16x32_bf16
+// (fp32 accumulation).  K advances 32 at a time through a ring of 4 LDS
+// stages that global_load_lds_dwordx4 fills directly (no staging registers),
+// 3 stages ahead of the MFMAs; each stage's MFMAs are split in two halves
+// around the workgroup barrier so the next stage's fragment reads overlap
+// MFMA work.  Workgroups are persistent and walk an XCD-aware tile order.
 // f32 kernel: 128x128x16 tiles on v_mfma_f32_16x16x4_f32 (the fp32-checked
 // mode; accumulates in fp32 like the reference CPU path).
 #include <algorithm>
@@ -32,31 +34,37 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-// Native vector types (not HIP's struct-based uint4/uint2), so staged
-// fragments stay in registers.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Native vector types (not HIP's struct-based uint4/uint2), so values stay
+// in registers.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxGroups = PRICHS_MAX_EXPERTS + 1;
-constexpr int kPadRowsDown = 256;  // packed down weights: rows padded to this
+constexpr int kPadRowsDown = 256;    // packed down weights: rows padded to this
+constexpr int kBf16KMultiple = 64;   // bf16 kernels need d and f to be multiples of this
 
 // SwiGLU of the bf16 epilogue (silu_ref is the reference formula with the
 // full-precision expf and division; silu_fast uses v_exp_f32 / v_rcp_f32).
 #ifndef PRICHS_BF16_SILU
 #define PRICHS_BF16_SILU silu_fast
 #endif
+// Wave grid of the bf16 kernel (WGM x WGN wave64s per 256x256 tile).
 #ifndef PRICHS_BF16_WGM
 #define PRICHS_BF16_WGM 2
 #endif
 #ifndef PRICHS_BF16_WGN
 #define PRICHS_BF16_WGN 4
 #endif
+// M-tiles per band of the tile order.
+#ifndef PRICHS_BAND_M
+#define PRICHS_BAND_M 4
+#endif
 
 // ------------------------------------------------------------------------
-// Tile scheduler shared by both kernels.
+// Tile scheduler shared by the kernels.
 // ------------------------------------------------------------------------
 struct TileMap {
   int prefix[kMaxGroups + 1];  // first global M-tile of each group
+  int offs[kMaxGroups + 1];    // offsets[] of the launch (row range of each group)
 };
 
 __device__ inline void build_tile_map(TileMap &tm, const int32_t *offsets, int G, int BM) {
@@ -64,69 +72,145 @@ __device__ inline void build_tile_map(TileMap &tm, const int32_t *offsets, int G
     int run = 0;
     for (int g = 0; g < G; ++g) {
       tm.prefix[g] = run;
+      tm.offs[g] = offsets[g];
       const int mg = offsets[g + 1] - offsets[g];
       run += mg > 0 ? (mg + BM - 1) / BM : 0;
     }
     tm.prefix[G] = run;
+    tm.offs[G] = offsets[G];
   }
   __syncthreads();
 }
 
+// Group of global M-tile mt (empty groups own no tiles and are skipped).
 __device__ inline int find_group(const TileMap &tm, int G, int mt) {
   int g = 0;
   while (g + 1 < G && tm.prefix[g + 1] <= mt) ++g;
   return g;
 }
 
+// Linear tile id -> (M-tile, N-tile): bands of PRICHS_BAND_M M-tiles with the
+// N-tiles outermost inside a band, so a run of consecutive tiles shares a few
+// A panels and B panels.
+__device__ inline void tile_coords(int t, int m_tiles, int n_tiles, int &mt, int &nt) {
+  const int band_tiles = PRICHS_BAND_M * n_tiles;
+  const int band = t / band_tiles;
+  const int r = t - band * band_tiles;
+  const int rows = min(PRICHS_BAND_M, m_tiles - band * PRICHS_BAND_M);
+  mt = band * PRICHS_BAND_M + r % rows;
+  nt = r / rows;
+}
+
+// Workgroups are dealt round-robin to the 8 XCDs; renumbering them so each XCD
+// runs a contiguous run of the tile order keeps shared panels in its L2.
+__device__ inline int xcd_block_id() {
+  const int nblk = gridDim.x;
+  return (nblk % 8 == 0) ? (int)(blockIdx.x % 8) * (nblk / 8) + (int)(blockIdx.x / 8)
+                         : (int)blockIdx.x;
+}
+
 // ------------------------------------------------------------------------
 // bf16 kernel
 // ------------------------------------------------------------------------
-namespace bf {
-// Tile shape of one workgroup: BM x BN outputs, K consumed BK at a time.
-// WGM x WGN wave64s; a wave owns a WM x WN sub-tile of 16x16 MFMA blocks.
-constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int WGM = PRICHS_BF16_WGM, WGN = PRICHS_BF16_WGN;
-constexpr int kThreads = 64 * WGM * WGN;
-constexpr int WM = BM / WGM, WN = BN / WGN;
-constexpr int MI = WM / 16, NJ = WN / 16;
-constexpr int kIl = WN / 2;             // gate/up interleave: packed blocks [kIl gate | kIl up]
-constexpr int kRowsPerPass = kThreads / 8;  // 8 threads load one 128-byte row slice
-constexpr int LA = BM / kRowsPerPass;   // A chunks per thread per stage
-constexpr int LB = BN / kRowsPerPass;   // B chunks per thread per stage
-constexpr int kStageElems = (BM + BN) * BK;
-constexpr size_t kLdsBytes = 2 * kStageElems * sizeof(bf16_t);
-constexpr int kBandM = 4;               // M-tiles per band of the tile order
-static_assert(WN % 32 == 0 && kIl % 16 == 0, "a wave's N sub-tile holds whole gate/up blocks");
-static_assert(BN % (2 * kIl) == 0, "packed gate/up rows are padded to a multiple of BN");
-static_assert(kRowsPerPass % 8 == 0, "the LDS swizzle key (row & 7) must be pass-invariant");
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a gfx950 CU");
+// LDS stage layout: [rows][32] bf16, 64-byte rows of 4 16-byte chunks.  The
+// XOR key makes the 16 rows of one fragment read hit distinct banks whether
+// the LDS serves 8 or 16 lanes of a ds_read_b128 per cycle.
+constexpr int kBK = 32;
+__device__ inline int swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+__device__ inline int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ swz(row)) << 3); }
 
-// LDS element offset of (row, 16-byte chunk) in a [rows][BK] tile; the XOR
-// swizzle spreads the 16 rows of one MFMA fragment read over all banks.
-__device__ inline int lds_off(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] at [15:14]).
+#define PRICHS_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
 
-// Linear tile id -> (M-tile, N-tile): bands of kBandM M-tiles, N-tiles
-// outermost inside a band, so 32 consecutive tiles (one XCD's share of a
-// persistent round) touch kBandM A panels and 8 B panels.
-__device__ inline void tile_coords(int t, int m_tiles, int n_tiles, int &mt, int &nt) {
-  const int band_tiles = kBandM * n_tiles;
-  const int band = t / band_tiles;
-  const int r = t - band * band_tiles;
-  const int rows = min(kBandM, m_tiles - band * kBandM);
-  mt = band * kBandM + r % rows;
-  nt = r / rows;
+// Non-template wrappers of the target builtins: a builtin call whose
+// arguments depend on a kernel template parameter fails (silently) in the
+// host compilation pass, which then emits no host stub for the kernel.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+#define PRICHS_VMCNT_CASE(v) \
+  case v:                    \
+    PRICHS_WAIT_VMCNT(v);    \
+    break;
+    PRICHS_VMCNT_CASE(0) PRICHS_VMCNT_CASE(1) PRICHS_VMCNT_CASE(2) PRICHS_VMCNT_CASE(3)
+    PRICHS_VMCNT_CASE(4) PRICHS_VMCNT_CASE(5) PRICHS_VMCNT_CASE(6) PRICHS_VMCNT_CASE(7)
+    PRICHS_VMCNT_CASE(8) PRICHS_VMCNT_CASE(9) PRICHS_VMCNT_CASE(10) PRICHS_VMCNT_CASE(11)
+    PRICHS_VMCNT_CASE(12) PRICHS_VMCNT_CASE(15) PRICHS_VMCNT_CASE(16) PRICHS_VMCNT_CASE(18)
+    PRICHS_VMCNT_CASE(20) PRICHS_VMCNT_CASE(24)
+#undef PRICHS_VMCNT_CASE
+    default:
+      PRICHS_WAIT_VMCNT(0);  // any other count: wait for everything (always safe)
+      break;
+  }
 }
+__device__ __forceinline__ void dma_16b(const bf16_t *src, bf16_t *lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, lds_dst, 16, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 w, bf16x8 a, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, a, c, 0, 0, 0);
+}
+
+// Workgroup barrier without a memory fence: LDS-DMA completion is tracked by
+// the explicit vmcnt waits, and a fence would force vmcnt(0).
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = kBK, kStages = 4;
+  static constexpr int WGM = WGM_, WGN = WGN_;
+  static constexpr int kWaves = WGM * WGN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int MI = WM / 16, NJ = WN / 16;
+  static constexpr int kIl = WN / 2;         // gate/up interleave: packed blocks [kIl gate | kIl up]
+  static constexpr int kRowsPerInst = 16;    // one wave instruction fills 1 KiB = 16 rows of 64 B
+  static constexpr int kInstA = BM / kRowsPerInst / kWaves;
+  static constexpr int kInstB = BN / kRowsPerInst / kWaves;
+  static constexpr int kInstPerStage = kInstA + kInstB;
+  static constexpr int kStageElems = (BM + BN) * BK;
+  static constexpr size_t kLdsBytes = (size_t)kStages * kStageElems * sizeof(bf16_t);
+  static_assert(WN % 32 == 0 && MI % 2 == 0, "whole gate/up blocks and two A halves per wave");
+  static_assert(BN % (2 * kIl) == 0, "packed gate/up rows are padded to a multiple of BN");
+  static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
+                "the DMA instructions of one stage cover the A and B tiles exactly");
+  static_assert(3 * kInstPerStage <= 63, "vmcnt immediates");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a gfx950 CU");
+};
+// gate/up: 256x256 tiles; down: PRICHS_DOWN_BM x 256 tiles (smaller M tiles
+// spread the down GEMM's fewer tiles more evenly over the CUs).
+#ifndef PRICHS_DOWN_BM
+#define PRICHS_DOWN_BM 256
+#endif
+using Bf16 = Bf16Cfg<256, 256, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
+using Bf16Down = Bf16Cfg<PRICHS_DOWN_BM, 256, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
+static_assert(Bf16::BN == Bf16Down::BN, "both bf16 GEMMs pad packed weights to the same N tile");
 
 // C[m, n] = sum_k A[row(m), k] * B[n, k] for the rows of each group, with
 // B = packed weights [Np, K] of group g.  The MFMA takes the weight fragment
 // as its first operand, so each lane's accumulator holds 4 consecutive
-// output columns of one row (D[n][m] of v_mfma_f32_16x16x32_bf16).
-template <bool GATEUP>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
+// output columns of one row (D[n][m] of v_mfma_f32_16x16x32_bf16), stored as
+// one 8-byte write.
+// Both bf16 configurations run the same number of waves, so the launch bound
+// is a constant (a bound that depends on a template parameter fails to
+// substitute in the host pass).
+constexpr int kBf16Threads = 64 * PRICHS_BF16_WGM * PRICHS_BF16_WGN;
+
+template <class Cf, bool GATEUP>
+__global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
     bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
     int G) {
+  constexpr int BM = Cf::BM, BN = Cf::BN, BK = Cf::BK, kStages = Cf::kStages;
+  constexpr int WGN = Cf::WGN, WM = Cf::WM, WN = Cf::WN, MI = Cf::MI, NJ = Cf::NJ;
+  constexpr int kRowsPerInst = Cf::kRowsPerInst, kInstA = Cf::kInstA, kInstB = Cf::kInstB;
+  constexpr int kInstPerStage = Cf::kInstPerStage, kStageElems = Cf::kStageElems;
+  static_assert(Cf::kThreads == kBf16Threads, "launch bound of the bf16 kernels");
+
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   __shared__ TileMap tm;
   build_tile_map(tm, offsets, G, BM);
@@ -140,43 +224,42 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
   const int total = m_tiles * n_tiles;
   const int KT = K / BK;
 
-  const int ld_row = tid >> 3;
-  const int ld_chunk = tid & 7;
-  const int st_off = lds_off(ld_row, ld_chunk);  // + kRowsPerPass * i * BK per pass i
+  // DMA lane mapping: instruction i of wave w fills rows r0 = 16 (w kInst + i)
+  // .. r0 + 15; lane l lands at row r0 + l/4, physical chunk l%4, so it loads
+  // the logical chunk (l%4) ^ swz(row) (swz depends on row % 8 only).
+  const int dma_row = lane >> 2;
+  const int dma_chunk = (lane & 3) ^ swz(dma_row);
 
+  // Fragment reads: lane l reads row l%16 of a 16-row block, chunk l/16.
   const int fr = lane & 15;
-  const int a_rd0 = lds_off(wm * WM + fr, lane >> 4);
-  const int a_rd1 = lds_off(wm * WM + fr, 4 + (lane >> 4));
-  const int b_rd0 = lds_off(wn * WN + fr, lane >> 4);
-  const int b_rd1 = lds_off(wn * WN + fr, 4 + (lane >> 4));
+  const int a_rd = lds_off(wm * WM + fr, lane >> 4);
+  const int b_rd = lds_off(wn * WN + fr, lane >> 4);
 
-  // Workgroups are dealt round-robin to the 8 XCDs; renumber them so each
-  // XCD runs a contiguous run of the tile order (shared panels in its L2).
   const int nblk = gridDim.x;
-  const int lb = (nblk % 8 == 0) ? (int)(blockIdx.x % 8) * (nblk / 8) + (int)(blockIdx.x / 8)
-                                 : (int)blockIdx.x;
-
-  for (int t = lb; t < total; t += nblk) {
+  for (int t = xcd_block_id(); t < total; t += nblk) {
     int mt, nt;
     tile_coords(t, m_tiles, n_tiles, mt, nt);
     const int g = find_group(tm, G, mt);
-    const int row0 = offsets[g];
-    const int mg = offsets[g + 1] - row0;
+    const int row0 = tm.offs[g];
+    const int mg = tm.offs[g + 1] - row0;
     const int m0 = (mt - tm.prefix[g]) * BM;
     const int n0 = nt * BN;
 
-    uint32_t a_off[LA];
+    uint32_t a_goff[kInstA], b_goff[kInstB];
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      int lr = m0 + ld_row + kRowsPerPass * i;
-      lr = lr < mg ? lr : mg - 1;
+    for (int i = 0; i < kInstA; ++i) {
+      int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
+      lr = lr < mg ? lr : mg - 1;  // rows past the group repeat its last row
       const int vr = row0 + lr;
       const int src = a_rows ? a_rows[vr] : vr;
-      a_off[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(ld_chunk * 8);
+      a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
     }
-    const bf16_t *b_base =
-        B + (long long)g * b_group_stride + (long long)(n0 + ld_row) * K + ld_chunk * 8;
-    const int b_pass = kRowsPerPass * K;
+#pragma unroll
+    for (int i = 0; i < kInstB; ++i) {
+      const int nr = n0 + (wave * kInstB + i) * kRowsPerInst + dma_row;
+      b_goff[i] = (uint32_t)nr * (uint32_t)K + (uint32_t)(dma_chunk * 8);
+    }
+    const bf16_t *Bg = B + (long long)g * b_group_stride;
 
     f32x4 acc[MI][NJ];
 #pragma unroll
@@ -184,57 +267,93 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
 #pragma unroll
       for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 ra[LA], rb[LB];
+    // The previous tile's stores drain and every wave is past its last LDS
+    // read before the ring is refilled.
+    wait_vmcnt(0);
+    lds_barrier();
+
+#define PRICHS_ISSUE_STAGE(kt_)                                                       \
+  do {                                                                               \
+    const int k0_ = (kt_) * BK;                                                      \
+    bf16_t *st_ = lds + ((kt_) & (kStages - 1)) * kStageElems;                       \
+    _Pragma("unroll") for (int i_ = 0; i_ < kInstA; ++i_)                            \
+        dma_16b(A + a_goff[i_] + k0_, st_ + (wave * kInstA + i_) * kRowsPerInst * BK); \
+    _Pragma("unroll") for (int i_ = 0; i_ < kInstB; ++i_)                            \
+        dma_16b(Bg + b_goff[i_] + k0_, st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK); \
+  } while (0)
+
+    // Prologue: stages 0..3 in flight; stage 0 lands and is read.
+    PRICHS_ISSUE_STAGE(0);
+    if (KT > 1) PRICHS_ISSUE_STAGE(1);
+    if (KT > 2) PRICHS_ISSUE_STAGE(2);
+    if (KT > 3) PRICHS_ISSUE_STAGE(3);
+    {
+      const int ahead = min(3, KT - 1);  // stages issued after stage 0
+      if (ahead == 3)
+        wait_vmcnt(3 * kInstPerStage);
+      else if (ahead == 2)
+        wait_vmcnt(2 * kInstPerStage);
+      else if (ahead == 1)
+        wait_vmcnt(kInstPerStage);
+      else
+        wait_vmcnt(0);
+    }
+    lds_barrier();
+
+    bf16x8 af[MI], wf[NJ], wn_next[NJ];
 #pragma unroll
-    for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(A + a_off[i]);
+    for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(lds + a_rd + i * 16 * BK);
 #pragma unroll
-    for (int i = 0; i < LB; ++i) rb[i] = *reinterpret_cast<const u32x4 *>(b_base + i * b_pass);
-#pragma unroll
-    for (int i = 0; i < LA; ++i)
-      *reinterpret_cast<u32x4 *>(lds + st_off + kRowsPerPass * i * BK) = ra[i];
-#pragma unroll
-    for (int i = 0; i < LB; ++i)
-      *reinterpret_cast<u32x4 *>(lds + BM * BK + st_off + kRowsPerPass * i * BK) = rb[i];
-    __syncthreads();
+    for (int j = 0; j < NJ; ++j)
+      wf[j] = *reinterpret_cast<const bf16x8 *>(lds + BM * BK + b_rd + j * 16 * BK);
 
     for (int kt = 0; kt < KT; ++kt) {
-      const bool more = kt + 1 < KT;
-      if (more) {
-        const int k0 = (kt + 1) * BK;
+      // First half: A fragments 0 .. MI/2-1 of stage kt.
 #pragma unroll
-        for (int i = 0; i < LA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(A + a_off[i] + k0);
-#pragma unroll
-        for (int i = 0; i < LB; ++i)
-          rb[i] = *reinterpret_cast<const u32x4 *>(b_base + i * b_pass + k0);
-      }
-      const bf16_t *as = lds + (kt & 1) * kStageElems;
-      const bf16_t *bs = as + BM * BK;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        bf16x8 af[MI], wf[NJ];
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-          af[i] = *reinterpret_cast<const bf16x8 *>(as + (ks ? a_rd1 : a_rd0) + i * 16 * BK);
+      for (int i = 0; i < MI / 2; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-          wf[j] = *reinterpret_cast<const bf16x8 *>(bs + (ks ? b_rd1 : b_rd0) + j * 16 * BK);
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int j = 0; j < NJ; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
-      }
+          acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
+
+      const bool more = kt + 1 < KT;
       if (more) {
-        bf16_t *as_n = lds + ((kt + 1) & 1) * kStageElems;
+        // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
+        const int ahead = min(2, KT - 2 - kt);
+        if (ahead == 2)
+          wait_vmcnt(2 * kInstPerStage);
+        else if (ahead == 1)
+          wait_vmcnt(kInstPerStage);
+        else
+          wait_vmcnt(0);
+        lds_barrier();
+        // Every wave has read stage kt (in the previous iteration), so its
+        // slot takes stage kt + 4.
+        if (kt + 4 < KT) PRICHS_ISSUE_STAGE(kt + 4);
+        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
+        const bf16_t *bs = as + BM * BK;
 #pragma unroll
-        for (int i = 0; i < LA; ++i)
-          *reinterpret_cast<u32x4 *>(as_n + st_off + kRowsPerPass * i * BK) = ra[i];
+        for (int j = 0; j < NJ; ++j)
+          wn_next[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
 #pragma unroll
-        for (int i = 0; i < LB; ++i)
-          *reinterpret_cast<u32x4 *>(as_n + BM * BK + st_off + kRowsPerPass * i * BK) = rb[i];
+        for (int i = 0; i < MI / 2; ++i)
+          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
       }
-      __syncthreads();
+      // Second half: A fragments MI/2 .. MI-1 of stage kt.
+#pragma unroll
+      for (int i = MI / 2; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
+      if (more) {
+        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
+#pragma unroll
+        for (int i = MI / 2; i < MI; ++i)
+          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) wf[j] = wn_next[j];
+      }
     }
+#undef PRICHS_ISSUE_STAGE
 
     // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
     //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
@@ -284,427 +403,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     }
   }
 }
-}  // namespace bf
 
-// ------------------------------------------------------------------------
-// bf16 kernel, direct-to-LDS pipeline
-// ------------------------------------------------------------------------
-// Same tile, wave grid, operand order and epilogue as bf::grouped_gemm_kernel;
-// the staging differs: global_load_lds_dwordx4 writes each lane's 16 bytes
-// straight into LDS (no staging registers, no ds_write), K advances 32 at a
-// time through a ring of 4 LDS stages, and loads run 3 stages ahead.  One
-// workgroup barrier per stage; waits are explicit vmcnt counts.
-namespace bf3 {
-constexpr int BM = 256, BN = 256, BK = 32, kStages = 4;
-constexpr int WGM = 2, WGN = 4;
-constexpr int kThreads = 64 * WGM * WGN;
-constexpr int kWaves = WGM * WGN;
-constexpr int WM = BM / WGM, WN = BN / WGN;
-constexpr int MI = WM / 16, NJ = WN / 16;
-constexpr int kIl = WN / 2;
-constexpr int kRowsPerInst = 16;  // one wave instruction fills 1 KiB = 16 rows of 64 bytes
-constexpr int kInstA = BM / kRowsPerInst / kWaves;
-constexpr int kInstB = BN / kRowsPerInst / kWaves;
-constexpr int kInstPerStage = kInstA + kInstB;
-constexpr int kStageElems = (BM + BN) * BK;
-constexpr size_t kLdsBytes = (size_t)kStages * kStageElems * sizeof(bf16_t);
-static_assert(kIl == bf::kIl, "both bf16 kernels consume the same packed gate/up layout");
-static_assert(BN == bf::BN && BM == bf::BM, "tile shape shared with the register-staged kernel");
-static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
-              "the DMA instructions of one stage cover the A and B tiles exactly");
-static_assert(kInstPerStage * 2 <= 63, "vmcnt immediates");
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a gfx950 CU");
-
-// 64-byte rows of 4 16-byte chunks.  The key makes the 16 rows of one
-// fragment read hit distinct banks whether the LDS serves 8 or 16 lanes of a
-// ds_read_b128 per cycle.
-__device__ inline int swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
-__device__ inline int lds_off(int row, int chunk) { return row * BK + ((chunk ^ swz(row)) << 3); }
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] at [15:14]).
-#define PRICHS_WAIT_VMCNT(n) \
-  __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
-
-__device__ inline void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-template <bool GATEUP>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
-    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
-    const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
-    bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
-    int G) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  __shared__ TileMap tm;
-  build_tile_map(tm, offsets, G, BM);
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
-  const int n_tiles = Np / BN;
-  const int m_tiles = tm.prefix[G];
-  const int total = m_tiles * n_tiles;
-  const int KT = K / BK;
-
-  // DMA lane mapping: instruction i of wave w fills rows r0 = 16 (w kInst + i)
-  // .. r0 + 15; lane l lands at r0 + l/4, physical chunk l%4, so it loads the
-  // logical chunk (l%4) ^ swz(row).
-  const int dma_row = lane >> 2;
-  const int dma_chunk = (lane & 3) ^ swz(dma_row);  // swz depends on row % 8 only
-
-  const int fr = lane & 15;
-  const int a_rd = lds_off(wm * WM + fr, lane >> 4);
-  const int b_rd = lds_off(wn * WN + fr, lane >> 4);
-
-  const int nblk = gridDim.x;
-  const int lb = (nblk % 8 == 0) ? (int)(blockIdx.x % 8) * (nblk / 8) + (int)(blockIdx.x / 8)
-                                 : (int)blockIdx.x;
-
-  for (int t = lb; t < total; t += nblk) {
-    int mt, nt;
-    bf::tile_coords(t, m_tiles, n_tiles, mt, nt);
-    const int g = find_group(tm, G, mt);
-    const int row0 = offsets[g];
-    const int mg = offsets[g + 1] - row0;
-    const int m0 = (mt - tm.prefix[g]) * BM;
-    const int n0 = nt * BN;
-
-    uint32_t a_goff[kInstA], b_goff[kInstB];
-#pragma unroll
-    for (int i = 0; i < kInstA; ++i) {
-      int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
-      lr = lr < mg ? lr : mg - 1;
-      const int vr = row0 + lr;
-      const int src = a_rows ? a_rows[vr] : vr;
-      a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < kInstB; ++i) {
-      const int nr = n0 + (wave * kInstB + i) * kRowsPerInst + dma_row;
-      b_goff[i] = (uint32_t)nr * (uint32_t)K + (uint32_t)(dma_chunk * 8);
-    }
-    const bf16_t *Bg = B + (long long)g * b_group_stride;
-
-    f32x4 acc[MI][NJ];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // The previous tile's epilogue stores drain and every wave is past its
-    // last LDS read before the ring is refilled.
-    PRICHS_WAIT_VMCNT(0);
-    lds_barrier();
-
-#define PRICHS_ISSUE_STAGE(kt_)                                                       \
-  do {                                                                               \
-    const int k0_ = (kt_) * BK;                                                      \
-    bf16_t *st_ = lds + ((kt_) & (kStages - 1)) * kStageElems;                       \
-    _Pragma("unroll") for (int i_ = 0; i_ < kInstA; ++i_)                            \
-        __builtin_amdgcn_global_load_lds(A + a_goff[i_] + k0_,                       \
-                                         st_ + (wave * kInstA + i_) * kRowsPerInst * BK, \
-                                         16, 0, 0);                                  \
-    _Pragma("unroll") for (int i_ = 0; i_ < kInstB; ++i_)                            \
-        __builtin_amdgcn_global_load_lds(Bg + b_goff[i_] + k0_,                      \
-                                         st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK, \
-                                         16, 0, 0);                                  \
-  } while (0)
-
-    PRICHS_ISSUE_STAGE(0);
-    if (KT > 1) PRICHS_ISSUE_STAGE(1);
-    if (KT > 2) PRICHS_ISSUE_STAGE(2);
-
-    for (int kt = 0; kt < KT; ++kt) {
-      // Stages issued so far: min(kt + 3, KT); those after kt may stay in flight.
-      const int ahead = min(2, KT - 1 - kt);
-      if (ahead == 2)
-        PRICHS_WAIT_VMCNT(2 * kInstPerStage);
-      else if (ahead == 1)
-        PRICHS_WAIT_VMCNT(kInstPerStage);
-      else
-        PRICHS_WAIT_VMCNT(0);
-      lds_barrier();
-      // The slot refilled here was last read in iteration kt - 1, before the barrier.
-      if (kt + 3 < KT) PRICHS_ISSUE_STAGE(kt + 3);
-
-      const bf16_t *as = lds + (kt & (kStages - 1)) * kStageElems;
-      const bf16_t *bs = as + BM * BK;
-      bf16x8 af[MI], wf[NJ];
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) wf[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
-    }
-#undef PRICHS_ISSUE_STAGE
-
-    const int lr = m0 + wm * WM + fr;
-    const int cq = 4 * (lane >> 4);
-    if (GATEUP) {
-      const int cbase = (n0 + wn * WN) / 2 + cq;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int m = lr + 16 * i;
-        if (m < mg) {
-          bf16_t *crow = C + (long long)(row0 + m) * ldc;
-#pragma unroll
-          for (int j = 0; j < NJ / 2; ++j) {
-            const int col = cbase + 16 * j;
-            if (col < n_store) {
-              uint32_t h[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                h[r] = f32_to_bf16(PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
-              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-            }
-          }
-        }
-      }
-    } else {
-      const int cbase = n0 + wn * WN + cq;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int m = lr + 16 * i;
-        if (m < mg) {
-          bf16_t *crow = C + (long long)(row0 + m) * ldc;
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const int col = cbase + 16 * j;
-            if (col < n_store) {
-              uint32_t h[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(acc[i][j][r]);
-              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-            }
-          }
-        }
-      }
-    }
-  }
-}
-}  // namespace bf3
-
-// ------------------------------------------------------------------------
-// bf16 kernel, direct-to-LDS pipeline with fragment reads hidden under MFMAs
-// ------------------------------------------------------------------------
-// Same LDS ring, DMA mapping, tile order and epilogue as bf3.  Each stage's
-// MFMAs are split in two halves around the workgroup barrier: after the
-// first half frees the A fragments of rows 0..3, the wave waits for the next
-// stage, passes the barrier, issues that stage's fragment reads (into the
-// freed registers) and the DMA of stage kt + 4, and only then runs the
-// second half, so the LDS read latency and bandwidth of one stage overlap the
-// MFMAs of the previous one.
-namespace bf4 {
-using namespace bf3;  // tile shape, swizzle, DMA layout
-static_assert(MI % 2 == 0, "two halves of A fragments");
-
-template <bool GATEUP>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
-    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
-    const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
-    bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
-    int G) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  __shared__ TileMap tm;
-  build_tile_map(tm, offsets, G, BM);
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
-  const int n_tiles = Np / BN;
-  const int m_tiles = tm.prefix[G];
-  const int total = m_tiles * n_tiles;
-  const int KT = K / BK;
-
-  const int dma_row = lane >> 2;
-  const int dma_chunk = (lane & 3) ^ swz(dma_row);
-  const int fr = lane & 15;
-  const int a_rd = lds_off(wm * WM + fr, lane >> 4);
-  const int b_rd = lds_off(wn * WN + fr, lane >> 4);
-
-  const int nblk = gridDim.x;
-  const int lb = (nblk % 8 == 0) ? (int)(blockIdx.x % 8) * (nblk / 8) + (int)(blockIdx.x / 8)
-                                 : (int)blockIdx.x;
-
-  for (int t = lb; t < total; t += nblk) {
-    int mt, nt;
-    bf::tile_coords(t, m_tiles, n_tiles, mt, nt);
-    const int g = find_group(tm, G, mt);
-    const int row0 = offsets[g];
-    const int mg = offsets[g + 1] - row0;
-    const int m0 = (mt - tm.prefix[g]) * BM;
-    const int n0 = nt * BN;
-
-    uint32_t a_goff[kInstA], b_goff[kInstB];
-#pragma unroll
-    for (int i = 0; i < kInstA; ++i) {
-      int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
-      lr = lr < mg ? lr : mg - 1;
-      const int vr = row0 + lr;
-      const int src = a_rows ? a_rows[vr] : vr;
-      a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < kInstB; ++i) {
-      const int nr = n0 + (wave * kInstB + i) * kRowsPerInst + dma_row;
-      b_goff[i] = (uint32_t)nr * (uint32_t)K + (uint32_t)(dma_chunk * 8);
-    }
-    const bf16_t *Bg = B + (long long)g * b_group_stride;
-
-    f32x4 acc[MI][NJ];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    PRICHS_WAIT_VMCNT(0);
-    lds_barrier();
-
-#define PRICHS_ISSUE_STAGE(kt_)                                                       \
-  do {                                                                               \
-    const int k0_ = (kt_) * BK;                                                      \
-    bf16_t *st_ = lds + ((kt_) & (kStages - 1)) * kStageElems;                       \
-    _Pragma("unroll") for (int i_ = 0; i_ < kInstA; ++i_)                            \
-        __builtin_amdgcn_global_load_lds(A + a_goff[i_] + k0_,                       \
-                                         st_ + (wave * kInstA + i_) * kRowsPerInst * BK, \
-                                         16, 0, 0);                                  \
-    _Pragma("unroll") for (int i_ = 0; i_ < kInstB; ++i_)                            \
-        __builtin_amdgcn_global_load_lds(Bg + b_goff[i_] + k0_,                      \
-                                         st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK, \
-                                         16, 0, 0);                                  \
-  } while (0)
-
-    // Prologue: stages 0..3 in flight; stage 0 lands and is read.
-    PRICHS_ISSUE_STAGE(0);
-    if (KT > 1) PRICHS_ISSUE_STAGE(1);
-    if (KT > 2) PRICHS_ISSUE_STAGE(2);
-    if (KT > 3) PRICHS_ISSUE_STAGE(3);
-    {
-      const int ahead = min(3, KT - 1);  // stages issued after stage 0
-      if (ahead == 3)
-        PRICHS_WAIT_VMCNT(3 * kInstPerStage);
-      else if (ahead == 2)
-        PRICHS_WAIT_VMCNT(2 * kInstPerStage);
-      else if (ahead == 1)
-        PRICHS_WAIT_VMCNT(kInstPerStage);
-      else
-        PRICHS_WAIT_VMCNT(0);
-    }
-    lds_barrier();
-
-    bf16x8 af[MI], wf[NJ], wn_next[NJ];
-    {
-      const bf16_t *as = lds;
-      const bf16_t *bs = as + BM * BK;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) wf[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
-    }
-
-    for (int kt = 0; kt < KT; ++kt) {
-      // First half: A rows 0 .. MI/2-1 of stage kt.
-#pragma unroll
-      for (int i = 0; i < MI / 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
-
-      const bool more = kt + 1 < KT;
-      if (more) {
-        // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
-        const int ahead = min(2, KT - 2 - kt);
-        if (ahead == 2)
-          PRICHS_WAIT_VMCNT(2 * kInstPerStage);
-        else if (ahead == 1)
-          PRICHS_WAIT_VMCNT(kInstPerStage);
-        else
-          PRICHS_WAIT_VMCNT(0);
-        lds_barrier();
-        // Every wave has read stage kt (in the previous iteration), so its
-        // slot takes stage kt + 4.
-        if (kt + 4 < KT) PRICHS_ISSUE_STAGE(kt + 4);
-        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
-        const bf16_t *bs = as + BM * BK;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          wn_next[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
-#pragma unroll
-        for (int i = 0; i < MI / 2; ++i)
-          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
-      }
-      // Second half: A rows MI/2 .. MI-1 of stage kt.
-#pragma unroll
-      for (int i = MI / 2; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
-      if (more) {
-        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
-#pragma unroll
-        for (int i = MI / 2; i < MI; ++i)
-          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) wf[j] = wn_next[j];
-      }
-    }
-#undef PRICHS_ISSUE_STAGE
-
-    const int lr = m0 + wm * WM + fr;
-    const int cq = 4 * (lane >> 4);
-    if (GATEUP) {
-      const int cbase = (n0 + wn * WN) / 2 + cq;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int m = lr + 16 * i;
-        if (m < mg) {
-          bf16_t *crow = C + (long long)(row0 + m) * ldc;
-#pragma unroll
-          for (int j = 0; j < NJ / 2; ++j) {
-            const int col = cbase + 16 * j;
-            if (col < n_store) {
-              uint32_t h[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                h[r] = f32_to_bf16(PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
-              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-            }
-          }
-        }
-      }
-    } else {
-      const int cbase = n0 + wn * WN + cq;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int m = lr + 16 * i;
-        if (m < mg) {
-          bf16_t *crow = C + (long long)(row0 + m) * ldc;
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const int col = cbase + 16 * j;
-            if (col < n_store) {
-              uint32_t h[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(acc[i][j][r]);
-              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-            }
-          }
-        }
-      }
-    }
-  }
-}
-}  // namespace bf4
 
 // ------------------------------------------------------------------------
 // f32 kernel (fp32-checked mode)
@@ -853,12 +552,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
 }
 }  // namespace fp
 
-size_t il_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)bf::kIl : (size_t)fp::kIl; }
-size_t bn_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)bf::BN : (size_t)fp::BN; }
+size_t il_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)Bf16::kIl : (size_t)fp::kIl; }
+size_t bn_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)Bf16::BN : (size_t)fp::BN; }
 
 int check_gemm_shape(size_t d, size_t f, int dtype, const char *who) {
   if (!dtype_ok(dtype)) return fail(PRICHS_ERR_INVALID_ARGUMENT, "%s: bad dtype %d", who, dtype);
-  const size_t q = dtype == PRICHS_DTYPE_BF16 ? (size_t)bf::BK : (size_t)fp::BK;
+  const size_t q = dtype == PRICHS_DTYPE_BF16 ? (size_t)kBf16KMultiple : (size_t)fp::BK;
   if (d == 0 || f == 0 || d % q || f % q)
     return fail(PRICHS_ERR_UNSUPPORTED, "%s: d=%zu and f=%zu must be positive multiples of %zu",
                 who, d, f, q);
@@ -896,16 +595,28 @@ template <typename T> void pack_down_impl(const float *down, size_t d, size_t f,
     for (size_t k = 0; k < f; ++k) put<T>(out, n * f + k, n < d ? down[k * d + n] : 0.0f);
 }
 
-#ifndef PRICHS_GEMM_VERSION
-#define PRICHS_GEMM_VERSION 4
-#endif
-#if PRICHS_GEMM_VERSION == 4
-namespace BFK = bf4;
-#elif PRICHS_GEMM_VERSION == 3
-namespace BFK = bf3;
-#else
-namespace BFK = bf;
-#endif
+template <class Cf, bool GATEUP>
+int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
+                int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
+                size_t max_rows, int cus, hipStream_t s) {
+  // Persistent grid: one workgroup per CU (the LDS ring allows one), fewer
+  // when the launch has fewer tiles.
+  const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN);
+  const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus));
+  static bool attr_set = false;
+  if (!attr_set) {
+    PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&bf16_gemm_kernel<Cf, GATEUP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)Cf::kLdsBytes),
+                   "grouped gemm: set LDS size");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((bf16_gemm_kernel<Cf, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
+                     static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
+                     b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G);
+  PRICHS_LAUNCH_CHECK("grouped gemm launch");
+  return PRICHS_OK;
+}
 
 int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, const void *B,
                    long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
@@ -913,21 +624,11 @@ int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, c
   const int cus = device_cu_count();
   if (cus <= 0) return fail(PRICHS_ERR_HIP, "grouped gemm: cannot query the device");
   if (dtype == PRICHS_DTYPE_BF16) {
-    const size_t ub = (max_rows / BFK::BM + G) * (size_t)(Np / BFK::BN);
-    const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus));
-    auto kern = gateup ? BFK::grouped_gemm_kernel<true> : BFK::grouped_gemm_kernel<false>;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[gateup]) {
-      PRICHS_HIP_TRY(hipFuncSetAttribute((const void *)kern,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)BFK::kLdsBytes),
-                     "grouped gemm: set LDS size");
-      attr_set[gateup] = true;
-    }
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(BFK::kThreads), BFK::kLdsBytes, s,
-                       static_cast<const bf16_t *>(A), a_rows, lda,
-                       static_cast<const bf16_t *>(B), b_stride, Np, K,
-                       static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G);
+    if (gateup)
+      return launch_bf16<Bf16, true>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
+                                     offsets, G, max_rows, cus, s);
+    return launch_bf16<Bf16Down, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
+                                        offsets, G, max_rows, cus, s);
   } else {
     const size_t ub = (max_rows / fp::BM + G) * (size_t)(Np / fp::BN);
     const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus * 4));
