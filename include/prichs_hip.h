@@ -230,6 +230,59 @@ int prichs_rope_forward(void *qk, int dtype, const float *cos_cache,
                         size_t seq_len, size_t n_heads, size_t head_dim,
                         size_t pos_offset, int sign, void *stream);
 
+/* RoPE with a row stride (elements between consecutive rows of qk), for Q
+ * or K living inside a fused [rows, q | k | v] projection buffer.  Same
+ * arithmetic as prichs_rope_forward (backward.rs:160-188). */
+int prichs_rope_forward_ld(void *qk, size_t row_stride, int dtype,
+                           const float *cos_cache, const float *sin_cache,
+                           size_t cache_rows, size_t batch, size_t seq_len,
+                           size_t n_heads, size_t head_dim, size_t pos_offset,
+                           int sign, void *stream);
+
+/* out = a + b element-wise in f32 arithmetic; each operand bf16 or f32.
+ * Replaces add_tensors (crates/prichs-core/src/ops.rs:250-267) for the
+ * block's residual connections.  n % 8 == 0, 16-byte aligned operands. */
+int prichs_add(const void *a, int a_dtype, const void *b, int b_dtype,
+               void *out, int out_dtype, size_t n, void *stream);
+
+/* Dense GEMM C[M, N] = A[M, K] @ W on the bf16 (or f32) MFMA kernel of the
+ * grouped GEMMs: replaces matmul_2d's device dispatch / forward_gemm
+ * (crates/prichs-core/src/ops.rs:24-31; crates/prichs-cuda/src/engine.rs:
+ * 757-826) for the block's projections.  W comes from prichs_pack_weight.
+ * Row strides lda (multiple of 8) and ldc (multiple of 4); K and N multiples
+ * of 64 (bf16) or 16 (f32); fp32 accumulation. */
+size_t prichs_packed_weight_elems(size_t K, size_t N, int dtype);
+int prichs_pack_weight(const float *w, size_t K, size_t N, int dtype,
+                       void *packed_out);
+int prichs_gemm(const void *a, size_t lda, size_t M, size_t K,
+                const void *w_packed, size_t N, void *c, size_t ldc, int dtype,
+                void *stream);
+
+/* Causal GQA self-attention forward (flash-style; bf16 in/out, fp32
+ * softmax and accumulation).  Restates the per-head attention of
+ * crates/prichs-model/src/attention.rs:94-149 -- query head h attends with
+ * kv head h / (n_heads / n_kv_heads), scores (q . k) / sqrt(head_dim) over
+ * j <= i, softmax over the causal row -- for `batch` independent sequences:
+ * row r of sequence b is row b * seq_len + r of q/k/v/o; head h of q and o
+ * starts at column h * head_dim, kv head j of k and v at column j * head_dim
+ * (leading dimensions ldq/ldk/ldv/ldo, multiples of 8).  Replaces the
+ * materialised-score attention of gpu_batched_attention_forward
+ * (crates/prichs-cuda/src/engine.rs:1181-1405).  head_dim must be 128. */
+int prichs_attention_forward(const void *q, size_t ldq, const void *k,
+                             size_t ldk, const void *v, size_t ldv, void *o,
+                             size_t ldo, size_t batch, size_t seq_len,
+                             size_t n_heads, size_t n_kv_heads,
+                             size_t head_dim, int dtype, void *stream);
+
+/* RoPE cos/sin tables on the host (no GPU needed): replaces
+ * precompute_rope_cache (crates/prichs-core/src/backward.rs:136-157).
+ * cos/sin [max_seq_len, head_dim/2]: freq_i = 1/theta^(2i/hd) (libm powf),
+ * angle = (float)t * freq_i, libm cosf/sinf -- bit-identical to the
+ * reference's f32 computation on the same libm.  Upload the tables for
+ * prichs_rope_forward / launch_rope. */
+int prichs_rope_cache(size_t max_seq_len, size_t head_dim, float theta,
+                      float *cos_out, float *sin_out);
+
 /* ---------------------------------------------------------------------- */
 /* 3. MoE engine (owns packed weights + workspace; replaces the MoE part of */
 /*    GpuModelEngine: engine.rs:363-649, 668-689, 1917-2239)               */
@@ -300,6 +353,61 @@ int prichs_moe_engine_stash(const prichs_moe_engine *eng,
 int prichs_moe_engine_set_timing(prichs_moe_engine *eng, int max_forwards);
 int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
                                int *n_forwards);
+
+/* ---------------------------------------------------------------------- */
+/* 4. PrichsBlock engine (crates/prichs-model/src/block.rs:50-68): RMSNorm,  */
+/*    GQA attention with RoPE, residual, RMSNorm, the MoE engine, residual. */
+/* ---------------------------------------------------------------------- */
+typedef struct prichs_block_engine prichs_block_engine;
+
+/* Creates a block engine (bf16 activations and weights, fp32 accumulation,
+ * f32 residual stream) for up to max_tokens rows and positions below
+ * max_seq_len; the RoPE tables for rope_theta are built here
+ * (prichs_rope_cache).  head_dim = d / n_heads must be 128. */
+int prichs_block_engine_create(size_t d, size_t n_heads, size_t n_kv_heads,
+                               size_t f, size_t E, size_t k, size_t n_shared,
+                               size_t max_tokens, size_t max_seq_len,
+                               float rope_theta, float eps,
+                               prichs_block_engine **out);
+int prichs_block_engine_destroy(prichs_block_engine *eng);
+
+/* Host f32 weights in the reference layouts (block.rs:15-48,
+ * attention.rs:17-26): input_norm / post_attn_norm [d], wq [d, d],
+ * wk / wv [d, n_kv_heads * head_dim], wo [d, d]; the MoE weights as for
+ * prichs_moe_engine_upload.  Synchronous. */
+int prichs_block_engine_upload(prichs_block_engine *eng, const float *input_norm,
+                               const float *post_attn_norm, const float *wq,
+                               const float *wk, const float *wv, const float *wo,
+                               const float *w_router, const float *router_bias,
+                               const float *const *gate, const float *const *up,
+                               const float *const *down);
+
+/* x: bf16 [batch * seq_len, d] (device), `batch` independent sequences at
+ * positions pos_offset .. pos_offset + seq_len - 1; out [batch * seq_len, d]
+ * of out_dtype (device).  concept_bias as for prichs_moe_engine_forward. */
+int prichs_block_engine_forward(prichs_block_engine *eng, const void *x,
+                                size_t batch, size_t seq_len, size_t pos_offset,
+                                const float *concept_bias, size_t n_concept,
+                                void *out, int out_dtype, void *stream);
+
+/* Device views of the last forward's intermediates: normed1 bf16 [T, d],
+ * qkv bf16 [T, d + 2 * n_kv_heads * head_dim] (q and k after RoPE), attn
+ * bf16 [T, d] (concatenated heads), attn_out bf16 [T, d] (after Wo),
+ * x1 f32 [T, d], normed2 bf16 [T, d], moe_out bf16 [T, d], and the embedded
+ * MoE engine (for prichs_moe_engine_stash).  Valid until the next forward. */
+typedef struct prichs_block_stash {
+  size_t T;
+  const void *normed1;
+  const void *qkv;
+  const void *attn;
+  const void *attn_out;
+  const float *x1;
+  const void *normed2;
+  const void *moe_out;
+  const prichs_moe_engine *moe;
+} prichs_block_stash;
+int prichs_block_engine_stash(const prichs_block_engine *eng,
+                              prichs_block_stash *out);
 
 #ifdef __cplusplus
 }

@@ -62,6 +62,14 @@ def lib():
         L.orc_precompute_rope_cache.restype = None
         L.orc_rope_forward_in_place.argtypes = [_f32p, _f32p, _f32p, sz, sz, sz, sz]
         L.orc_rope_forward_in_place.restype = None
+        L.orc_attention_forward.argtypes = [_f32p, sz, sz, sz, sz, sz, _f32p, _f32p, _f32p, _f32p,
+                                            _f32p, _f32p, sz, _f32p, C.c_void_p]
+        L.orc_attention_forward.restype = C.c_int
+        L.orc_block_forward.argtypes = [_f32p, sz, sz, sz, sz, sz, sz, _f32p, _f32p, C.c_float,
+                                        _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, sz, sz, sz, sz,
+                                        sz, _f32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_block_forward.restype = C.c_int
         L.orc_num_threads.restype = C.c_int
         L.orc_set_num_threads.argtypes = [C.c_int]
         L.orc_set_num_threads.restype = None
@@ -199,3 +207,46 @@ def rope_forward(t, cos, sin, pos_offset=0):
     S, H, hd = t.shape
     lib().orc_rope_forward_in_place(t, _c(cos), _c(sin), S, H, hd, pos_offset)
     return t
+
+
+def attention_forward(x, Hq, Hkv, wq, wk, wv, wo, cos, sin, pos_offset=0, want_concat=False):
+    """SelfAttention::forward_with_rope (attention.rs:56-176) of one sequence x [S, d]."""
+    x = _c(x)
+    S, d = x.shape
+    hd = d // Hq
+    out = np.empty((S, d), np.float32)
+    cat = np.empty((S, d), np.float32) if want_concat else None
+    rc = lib().orc_attention_forward(x, S, d, Hq, Hkv, hd, _c(wq), _c(wk), _c(wv), _c(wo),
+                                     _c(cos), _c(sin), pos_offset, out,
+                                     None if cat is None else cat.ctypes.data)
+    if rc != 0:
+        raise ValueError("bad attention arguments")
+    return (out, cat) if want_concat else out
+
+
+def block_forward(inp):
+    """PrichsBlock::forward_with_rope (block.rs:50-68) over inp.batch sequences
+    (a prichs_amd.synth.BlockInputs); returns dict(out, attn, x1, moe)."""
+    m = inp.moe
+    T, d = inp.x.shape
+    S, E, k, n_sh = m.n_shared + m.E, m.E, m.k, m.n_shared
+    gates = [_c(a) for a in m.gate]
+    ups = [_c(a) for a in m.up]
+    downs = [_c(a) for a in m.down]
+    arr_t = C.c_void_p * S
+    pg = arr_t(*[a.ctypes.data for a in gates])
+    pu = arr_t(*[a.ctypes.data for a in ups])
+    pd = arr_t(*[a.ctypes.data for a in downs])
+    out = np.empty((T, d), np.float32)
+    attn = np.empty((T, d), np.float32)
+    x1 = np.empty((T, d), np.float32)
+    mo = np.empty((T, d), np.float32)
+    rc = lib().orc_block_forward(
+        _c(inp.x), inp.batch, inp.seq_len, d, inp.n_heads, inp.n_kv_heads, inp.head_dim,
+        _c(inp.input_norm), _c(inp.post_norm), inp.eps, _c(inp.wq), _c(inp.wk), _c(inp.wv),
+        _c(inp.wo), _c(inp.cos), _c(inp.sin), 0, m.f, E, k, n_sh, _c(m.w_router),
+        _c(m.router_bias), C.cast(pg, C.c_void_p), C.cast(pu, C.c_void_p),
+        C.cast(pd, C.c_void_p), out, attn.ctypes.data, x1.ctypes.data, mo.ctypes.data)
+    if rc != 0:
+        raise RuntimeError("oracle block_forward failed")
+    return dict(out=out, attn=attn, x1=x1, moe=mo)

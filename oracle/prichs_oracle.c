@@ -33,6 +33,12 @@
  *   orc_precompute_rope_cache / orc_rope_forward_in_place
  *                            cos=1/sin=0 identity (engine.rs:2970-2972), norm
  *                            preservation, float64 closed form.
+ *   orc_attention_forward    float64 causal-softmax attention recomputed in
+ *                            numpy (GQA head mapping, RoPE); softmax rows sum
+ *                            to 1 and causal zeros (engine.rs:2948-3029);
+ *                            row 0 attends only to itself.
+ *   orc_block_forward        float64 re-assembly of the block from the pinned
+ *                            pieces (RMSNorm, attention, MoE, residuals).
  */
 #include <math.h>
 #include <stddef.h>
@@ -387,6 +393,150 @@ ORC_API void orc_rope_forward_in_place(float *tensor, const float *cos_cache,
       }
     }
   }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Self-attention of one sequence: crates/prichs-model/src/attention.rs:56-176 */
+/*                                                                            */
+/* q = x Wq, k = x Wk, v = x Wv (ops.rs GEMM order); RoPE on q (Hq heads) and */
+/* k (Hkv heads) at positions t + pos_offset; per head h with kv head         */
+/* h / (Hq / Hkv):                                                            */
+/*   score[i][j] = (sum_d q[i][d] k[j][d]) * scale, j <= i, d ascending,      */
+/*     scale = 1 / sqrt(hd) in f32;                                           */
+/*   softmax over j <= i: m = fold(-inf, max), e = exp(s - m), s = sum e      */
+/*     (j ascending), p = e * (1 / max(s, 1e-9));                             */
+/*   head_out[i][d] = sum over j ascending of p[j] * v[j][d] (product, then  */
+/*     sum).                                                                  */
+/* concat heads along columns (head h at h*hd), out = concat Wo.              */
+/* Requires Hq * hd == d (attention.rs indexes q rows with hidden_dim).       */
+/* attn_concat [S, d] may be NULL.                                            */
+/* ------------------------------------------------------------------------ */
+ORC_API int orc_attention_forward(const float *x, size_t S, size_t d, size_t Hq,
+                                  size_t Hkv, size_t hd, const float *wq,
+                                  const float *wk, const float *wv,
+                                  const float *wo, const float *cos_cache,
+                                  const float *sin_cache, size_t pos_offset,
+                                  float *out, float *attn_concat) {
+  if (Hq == 0 || Hkv == 0 || Hq % Hkv || Hq * hd != d || hd % 2) return -1;
+  const size_t kvw = Hkv * hd;
+  float *q = (float *)malloc(sizeof(float) * S * d);
+  float *k = (float *)malloc(sizeof(float) * S * kvw);
+  float *v = (float *)malloc(sizeof(float) * S * kvw);
+  float *cat = attn_concat ? attn_concat : (float *)malloc(sizeof(float) * S * d);
+  if (!q || !k || !v || !cat) {
+    free(q);
+    free(k);
+    free(v);
+    if (!attn_concat) free(cat);
+    return -1;
+  }
+  orc_matmul_2d(x, wq, q, S, d, d);
+  orc_matmul_2d(x, wk, k, S, d, kvw);
+  orc_matmul_2d(x, wv, v, S, d, kvw);
+  orc_rope_forward_in_place(q, cos_cache, sin_cache, S, Hq, hd, pos_offset);
+  orc_rope_forward_in_place(k, cos_cache, sin_cache, S, Hkv, hd, pos_offset);
+  const float scale = 1.0f / sqrtf((float)hd);
+  const size_t group = Hq / Hkv;
+  int bad = 0;
+  long long h;
+#pragma omp parallel for schedule(dynamic) reduction(| : bad)
+  for (h = 0; h < (long long)Hq; ++h) {
+    const size_t kvh = (size_t)h / group;
+    float *row = (float *)malloc(sizeof(float) * (S ? S : 1));
+    float *acc = (float *)malloc(sizeof(float) * hd);
+    if (!row || !acc) {
+      bad = 1;
+      free(row);
+      free(acc);
+      continue;
+    }
+    for (size_t i = 0; i < S; ++i) {
+      const float *qr = q + i * d + (size_t)h * hd;
+      for (size_t j = 0; j <= i; ++j) {
+        const float *kr = k + j * kvw + kvh * hd;
+        float dot = 0.0f;
+        for (size_t c = 0; c < hd; ++c) {
+          float p = qr[c] * kr[c];
+          dot = dot + p;
+        }
+        row[j] = dot * scale;
+      }
+      float mx = -INFINITY;
+      for (size_t j = 0; j <= i; ++j) mx = fmaxf(mx, row[j]);
+      float sum = 0.0f;
+      for (size_t j = 0; j <= i; ++j) {
+        float e = expf(row[j] - mx);
+        row[j] = e;
+        sum = sum + e;
+      }
+      const float inv = 1.0f / fmaxf(sum, 1e-9f);
+      for (size_t j = 0; j <= i; ++j) row[j] = row[j] * inv;
+      for (size_t c = 0; c < hd; ++c) acc[c] = 0.0f;
+      for (size_t j = 0; j <= i; ++j) {
+        const float *vr = v + j * kvw + kvh * hd;
+        const float w = row[j];
+        for (size_t c = 0; c < hd; ++c) {
+          float p = w * vr[c];
+          acc[c] = acc[c] + p;
+        }
+      }
+      memcpy(cat + i * d + (size_t)h * hd, acc, sizeof(float) * hd);
+    }
+    free(row);
+    free(acc);
+  }
+  if (!bad) orc_matmul_2d(cat, wo, out, S, d, d);
+  free(q);
+  free(k);
+  free(v);
+  if (!attn_concat) free(cat);
+  return bad ? -1 : 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* PrichsBlock::forward_with_rope: crates/prichs-model/src/block.rs:50-68,    */
+/* for `batch` independent sequences of seq_len rows (the block has no batch  */
+/* dimension; rows of different sequences never meet in attention, and the    */
+/* per-token RMSNorm / MoE / residual steps are row-wise):                     */
+/*   n1 = rms_norm(x, input_norm); x1 = x + Attn(n1);                         */
+/*   n2 = rms_norm(x1, post_norm); out = x1 + MoE(n2).                        */
+/* MoE weights as in orc_moe_forward (shared expert first when n_shared = 1). */
+/* Optional outputs (NULL to skip): attn_out [T, d] (the attention sub-layer  */
+/* output before the residual), x1 [T, d], moe_out [T, d].                    */
+/* ------------------------------------------------------------------------ */
+ORC_API int orc_block_forward(
+    const float *x, size_t batch, size_t seq_len, size_t d, size_t Hq, size_t Hkv,
+    size_t hd, const float *input_norm, const float *post_norm, float eps,
+    const float *wq, const float *wk, const float *wv, const float *wo,
+    const float *cos_cache, const float *sin_cache, size_t pos_offset, size_t f,
+    size_t E, size_t k, size_t n_shared, const float *w_router,
+    const float *router_bias, const float *const *w_gate,
+    const float *const *w_up, const float *const *w_down, float *out,
+    float *attn_out, float *x1_out, float *moe_out) {
+  const size_t T = batch * seq_len;
+  int rc = 0;
+  float *n1 = (float *)malloc(sizeof(float) * T * d);
+  float *att = attn_out ? attn_out : (float *)malloc(sizeof(float) * T * d);
+  float *x1 = x1_out ? x1_out : (float *)malloc(sizeof(float) * T * d);
+  float *mo = moe_out ? moe_out : (float *)malloc(sizeof(float) * T * d);
+  if (!n1 || !att || !x1 || !mo) rc = -1;
+  if (rc == 0) orc_rms_norm(x, input_norm, n1, T, d, eps);
+  for (size_t b = 0; rc == 0 && b < batch; ++b)
+    rc = orc_attention_forward(n1 + b * seq_len * d, seq_len, d, Hq, Hkv, hd, wq, wk, wv,
+                               wo, cos_cache, sin_cache, pos_offset,
+                               att + b * seq_len * d, NULL);
+  if (rc == 0) {
+    orc_add_tensors(x, att, x1, T * d);
+    orc_rms_norm(x1, post_norm, n1, T, d, eps);
+    rc = orc_moe_forward(n1, T, d, f, E, k, n_shared, w_router, router_bias, NULL, 0, w_gate,
+                         w_up, w_down, mo, NULL, NULL, NULL, NULL, NULL, NULL, NULL);
+  }
+  if (rc == 0) orc_add_tensors(x1, mo, out, T * d);
+  free(n1);
+  if (!attn_out) free(att);
+  if (!x1_out) free(x1);
+  if (!moe_out) free(mo);
+  return rc;
 }
 
 /* Number of OpenMP threads the oracle will use (1 without OpenMP). */

@@ -51,6 +51,20 @@ class MoEStash(C.Structure):
     ]
 
 
+class BlockStash(C.Structure):
+    _fields_ = [
+        ("T", C.c_size_t),
+        ("normed1", C.c_void_p),
+        ("qkv", C.c_void_p),
+        ("attn", C.c_void_p),
+        ("attn_out", C.c_void_p),
+        ("x1", C.c_void_p),
+        ("normed2", C.c_void_p),
+        ("moe_out", C.c_void_p),
+        ("moe", C.c_void_p),
+    ]
+
+
 _sz, _i, _f, _vp = C.c_size_t, C.c_int, C.c_float, C.c_void_p
 
 # name -> (restype, argtypes)
@@ -77,6 +91,21 @@ SIGNATURES = {
     "prichs_moe_combine": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _sz, _sz, _i, _vp, _i, _vp]),
     "prichs_rmsnorm_forward": (_i, [_vp, _i, _vp, _vp, _i, _vp, _sz, _sz, _f, _vp]),
     "prichs_rope_forward": (_i, [_vp, _i, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _vp]),
+    "prichs_rope_cache": (_i, [_sz, _sz, _f, _vp, _vp]),
+    "prichs_rope_forward_ld": (_i, [_vp, _sz, _i, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _vp]),
+    "prichs_add": (_i, [_vp, _i, _vp, _i, _vp, _i, _sz, _vp]),
+    "prichs_packed_weight_elems": (_sz, [_sz, _sz, _i]),
+    "prichs_pack_weight": (_i, [_vp, _sz, _sz, _i, _vp]),
+    "prichs_gemm": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _i, _vp]),
+    "prichs_attention_forward": (_i, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
+                                      _sz, _i, _vp]),
+    "prichs_block_engine_create": (_i, [_sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
+                                        C.POINTER(_vp)]),
+    "prichs_block_engine_destroy": (_i, [_vp]),
+    "prichs_block_engine_upload": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                        _vp]),
+    "prichs_block_engine_forward": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _i, _vp]),
+    "prichs_block_engine_stash": (_i, [_vp, C.POINTER(BlockStash)]),
     "prichs_moe_engine_create": (_i, [_sz, _sz, _sz, _sz, _sz, _i, _sz, C.POINTER(_vp)]),
     "prichs_moe_engine_destroy": (_i, [_vp]),
     "prichs_moe_engine_upload": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),

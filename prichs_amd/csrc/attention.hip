@@ -1,0 +1,282 @@
+// attention.hip -- causal GQA self-attention forward (flash-style) on CDNA4
+// MFMA, for the PrichsBlock attention sub-layer.
+//
+// Semantics: crates/prichs-model/src/attention.rs:94-149 -- per head h with
+// kv head h / (Hq / Hkv): scores = (q . k) * scale over j <= i, softmax over
+// the causal row, out = sum_j p_j v_j.  The T x T score matrix is never
+// materialised: each workgroup streams 64-row K/V blocks through LDS and
+// keeps an online softmax (running max m and partial sums l per query row).
+//
+// Layout per workgroup: one (sequence b, query head h, 128-query block);
+// 4 wave64s, each owning 32 query rows (two 16-row MFMA blocks).
+//   S^T = K Q^T     v_mfma_f32_16x16x32_bf16(K frag, Q frag): the lane owning
+//                   query column q = lane % 16 holds the scores of kv rows
+//                   4*(lane/16) + r of every 16-row kv block;
+//   O^T += V^T P^T  v_mfma_f32_16x16x32_bf16(V^T frag, P frag): P (bf16) is
+//                   taken straight from the softmax registers -- the MFMA's
+//                   k index runs over kv rows {4g..4g+3, 16+4g..16+4g+3} of
+//                   each 32-row step (g = lane / 16), and the V^T fragment
+//                   reads the same kv rows -- so no lane exchange is needed,
+//                   and the lane that owns query q also owns its output row.
+// K sits in LDS row-major ([kv][128], 16-byte chunks XOR-swizzled by row);
+// V is written transposed ([128 d][64 kv], 8-byte chunks XOR-swizzled by
+// row) so both fragment reads are bank-conflict free.
+#include "common.hpp"
+
+namespace prichs {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kHd = 128;      // head dim supported by this kernel
+constexpr int kBQ = 128;      // query rows per workgroup
+constexpr int kBKV = 64;      // kv rows per block
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kKElems = kBKV * kHd;   // K tile [64][128]
+constexpr int kVElems = kHd * kBKV;   // V^T tile [128][64]
+constexpr size_t kLdsBytes = (size_t)(kKElems + kVElems) * sizeof(bf16_t);
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// K tile: element offset of (kv row, 16-byte chunk c in 0..15).
+__device__ __forceinline__ int k_off(int kv, int c) { return kv * kHd + ((c ^ (kv & 15)) << 3); }
+// V^T tile: element offset of (d row, 8-byte chunk c in 0..15) of 64 kv.
+__device__ __forceinline__ int vt_off(int d, int c) { return d * kBKV + ((c ^ (d & 15)) << 2); }
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
+
+// q/k/v/o: row r of sequence b is row b*S + r; head h of q/o starts at column
+// h*128, kv head j of k/v at column j*128 (leading dimensions ldq/ldk/ldv/ldo).
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
+    const bf16_t *__restrict__ q, int ldq, const bf16_t *__restrict__ k, int ldk,
+    const bf16_t *__restrict__ v, int ldv, bf16_t *__restrict__ o, int ldo, int S, int Hq,
+    int group, float scale_log2) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  bf16_t *ks = lds;
+  bf16_t *vts = lds + kKElems;
+
+  // Grid (head, sequence, query block): blocks are dispatched x-fastest, so
+  // every head's longest causal rows (the last query block) go first.
+  const int n_qb = (S + kBQ - 1) / kBQ;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int qb = n_qb - 1 - (int)blockIdx.z;
+  const int kvh = h / group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 4;    // 0..3
+  const int l16 = lane & 15;  // 0..15
+
+  const size_t seq0 = (size_t)b * S;
+  const bf16_t *kbase = k + seq0 * ldk + (size_t)kvh * kHd;
+  const bf16_t *vbase = v + seq0 * ldv + (size_t)kvh * kHd;
+
+  // Query rows of this wave: q0 + 16*nb + l16 (nb = 0, 1).
+  const int q0 = qb * kBQ + wave * 32;
+
+  // Q fragments (B operand of S^T = K Q^T): lane holds Q[q][32kk + 8g .. +8].
+  bf16x8 qf[2][4];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    int qr = q0 + 16 * nb + l16;
+    qr = qr < S ? qr : S - 1;
+    const bf16_t *qrow = q + (seq0 + qr) * ldq + (size_t)h * kHd + 8 * g;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qf[nb][kk] = *reinterpret_cast<const bf16x8 *>(qrow + 32 * kk);
+  }
+
+  f32x4 oacc[8][2];  // O^T blocks: d block jd, query block nb
+#pragma unroll
+  for (int jd = 0; jd < 8; ++jd)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) oacc[jd][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY};  // running max (log2 units) of row q
+  float l_part[2] = {0.f, 0.f};              // this lane's share of the row sum
+
+  // kv blocks up to the last query row of the workgroup (causal).
+  const int q_last = min(S, (qb + 1) * kBQ) - 1;
+  const int n_kvb = q_last / kBKV + 1;
+
+  for (int kb = 0; kb < n_kvb; ++kb) {
+    const int kv0 = kb * kBKV;
+    __syncthreads();  // previous block's K / V^T reads are done
+    // K tile: 64 rows x 16 chunks of 16 B; thread covers chunks t + 256 i.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kThreads * i;
+      const int kr = c >> 4, ch = c & 15;
+      int src = kv0 + kr;
+      src = src < S ? src : S - 1;
+      const u32x4 val = *reinterpret_cast<const u32x4 *>(kbase + (size_t)src * ldk + 8 * ch);
+      *reinterpret_cast<u32x4 *>(ks + k_off(kr, ch)) = val;
+    }
+    // V^T tile: lane = kv row, wave w + 4i picks 8 d columns; 8 transposed writes.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = 8 * (wave + kWaves * i);
+      int src = kv0 + lane;
+      src = src < S ? src : S - 1;
+      const u32x4 val = *reinterpret_cast<const u32x4 *>(vbase + (size_t)src * ldv + d0);
+      const int kc = lane >> 2, kin = lane & 3;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w32 = val[e >> 1];
+        const bf16_t hv = (e & 1) ? (bf16_t)(w32 >> 16) : (bf16_t)(w32 & 0xffffu);
+        vts[vt_off(d0 + e, kc) + kin] = hv;
+      }
+    }
+    __syncthreads();
+
+    // S^T = K Q^T for 4 kv blocks x 2 query blocks.
+    f32x4 st[4][2];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) st[c][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x8 kf[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        kf[c] = *reinterpret_cast<const bf16x8 *>(ks + k_off(16 * c + l16, 4 * kk + g));
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) st[c][nb] = mfma_bf16(kf[c], qf[nb][kk], st[c][nb]);
+    }
+
+    // Online softmax.  st[c][nb][r] = score of (query q0 + 16nb + l16,
+    // kv kv0 + 16c + 4g + r).
+    u32x4 pf[2][2];  // P fragments: [nb][32-row kv step]
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int qrow = q0 + 16 * nb + l16;
+      float s[16];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kv = kv0 + 16 * c + 4 * g + r;
+          float x = st[c][nb][r] * scale_log2;
+          x = (kv <= qrow && kv < S) ? x : -INFINITY;
+          s[4 * c + r] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_run[nb], mloc);
+      // Rows with no valid score yet keep m = -inf; exp2(-inf - -inf) would be NaN.
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run[nb] - m_use);
+      m_run[nb] = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = fast_exp2(s[i] - m_use);
+        s[i] = p;
+        psum += p;
+      }
+      l_part[nb] = l_part[nb] * alpha + psum;
+#pragma unroll
+      for (int jd = 0; jd < 8; ++jd) oacc[jd][nb] = oacc[jd][nb] * alpha;
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        // k slots 0..3: kv block 2 ks2 (rows 4g + r); slots 4..7: block 2 ks2 + 1.
+        const float *a0 = s + 4 * (2 * ks2);
+        const float *a1 = s + 4 * (2 * ks2 + 1);
+        pf[nb][ks2] = u32x4{pack_bf16(a0[0], a0[1]), pack_bf16(a0[2], a0[3]),
+                            pack_bf16(a1[0], a1[1]), pack_bf16(a1[2], a1[3])};
+      }
+    }
+
+    // O^T += V^T P^T: d blocks jd, 32-row kv steps ks2.
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+#pragma unroll
+      for (int jd = 0; jd < 8; ++jd) {
+        const int dr = 16 * jd + l16;
+        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vts + vt_off(dr, 8 * ks2 + g));
+        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vts + vt_off(dr, 8 * ks2 + 4 + g));
+        const u32x4 vv = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          oacc[jd][nb] = mfma_bf16(vf, __builtin_bit_cast(bf16x8, pf[nb][ks2]), oacc[jd][nb]);
+      }
+    }
+  }
+
+  // Normalise by the row sum and store: lane holds O[q][16 jd + 4g + r].
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    float l = l_part[nb];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const float inv = 1.0f / fmaxf(l, 1e-30f);
+    const int qrow = q0 + 16 * nb + l16;
+    if (qrow < S) {
+      bf16_t *orow = o + (seq0 + qrow) * ldo + (size_t)h * kHd + 4 * g;
+#pragma unroll
+      for (int jd = 0; jd < 8; ++jd) {
+        const f32x4 a = oacc[jd][nb];
+        *reinterpret_cast<u32x2 *>(orow + 16 * jd) =
+            u32x2{pack_bf16(a[0] * inv, a[1] * inv), pack_bf16(a[2] * inv, a[3] * inv)};
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace prichs
+
+using namespace prichs;
+
+extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k, size_t ldk,
+                                        const void *v, size_t ldv, void *o, size_t ldo,
+                                        size_t batch, size_t seq_len, size_t n_heads,
+                                        size_t n_kv_heads, size_t head_dim, int dtype,
+                                        void *stream) {
+  PRICHS_REQUIRE(dtype == PRICHS_DTYPE_BF16, "attention: only bf16 is supported (dtype=%d)", dtype);
+  if (head_dim != (size_t)kHd)
+    return fail(PRICHS_ERR_UNSUPPORTED, "attention: head_dim=%zu (only %d is supported)",
+                head_dim, kHd);
+  PRICHS_REQUIRE(n_heads >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0,
+                 "attention: n_heads=%zu must be a positive multiple of n_kv_heads=%zu",
+                 n_heads, n_kv_heads);
+  PRICHS_REQUIRE(ldq >= n_heads * head_dim && ldo >= n_heads * head_dim &&
+                     ldk >= n_kv_heads * head_dim && ldv >= n_kv_heads * head_dim,
+                 "attention: leading dimensions too small");
+  PRICHS_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0,
+                 "attention: leading dimensions must be multiples of 8 elements");
+  PRICHS_REQUIRE(batch * seq_len <= (size_t)INT32_MAX && n_heads <= 65535 && batch <= 65535 &&
+                     ldq <= (size_t)INT32_MAX && ldk <= (size_t)INT32_MAX &&
+                     ldv <= (size_t)INT32_MAX && ldo <= (size_t)INT32_MAX,
+                 "attention: shape too large");
+  if (batch == 0 || seq_len == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(q && k && v && o, "attention: null pointer argument");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                       reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
+  PRICHS_REQUIRE(al % 16 == 0, "attention: q/k/v/o must be 16-byte aligned");
+  const int n_qb = (int)cdiv(seq_len, (size_t)kBQ);
+  const float scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
+  PRICHS_REQUIRE(n_qb <= 65535, "attention: seq_len too large");
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)n_heads, (unsigned)batch, (unsigned)n_qb),
+                     dim3(kThreads), kLdsBytes, as_stream(stream),
+                     static_cast<const bf16_t *>(q), (int)ldq, static_cast<const bf16_t *>(k),
+                     (int)ldk, static_cast<const bf16_t *>(v), (int)ldv,
+                     static_cast<bf16_t *>(o), (int)ldo, (int)seq_len, (int)n_heads,
+                     (int)(n_heads / n_kv_heads), scale_log2);
+  PRICHS_LAUNCH_CHECK("attention launch");
+  return PRICHS_OK;
+}

@@ -4,6 +4,8 @@
 // All loads/stores are 16-byte vectors along the contiguous dimension where
 // the shape allows it (one wave64 sweeps 1 KiB per instruction), with scalar
 // fallbacks for ragged shapes.
+#include <cmath>
+
 #include "common.hpp"
 
 namespace prichs {
@@ -185,8 +187,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT *__restrict__ x,
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void rope_kernel(T *__restrict__ qk, const float *__restrict__ cs,
                                                    const float *__restrict__ sn, long long rows,
-                                                   int seq_len, int H, int hd, int pos_offset,
-                                                   float sign) {
+                                                   long long ld, int seq_len, int H, int hd,
+                                                   int pos_offset, float sign) {
 #pragma clang fp contract(off)
   const int half = hd / 2;
   const int per_row = VEC ? half / 4 : half;  // threads per (row, head)
@@ -196,8 +198,9 @@ __global__ __launch_bounds__(256) void rope_kernel(T *__restrict__ qk, const flo
   const long long rh = gid / per_row;
   const int q = (int)(gid - rh * per_row);
   const long long row = rh / H;
+  const int hh = (int)(rh - row * H);
   const int pos = (int)(row % seq_len) + pos_offset;
-  T *base = qk + rh * hd;
+  T *base = qk + row * ld + (long long)hh * hd;
   const float *cr = cs + (size_t)pos * half;
   const float *sr = sn + (size_t)pos * half;
   if (VEC) {
@@ -283,16 +286,16 @@ void launch_combine_t(const void *y, const int32_t *idx, const float *w, const i
 }
 
 template <typename T>
-void launch_rope_t(void *qk, const float *cs, const float *sn, size_t batch, size_t seq, size_t H,
-                   size_t hd, size_t pos_off, float sign, hipStream_t s) {
+void launch_rope_t(void *qk, size_t ld, const float *cs, const float *sn, size_t batch, size_t seq,
+                   size_t H, size_t hd, size_t pos_off, float sign, hipStream_t s) {
   const size_t half = hd / 2;
-  const bool vec = half % 4 == 0 && aligned16(static_cast<T *>(qk)) && aligned16(cs) &&
-                   aligned16(sn);
+  const bool vec = half % 4 == 0 && (ld * sizeof(T)) % 16 == 0 &&
+                   aligned16(static_cast<T *>(qk)) && aligned16(cs) && aligned16(sn);
   const long long rows = (long long)(batch * seq);
   const size_t n = (size_t)rows * H * (vec ? half / 4 : half);
   auto kern = vec ? rope_kernel<T, true> : rope_kernel<T, false>;
   hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(256), 0, s, static_cast<T *>(qk), cs, sn, rows,
-                     (int)seq, (int)H, (int)hd, (int)pos_off, sign);
+                     (long long)ld, (int)seq, (int)H, (int)hd, (int)pos_off, sign);
 }
 
 }  // namespace
@@ -353,10 +356,11 @@ extern "C" int prichs_rmsnorm_forward(const void *x, int x_dtype, const float *w
   return PRICHS_OK;
 }
 
-extern "C" int prichs_rope_forward(void *qk, int dtype, const float *cos_cache,
-                                   const float *sin_cache, size_t cache_rows, size_t batch,
-                                   size_t seq_len, size_t n_heads, size_t head_dim,
-                                   size_t pos_offset, int sign, void *stream) {
+extern "C" int prichs_rope_forward_ld(void *qk, size_t row_stride, int dtype,
+                                      const float *cos_cache, const float *sin_cache,
+                                      size_t cache_rows, size_t batch, size_t seq_len,
+                                      size_t n_heads, size_t head_dim, size_t pos_offset, int sign,
+                                      void *stream) {
   PRICHS_REQUIRE(dtype_ok(dtype), "rope: bad dtype %d", dtype);
   PRICHS_REQUIRE(head_dim >= 2 && head_dim % 2 == 0, "rope: head_dim=%zu must be even",
                  head_dim);
@@ -366,16 +370,95 @@ extern "C" int prichs_rope_forward(void *qk, int dtype, const float *cos_cache,
                  cache_rows);
   PRICHS_REQUIRE(cache_rows <= (size_t)INT32_MAX && n_heads <= (size_t)INT32_MAX,
                  "rope: shape too large");
+  PRICHS_REQUIRE(row_stride >= n_heads * head_dim, "rope: row_stride=%zu < n_heads*head_dim",
+                 row_stride);
   if (batch == 0 || seq_len == 0 || n_heads == 0) return PRICHS_OK;
   PRICHS_REQUIRE(qk && cos_cache && sin_cache, "rope: null pointer argument");
   hipStream_t s = as_stream(stream);
   if (dtype == PRICHS_DTYPE_BF16)
-    launch_rope_t<bf16_t>(qk, cos_cache, sin_cache, batch, seq_len, n_heads, head_dim, pos_offset,
-                          (float)sign, s);
+    launch_rope_t<bf16_t>(qk, row_stride, cos_cache, sin_cache, batch, seq_len, n_heads,
+                          head_dim, pos_offset, (float)sign, s);
   else
-    launch_rope_t<float>(qk, cos_cache, sin_cache, batch, seq_len, n_heads, head_dim, pos_offset,
-                         (float)sign, s);
+    launch_rope_t<float>(qk, row_stride, cos_cache, sin_cache, batch, seq_len, n_heads, head_dim,
+                         pos_offset, (float)sign, s);
   PRICHS_LAUNCH_CHECK("rope launch");
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_rope_forward(void *qk, int dtype, const float *cos_cache,
+                                   const float *sin_cache, size_t cache_rows, size_t batch,
+                                   size_t seq_len, size_t n_heads, size_t head_dim,
+                                   size_t pos_offset, int sign, void *stream) {
+  return prichs_rope_forward_ld(qk, n_heads * head_dim, dtype, cos_cache, sin_cache, cache_rows,
+                                batch, seq_len, n_heads, head_dim, pos_offset, sign, stream);
+}
+
+// out = a + b element-wise (crates/prichs-core/src/ops.rs:250-267), f32
+// arithmetic, operands and result each bf16 or f32.
+template <typename A, typename B, typename O>
+__global__ __launch_bounds__(256) void add_kernel(const A *__restrict__ a, const B *__restrict__ b,
+                                                  O *__restrict__ out, long long n8) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  const V8 va = ld8(a + 8 * i), vb = ld8(b + 8 * i);
+  V8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r.v[j] = va.v[j] + vb.v[j];
+  st8(out + 8 * i, r);
+}
+
+template <typename A, typename B, typename O>
+void launch_add_t(const void *a, const void *b, void *out, size_t n, hipStream_t s) {
+  const long long n8 = (long long)(n / 8);
+  hipLaunchKernelGGL((add_kernel<A, B, O>), dim3(grid_for((size_t)n8)), dim3(256), 0, s,
+                     static_cast<const A *>(a), static_cast<const B *>(b), static_cast<O *>(out),
+                     n8);
+}
+
+extern "C" int prichs_add(const void *a, int a_dtype, const void *b, int b_dtype, void *out,
+                          int out_dtype, size_t n, void *stream) {
+  PRICHS_REQUIRE(dtype_ok(a_dtype) && dtype_ok(b_dtype) && dtype_ok(out_dtype), "add: bad dtype");
+  PRICHS_REQUIRE(n % 8 == 0, "add: n=%zu must be a multiple of 8", n);
+  if (n == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(a && b && out, "add: null pointer argument");
+  PRICHS_REQUIRE(((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                   reinterpret_cast<uintptr_t>(out)) & 15) == 0,
+                 "add: operands must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  const int key = a_dtype * 4 + b_dtype * 2 + out_dtype;
+  switch (key) {
+    case 0: launch_add_t<float, float, float>(a, b, out, n, s); break;
+    case 1: launch_add_t<float, float, bf16_t>(a, b, out, n, s); break;
+    case 2: launch_add_t<float, bf16_t, float>(a, b, out, n, s); break;
+    case 3: launch_add_t<float, bf16_t, bf16_t>(a, b, out, n, s); break;
+    case 4: launch_add_t<bf16_t, float, float>(a, b, out, n, s); break;
+    case 5: launch_add_t<bf16_t, float, bf16_t>(a, b, out, n, s); break;
+    case 6: launch_add_t<bf16_t, bf16_t, float>(a, b, out, n, s); break;
+    default: launch_add_t<bf16_t, bf16_t, bf16_t>(a, b, out, n, s); break;
+  }
+  PRICHS_LAUNCH_CHECK("add launch");
+  return PRICHS_OK;
+}
+
+// RoPE tables on the host (crates/prichs-core/src/backward.rs:136-157):
+// freq_i = 1 / theta^((2i)/hd) with libm powf, angle = (t as f32) * freq_i,
+// cos/sin with libm cosf/sinf -- the functions Rust's f32 methods call.
+extern "C" int prichs_rope_cache(size_t max_seq_len, size_t head_dim, float theta,
+                                 float *cos_out, float *sin_out) {
+  PRICHS_REQUIRE(head_dim >= 2 && head_dim % 2 == 0, "rope_cache: head_dim=%zu must be even",
+                 head_dim);
+  PRICHS_REQUIRE(cos_out && sin_out, "rope_cache: null pointer argument");
+  PRICHS_REQUIRE(max_seq_len <= ((size_t)1 << 31), "rope_cache: max_seq_len too large");
+  const size_t half = head_dim / 2;
+  for (size_t i = 0; i < half; ++i) {
+    volatile float exponent = (float)(2 * i) / (float)head_dim;
+    const float freq = 1.0f / powf(theta, exponent);
+    for (size_t t = 0; t < max_seq_len; ++t) {
+      volatile float angle = (float)t * freq;
+      cos_out[t * half + i] = cosf(angle);
+      sin_out[t * half + i] = sinf(angle);
+    }
+  }
   return PRICHS_OK;
 }
 

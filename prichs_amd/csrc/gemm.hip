@@ -67,8 +67,15 @@ struct TileMap {
   int offs[kMaxGroups + 1];    // offsets[] of the launch (row range of each group)
 };
 
-__device__ inline void build_tile_map(TileMap &tm, const int32_t *offsets, int G, int BM) {
-  if (threadIdx.x == 0) {
+// offsets == nullptr is the dense case: one group of dense_m rows (G == 1).
+__device__ inline void build_tile_map(TileMap &tm, const int32_t *offsets, int G, int BM,
+                                      int dense_m) {
+  if (threadIdx.x == 0 && offsets == nullptr) {
+    tm.prefix[0] = 0;
+    tm.offs[0] = 0;
+    tm.prefix[1] = (dense_m + BM - 1) / BM;
+    tm.offs[1] = dense_m;
+  } else if (threadIdx.x == 0) {
     int run = 0;
     for (int g = 0; g < G; ++g) {
       tm.prefix[g] = run;
@@ -204,7 +211,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
     bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
-    int G) {
+    int G, int dense_m) {
   constexpr int BM = Cf::BM, BN = Cf::BN, BK = Cf::BK, kStages = Cf::kStages;
   constexpr int WGN = Cf::WGN, WM = Cf::WM, WN = Cf::WN, MI = Cf::MI, NJ = Cf::NJ;
   constexpr int kRowsPerInst = Cf::kRowsPerInst, kInstA = Cf::kInstA, kInstB = Cf::kInstB;
@@ -213,7 +220,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
 
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   __shared__ TileMap tm;
-  build_tile_map(tm, offsets, G, BM);
+  build_tile_map(tm, offsets, G, BM, dense_m);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -424,10 +431,11 @@ template <bool GATEUP>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     const float *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const float *__restrict__ B, long long b_group_stride, int Np, int K,
-    float *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets, int G) {
+    float *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets, int G,
+    int dense_m) {
   extern __shared__ float ldsf[];
   __shared__ TileMap tm;
-  build_tile_map(tm, offsets, G, BM);
+  build_tile_map(tm, offsets, G, BM, dense_m);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -443,8 +451,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     const int mt = tile / n_tiles;
     const int nt = tile - mt * n_tiles;
     const int g = find_group(tm, G, mt);
-    const int row0 = offsets[g];
-    const int mg = offsets[g + 1] - row0;
+    const int row0 = tm.offs[g];
+    const int mg = tm.offs[g + 1] - row0;
     const int m0 = (mt - tm.prefix[g]) * BM;
     const int n0 = nt * BN;
     const float *Bg = B + (long long)g * b_group_stride;
@@ -598,7 +606,7 @@ template <typename T> void pack_down_impl(const float *down, size_t d, size_t f,
 template <class Cf, bool GATEUP>
 int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                 int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
-                size_t max_rows, int cus, hipStream_t s) {
+                int dense_m, size_t max_rows, int cus, hipStream_t s) {
   // Persistent grid: one workgroup per CU (the LDS ring allows one), fewer
   // when the launch has fewer tiles.
   const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN);
@@ -613,22 +621,23 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
   }
   hipLaunchKernelGGL((bf16_gemm_kernel<Cf, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
-                     b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G);
+                     b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G, dense_m);
   PRICHS_LAUNCH_CHECK("grouped gemm launch");
   return PRICHS_OK;
 }
 
 int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, const void *B,
                    long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
-                   const int32_t *offsets, int G, size_t max_rows, int dtype, hipStream_t s) {
+                   const int32_t *offsets, int G, int dense_m, size_t max_rows, int dtype,
+                   hipStream_t s) {
   const int cus = device_cu_count();
   if (cus <= 0) return fail(PRICHS_ERR_HIP, "grouped gemm: cannot query the device");
   if (dtype == PRICHS_DTYPE_BF16) {
     if (gateup)
       return launch_bf16<Bf16, true>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
-                                     offsets, G, max_rows, cus, s);
+                                     offsets, G, dense_m, max_rows, cus, s);
     return launch_bf16<Bf16Down, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
-                                        offsets, G, max_rows, cus, s);
+                                        offsets, G, dense_m, max_rows, cus, s);
   } else {
     const size_t ub = (max_rows / fp::BM + G) * (size_t)(Np / fp::BN);
     const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus * 4));
@@ -636,7 +645,7 @@ int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, c
     hipLaunchKernelGGL(kern, dim3(grid), dim3(fp::kThreads), fp::kLdsBytes, s,
                        static_cast<const float *>(A), a_rows, lda,
                        static_cast<const float *>(B), b_stride, Np, K,
-                       static_cast<float *>(Cp), ldc, n_store, offsets, G);
+                       static_cast<float *>(Cp), ldc, n_store, offsets, G, dense_m);
   }
   PRICHS_LAUNCH_CHECK("grouped gemm launch");
   return PRICHS_OK;
@@ -692,7 +701,7 @@ extern "C" int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_t
   PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX, "gate_up: max_rows too large");
   const size_t np = gate_up_np(f, dtype);
   return launch_grouped(true, x, row_token, (int)d, w_packed, (long long)(np * d), (int)np,
-                        (int)d, act, (int)f, (int)f, offsets, (int)G, max_rows, dtype,
+                        (int)d, act, (int)f, (int)f, offsets, (int)G, 0, max_rows, dtype,
                         as_stream(stream));
 }
 
@@ -706,6 +715,39 @@ extern "C" int prichs_grouped_down(const void *act, const int32_t *offsets, size
   PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX, "down: max_rows too large");
   const size_t np = roundup(d, kPadRowsDown);
   return launch_grouped(false, act, nullptr, (int)f, w_packed, (long long)(np * f), (int)np,
-                        (int)f, y, (int)d, (int)d, offsets, (int)G, max_rows, dtype,
+                        (int)f, y, (int)d, (int)d, offsets, (int)G, 0, max_rows, dtype,
+                        as_stream(stream));
+}
+
+extern "C" size_t prichs_packed_weight_elems(size_t K, size_t N, int dtype) {
+  if (!dtype_ok(dtype)) return 0;
+  return roundup(N, kPadRowsDown) * K;
+}
+
+extern "C" int prichs_pack_weight(const float *w, size_t K, size_t N, int dtype,
+                                  void *packed_out) {
+  // The layout of a packed down projection: [roundup(N, 256)][K] = W^T.
+  if (int rc = check_gemm_shape(N, K, dtype, "pack_weight")) return rc;
+  PRICHS_REQUIRE(w && packed_out, "pack_weight: null pointer argument");
+  if (dtype == PRICHS_DTYPE_BF16)
+    pack_down_impl<bf16_t>(w, N, K, packed_out);
+  else
+    pack_down_impl<float>(w, N, K, packed_out);
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_gemm(const void *a, size_t lda, size_t M, size_t K, const void *w_packed,
+                           size_t N, void *c, size_t ldc, int dtype, void *stream) {
+  if (int rc = check_gemm_shape(N, K, dtype, "gemm")) return rc;
+  PRICHS_REQUIRE(lda >= K && ldc >= N, "gemm: lda=%zu < K=%zu or ldc=%zu < N=%zu", lda, K, ldc, N);
+  PRICHS_REQUIRE(M <= (size_t)INT32_MAX && lda <= (size_t)INT32_MAX && ldc <= (size_t)INT32_MAX &&
+                     M * lda <= (size_t)UINT32_MAX,
+                 "gemm: M=%zu or leading dimensions too large", M);
+  PRICHS_REQUIRE(lda % 8 == 0 && ldc % 4 == 0, "gemm: lda must be a multiple of 8, ldc of 4");
+  if (M == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(a && w_packed && c, "gemm: null pointer argument");
+  const size_t np = roundup(N, kPadRowsDown);
+  return launch_grouped(false, a, nullptr, (int)lda, w_packed, (long long)(np * K), (int)np,
+                        (int)K, c, (int)ldc, (int)N, nullptr, 1, (int)M, M, dtype,
                         as_stream(stream));
 }

@@ -180,3 +180,55 @@ def rope_(qk, cos, sin, cache_rows, batch, seq_len, pos_offset=0, sign=1, stream
                                     cache_rows, batch, seq_len, H, hd, pos_offset, sign,
                                     _stream(stream)))
     return qk
+
+
+# ------------------------------------------------------- block sub-layers --
+def pack_weight(w: np.ndarray, dtype) -> np.ndarray:
+    """prichs_pack_weight (host): W [K, N] -> packed [roundup(N, 256), K]."""
+    lib = L.load()
+    code = dtype_code(dtype)
+    K, N = w.shape
+    n = lib.prichs_packed_weight_elems(K, N, code)
+    out = np.empty(n, dtype=_np_dtype(code))
+    wc = np.ascontiguousarray(w, dtype=np.float32)
+    L.check(lib.prichs_pack_weight(wc.ctypes.data, K, N, code, out.ctypes.data))
+    return out.reshape(-1, K)
+
+
+def gemm(a, w_packed, N, out=None, stream=None):
+    """prichs_gemm: C[M, N] = A[M, K] @ W (W packed by pack_weight / to_device_packed)."""
+    lib = L.load()
+    a = _dev(a)
+    M, K = a.shape
+    if out is None:
+        out = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    L.check(lib.prichs_gemm(_p(a), K, M, K, _p(w_packed), N, _p(out), out.stride(0),
+                            dtype_code(a), _stream(stream)))
+    return out
+
+
+def add(a, b, out_dtype=None, stream=None):
+    """prichs_add: a + b in f32 arithmetic."""
+    lib = L.load()
+    a, b = _dev(a), _dev(b)
+    out = torch.empty(a.shape, dtype=out_dtype or a.dtype, device=a.device)
+    L.check(lib.prichs_add(_p(a), dtype_code(a), _p(b), dtype_code(b), _p(out), dtype_code(out),
+                           a.numel(), _stream(stream)))
+    return out
+
+
+def attention(q, k, v, batch, seq_len, n_heads, n_kv_heads, head_dim=128, out=None,
+              stream=None):
+    """prichs_attention_forward on 2-D row views (rows = batch * seq_len; q/k/v may
+    be column slices of one fused buffer: their row strides are passed)."""
+    lib = L.load()
+    if out is None:
+        out = torch.empty((batch * seq_len, n_heads * head_dim), dtype=q.dtype, device=q.device)
+    for t in (q, k, v, out):
+        if t.stride(1) != 1:
+            raise ValueError("attention operands need unit column stride")
+    L.check(lib.prichs_attention_forward(_p(q), q.stride(0), _p(k), k.stride(0), _p(v),
+                                         v.stride(0), _p(out), out.stride(0), batch, seq_len,
+                                         n_heads, n_kv_heads, head_dim, dtype_code(q),
+                                         _stream(stream)))
+    return out

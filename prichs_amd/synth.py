@@ -182,3 +182,92 @@ def config_inputs(cfg: int, seed: int = 0, **overrides) -> MoEInputs:
     c = dict(CONFIGS[cfg])
     c.update(overrides)
     return make_moe_inputs(seed=seed, name=f"config{cfg}", **c)
+
+
+@dataclass
+class BlockInputs:
+    """One PrichsBlock's inputs (crates/prichs-model/src/block.rs:15-48) for
+    `batch` independent sequences of `seq_len` rows, reference layouts, f32.
+
+    x [batch * seq_len, d]; wq/wo [d, d]; wk/wv [d, n_kv_heads * head_dim];
+    input_norm/post_norm [d]; cos/sin the RoPE cache [cache_rows, head_dim/2]
+    (crates/prichs-core/src/backward.rs:136-157) for rope_theta; moe the
+    MoE sub-layer's MoEInputs (its x is unused).
+    """
+
+    name: str
+    batch: int
+    seq_len: int
+    d: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    rope_theta: float
+    eps: float
+    dtype: str
+    x: np.ndarray
+    input_norm: np.ndarray
+    post_norm: np.ndarray
+    wq: np.ndarray
+    wk: np.ndarray
+    wv: np.ndarray
+    wo: np.ndarray
+    cos: np.ndarray
+    sin: np.ndarray
+    moe: MoEInputs
+
+
+def rope_cache(max_seq_len: int, head_dim: int, theta: float):
+    """(cos, sin) RoPE tables [max_seq_len * head_dim/2] from the library's host
+    function prichs_rope_cache (backward.rs:136-157 with libm)."""
+    import ctypes as C
+
+    from . import _lib
+
+    half = head_dim // 2
+    cos = np.empty(max_seq_len * half, np.float32)
+    sin = np.empty(max_seq_len * half, np.float32)
+    _lib.check(_lib.load().prichs_rope_cache(max_seq_len, head_dim, C.c_float(theta),
+                                             cos.ctypes.data, sin.ctypes.data))
+    return cos, sin
+
+
+def make_block_inputs(batch: int = 4, seq_len: int = 2048, d: int = 1536, n_heads: int = 12,
+                      n_kv_heads: int = 3, f: int = 1280, E: int = 8, k: int = 2,
+                      n_shared: int = 1, rope_theta: float = 500000.0, dtype: str = "bf16",
+                      w_std: float = 0.02, seed: int = 0, name: str = "config5",
+                      cos_sin=None) -> BlockInputs:
+    """Configuration 5 by default: 4 x 2048 rows of x ~ N(0,1), every weight
+    ~ N(0, 0.02), norm weights ~ N(1, 0.02) (block.rs:25-26), router bias 0
+    (moe.rs:75), RoPE theta 500000; bf16 rounds every drawn tensor.
+    cos_sin may supply the RoPE cache (e.g. the oracle's glibc table)."""
+    g = SplitMixNormal(seed)
+    hd = d // n_heads
+    T = batch * seq_len
+    x = g.randn((T, d), 0.0, 1.0)
+    input_norm = g.randn((d,), 1.0, w_std)
+    post_norm = g.randn((d,), 1.0, w_std)
+    wq = g.randn((d, d), 0.0, w_std)
+    wk = g.randn((d, n_kv_heads * hd), 0.0, w_std)
+    wv = g.randn((d, n_kv_heads * hd), 0.0, w_std)
+    wo = g.randn((d, d), 0.0, w_std)
+    w_router = g.randn((d, E), 0.0, w_std)
+    gate, up, down = [], [], []
+    for _ in range(n_shared + E):
+        gate.append(g.randn((d, f), 0.0, w_std))
+        up.append(g.randn((d, f), 0.0, w_std))
+        down.append(g.randn((f, d), 0.0, w_std))
+    rnd = round_bf16 if dtype == "bf16" else (lambda a: np.ascontiguousarray(a, np.float32))
+    x, input_norm, post_norm = rnd(x), rnd(input_norm), rnd(post_norm)
+    wq, wk, wv, wo, w_router = rnd(wq), rnd(wk), rnd(wv), rnd(wo), rnd(w_router)
+    gate = [rnd(a) for a in gate]
+    up = [rnd(a) for a in up]
+    down = [rnd(a) for a in down]
+    moe = MoEInputs(name=name + "-moe", T=T, d=d, f=f, E=E, k=k, n_shared=n_shared, dtype=dtype,
+                    x=np.zeros((0, d), np.float32), w_router=w_router,
+                    router_bias=np.zeros(E, np.float32), gate=gate, up=up, down=down)
+    cos, sin = cos_sin if cos_sin is not None else rope_cache(max(seq_len, 1024), hd, rope_theta)
+    return BlockInputs(name=name, batch=batch, seq_len=seq_len, d=d, n_heads=n_heads,
+                       n_kv_heads=n_kv_heads, head_dim=hd, rope_theta=rope_theta, eps=1e-5,
+                       dtype=dtype, x=x, input_norm=input_norm, post_norm=post_norm, wq=wq,
+                       wk=wk, wv=wv, wo=wo, cos=cos, sin=sin, moe=moe)

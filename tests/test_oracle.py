@@ -274,3 +274,105 @@ def test_config1_golden_fixture(orc):
     np.testing.assert_array_equal(r["gw"], g["gw"])
     np.testing.assert_array_equal(r["out"][g["rows"]], g["out_rows"])
     assert float(np.abs(r["out"]).astype(np.float64).sum()) == float(g["out_abs_sum"])
+
+
+# ------------------------------------------------------------ attention --
+def _attention_f64(x, Hq, Hkv, wq, wk, wv, wo, cos, sin, pos_offset=0):
+    """Causal GQA softmax attention in float64 (attention.rs:56-176 semantics)."""
+    x = x.astype(np.float64)
+    S, d = x.shape
+    hd = d // Hq
+    q = (x @ wq.astype(np.float64)).reshape(S, Hq, hd)
+    k = (x @ wk.astype(np.float64)).reshape(S, Hkv, hd)
+    v = (x @ wv.astype(np.float64)).reshape(S, Hkv, hd)
+    c = cos.reshape(-1, hd // 2)[pos_offset:pos_offset + S, None, :].astype(np.float64)
+    s = sin.reshape(-1, hd // 2)[pos_offset:pos_offset + S, None, :].astype(np.float64)
+
+    def rope(t):
+        out = t.copy()
+        out[..., 0::2] = t[..., 0::2] * c - t[..., 1::2] * s
+        out[..., 1::2] = t[..., 0::2] * s + t[..., 1::2] * c
+        return out
+
+    q, k = rope(q), rope(k)
+    group = Hq // Hkv
+    cat = np.zeros((S, d))
+    probs = []
+    mask = np.tril(np.ones((S, S), bool))
+    for h in range(Hq):
+        sc = q[:, h] @ k[:, h // group].T / np.sqrt(hd)
+        sc = np.where(mask, sc, -np.inf)
+        p = np.exp(sc - sc.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        probs.append(p)
+        cat[:, h * hd:(h + 1) * hd] = p @ v[:, h // group]
+    return cat @ wo.astype(np.float64), cat, probs
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,hd,off", [(37, 4, 2, 16, 0), (64, 6, 3, 8, 5), (20, 2, 2, 32, 0)])
+def test_attention_float64(orc, S, Hq, Hkv, hd, off):
+    rng = np.random.default_rng(S * 7 + Hq)
+    d = Hq * hd
+    x = rng.standard_normal((S, d)).astype(np.float32)
+    wq = (0.2 * rng.standard_normal((d, d))).astype(np.float32)
+    wk = (0.2 * rng.standard_normal((d, Hkv * hd))).astype(np.float32)
+    wv = rng.standard_normal((d, Hkv * hd)).astype(np.float32)
+    wo = (0.2 * rng.standard_normal((d, d))).astype(np.float32)
+    cos, sin = orc.precompute_rope_cache(S + off + 3, hd, 500000.0)
+    out, cat = orc.attention_forward(x, Hq, Hkv, wq, wk, wv, wo, cos, sin, off, want_concat=True)
+    ref, ref_cat, probs = _attention_f64(x, Hq, Hkv, wq, wk, wv, wo, cos, sin, off)
+    assert rel_err(cat, ref_cat) < 2e-5
+    assert rel_err(out, ref) < 2e-5
+    # The reference's own invariants (engine.rs:2948-3029): softmax rows sum
+    # to 1 and the causal part above the diagonal is zero.
+    for p in probs:
+        assert np.abs(p.sum(1) - 1).max() < 1e-12 and not np.triu(p, 1).any()
+
+
+def test_attention_first_row_sees_only_itself(orc):
+    # Row 0 attends only to key 0, so its head output is v[0] exactly.
+    rng = np.random.default_rng(9)
+    S, Hq, Hkv, hd = 8, 2, 1, 8
+    d = Hq * hd
+    x = rng.standard_normal((S, d)).astype(np.float32)
+    eye = np.eye(d, dtype=np.float32)
+    wk = rng.standard_normal((d, hd)).astype(np.float32)
+    wv = rng.standard_normal((d, hd)).astype(np.float32)
+    cos, sin = orc.precompute_rope_cache(S, hd, 10000.0)
+    _, cat = orc.attention_forward(x, Hq, Hkv, eye, wk, wv, eye, cos, sin, want_concat=True)
+    v0 = orc.matmul_2d(x[:1], wv)[0]
+    np.testing.assert_array_equal(cat[0, :hd], v0)
+    np.testing.assert_array_equal(cat[0, hd:], v0)  # both query heads share kv head 0
+
+
+def test_rope_cache_library_matches_oracle(orc):
+    # The library's host table (prichs_rope_cache) is the one the GPU path uploads.
+    for theta, hd, S in [(500000.0, 128, 2048), (10000.0, 64, 1024), (10000.0, 6, 50)]:
+        c1, s1 = synth.rope_cache(S, hd, theta)
+        c2, s2 = orc.precompute_rope_cache(S, hd, theta)
+        np.testing.assert_array_equal(c1.view(np.uint32), c2.view(np.uint32))
+        np.testing.assert_array_equal(s1.view(np.uint32), s2.view(np.uint32))
+
+
+def test_block_forward_float64_reassembly(orc):
+    # Small block: 2 sequences x 24 rows, d = 64 (4 heads of 16), f = 64.
+    inp = synth.make_block_inputs(batch=2, seq_len=24, d=64, n_heads=4, n_kv_heads=2, f=64,
+                                  dtype="f32", name="mini-block", w_std=0.1)
+    r = orc.block_forward(inp)
+    x = inp.x.astype(np.float64)
+
+    def rms(a, w):
+        return a / np.sqrt((a * a).mean(1, keepdims=True) + inp.eps) * w
+
+    n1 = rms(x, inp.input_norm)
+    att = np.concatenate([
+        _attention_f64(n1[b * 24:(b + 1) * 24], 4, 2, inp.wq, inp.wk, inp.wv, inp.wo,
+                       inp.cos, inp.sin)[0] for b in range(2)])
+    assert rel_err(r["attn"], att) < 1e-4
+    x1 = x + att
+    assert rel_err(r["x1"], x1) < 1e-5
+    moe_in = synth.MoEInputs(**{**inp.moe.__dict__, "x": rms(x1, inp.post_norm).astype(np.float32),
+                                "T": 48})
+    ref_moe = orc.moe_forward(moe_in)
+    assert rel_err(r["moe"], _moe_float64(moe_in, ref_moe["sel"], ref_moe["gw"])) < 1e-4
+    assert rel_err(r["out"], x1 + r["moe"]) < 1e-6
