@@ -32,6 +32,8 @@ WORKLOADS = {
        "top-2, bf16 weights/activations, fp32 accumulate",
     3: "config3: as config2 with T=16384 and router bias skewing ~60% of assignments to experts 0-1",
     4: "config4: decode-shape MoE layer forward, T=32, d=1536, f=1280, bf16",
+    5: "config5: PrichsBlock forward (RMSNorm, GQA attention 12Q/3KV hd=128 with RoPE theta=500000, "
+       "residual, RMSNorm, MoE d=1536 f=1280 1+8 top-2, residual), 4 x 2048 tokens, bf16",
 }
 
 
@@ -89,6 +91,8 @@ def main():
 
     from prichs_amd import moe, synth
 
+    if args.config == 5:
+        return bench_block(args)
     log(f"bench: generating config {args.config} inputs")
     inp = synth.config_inputs(args.config)
     T, d, f, E, k, S = inp.T, inp.d, inp.f, inp.E, inp.k, inp.n_shared
@@ -171,6 +175,67 @@ def main():
         res["cpu_baseline"] = cpu_baseline(inp, args.cpu_seconds)
     else:
         res["cpu_baseline"] = None
+    eng.close()
+    print(json.dumps(res), flush=True)
+
+
+def bench_block(args):
+    """Config 5: one PrichsBlock forward per step (tokens/s), with the attention
+    kernel timed on its own over the same rows (causal TFLOP/s)."""
+    import torch
+
+    from prichs_amd import block, ops, synth
+
+    log("bench: generating config 5 inputs")
+    inp = synth.make_block_inputs()
+    B, S, d = inp.batch, inp.seq_len, inp.d
+    T = B * S
+    blk = block.PrichsBlock.from_inputs(inp)
+    eng = blk.engine
+    x = torch.from_numpy(inp.x).to("cuda").to(torch.bfloat16)
+    out = torch.empty((T, d), dtype=torch.bfloat16, device="cuda")
+    for _ in range(args.warmup):
+        eng.forward(x, B, S, out=out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.forward(x, B, S, out=out)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # Attention alone on the last forward's roped q/k/v, HIP events on the stream.
+    qkv = eng.stash()["qkv"]
+    Hq, Hkv, hd = inp.n_heads, inp.n_kv_heads, inp.head_dim
+    q, k, v = qkv[:, :Hq * hd], qkv[:, Hq * hd:(Hq + Hkv) * hd], qkv[:, (Hq + Hkv) * hd:]
+    ao = torch.empty((T, d), dtype=torch.bfloat16, device="cuda")
+    for _ in range(3):
+        ops.attention(q, k, v, B, S, Hq, Hkv, out=ao)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        ops.attention(q, k, v, B, S, Hq, Hkv, out=ao)
+    e1.record()
+    torch.cuda.synchronize()
+    att_ms = e0.elapsed_time(e1) / args.steps
+    att_flops = B * Hq * 4.0 * hd * S * (S + 1) / 2  # causal QK^T + PV
+    moe_flops = 6.0 * d * inp.moe.f * T * (inp.moe.k + 1)
+    proj_flops = 2.0 * T * d * (d + 2 * Hkv * hd) + 2.0 * T * d * d
+    ms = elapsed / args.steps * 1e3
+    res = {
+        "metric": "PrichsBlock forward tokens/s (config 5)",
+        "value": T * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded SplitMix64 + Box-Muller, seed 0)",
+        "config": {"workload": WORKLOADS[5], "batch": B, "seq_len": S, "d_model": d},
+        "roofline": {"kernel": "attn_fwd_kernel (causal GQA flash attention)", "bound": "mfma",
+                     "achieved": att_flops / (att_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": att_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                     "traffic": None, "algorithmic_flops_per_launch": att_flops,
+                     "avg_launch_ms": att_ms},
+        "block_tflops": (att_flops + moe_flops + proj_flops) / (ms * 1e-3) / 1e12,
+        "device": torch.cuda.get_device_name(0),
+        "cpu_baseline": None,
+    }
     eng.close()
     print(json.dumps(res), flush=True)
 
