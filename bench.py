@@ -79,6 +79,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 plain device copies of 1 GiB (known bytes) so that "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE can be scaled")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the MoE hot path "
@@ -91,6 +94,8 @@ def main():
 
     from prichs_amd import moe, synth
 
+    if args.copy_calibration:
+        copy_calibration()
     if args.config == 5:
         return bench_block(args)
     log(f"bench: generating config {args.config} inputs")
@@ -154,7 +159,9 @@ def main():
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": gu_tflops / peak,
-            "traffic": None,
+            "traffic": measured_traffic() if args.config == 2 else None,
+            "traffic_source": "profiles/pmc_config2_gate_up_traffic.txt (rocprofv3 --pmc "
+                              "FETCH_SIZE, WRITE_SIZE, copy-calibrated)" if args.config == 2 else None,
             "algorithmic_flops_per_launch": flops_gate_up,
             "avg_launch_ms": ms["gate_up"],
         },
@@ -177,6 +184,38 @@ def main():
         res["cpu_baseline"] = None
     eng.close()
     print(json.dumps(res), flush=True)
+
+
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """Three device-to-device copies of exactly COPY_BYTES (a plain copy kernel
+    whose FETCH_SIZE / WRITE_SIZE per dispatch should read COPY_BYTES)."""
+    import torch
+
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"bench: copy calibration, 3 x {COPY_BYTES} bytes")
+    del src, dst
+
+
+def measured_traffic():
+    """HBM bytes per gate/up launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_config2_gate_up_traffic.txt")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return float(line.split("=")[1].split()[0])
+    except OSError:
+        return None
+    return None
 
 
 def bench_block(args):
