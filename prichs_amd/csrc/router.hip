@@ -20,8 +20,13 @@ namespace prichs {
 
 namespace {
 
-constexpr int kRouterThreads = 256;
-constexpr int kRouterLdsBytes = 60 * 1024;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#ifndef PRICHS_ROUTER_THREADS
+#define PRICHS_ROUTER_THREADS 256
+#endif
+constexpr int kRouterThreads = PRICHS_ROUTER_THREADS;  // >= PRICHS_MAX_EXPERTS
+constexpr int kRouterLdsBytes = 60 * 1024;  // simple kernel: W chunk [E][kc + 4] f32
 
 int lanes_per_token_log2(int E) {
   int l = 0;
@@ -29,7 +34,7 @@ int lanes_per_token_log2(int E) {
   return l;
 }
 
-// Width of the router-weight chunk held in LDS as [E][kc + 4] f32.
+// Width of the router-weight chunk of the simple kernel.
 int router_chunk(int d, int E) {
   int kc = (kRouterLdsBytes / 4) / E - 4;
   kc = kc / 8 * 8;
@@ -37,86 +42,17 @@ int router_chunk(int d, int E) {
   return kc < dpad ? kc : dpad;
 }
 
-__device__ inline void load8(const float *p, float *v) {
-  const float4 a = *reinterpret_cast<const float4 *>(p);
-  const float4 b = *reinterpret_cast<const float4 *>(p + 4);
-  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-
-__device__ inline void load8(const bf16_t *p, float *v) {
-  const uint4 a = *reinterpret_cast<const uint4 *>(p);
-  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = __uint_as_float(w[i] << 16);
-    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-  }
-}
-
-template <typename XT, bool VEC>
-__global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
-    const XT *__restrict__ x, const float *__restrict__ w,
-    const float *__restrict__ bias, const float *__restrict__ concept,
-    int n_concept, int T, int d, int E, int k, int lpt_log2, int kc,
-    float *__restrict__ logits, int32_t *__restrict__ topk_idx,
-    float *__restrict__ topk_w, int32_t *__restrict__ block_counts) {
+// ---------------------------------------------------------------------------
+// Top-k gating of one token whose lpt lanes hold (raw, adj) of expert e = lane
+// index within the group (crates/prichs-core/src/ops.rs:219-248), then the
+// writes of idx / weights and the block's expert histogram.
+// ---------------------------------------------------------------------------
+__device__ inline void topk_epilogue(float acc, float adj, bool valid, int e, int t, int T, int E,
+                                     int k, int lpt, float *__restrict__ logits,
+                                     int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
+                                     int *cnt_s) {
 #pragma clang fp contract(off)
-  extern __shared__ float w_s[];  // [E][kc + 4]
-  __shared__ int cnt_s[PRICHS_MAX_EXPERTS];
-
-  const int lpt = 1 << lpt_log2;
-  const int tpb = kRouterThreads >> lpt_log2;
-  const int tid = threadIdx.x;
-  const int e = tid & (lpt - 1);
-  const int t = blockIdx.x * tpb + (tid >> lpt_log2);
-  const bool valid = (t < T) && (e < E);
-  const int kcp = kc + 4;
-  if (tid < E) cnt_s[tid] = 0;
-
-  // raw[t, e] = sum over k ascending of x[t, k] * W[k, e] (mul, then add).
-  float acc = 0.0f;
-  for (int k0 = 0; k0 < d; k0 += kc) {
-    const int n = min(kc, d - k0);
-    __syncthreads();
-    for (int i = tid; i < n * E; i += kRouterThreads) {
-      const int kk = i / E;
-      const int ee = i - kk * E;
-      w_s[ee * kcp + kk] = w[(size_t)(k0 + kk) * E + ee];
-    }
-    __syncthreads();
-    if (valid) {
-      const XT *xr = x + (size_t)t * d + k0;
-      const float *wr = w_s + e * kcp;
-      int kk = 0;
-      if (VEC) {
-        for (; kk + 8 <= n; kk += 8) {
-          float xv[8];
-          load8(xr + kk, xv);
-          const float4 w0 = *reinterpret_cast<const float4 *>(wr + kk);
-          const float4 w1 = *reinterpret_cast<const float4 *>(wr + kk + 4);
-          const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float p = xv[j] * wv[j];
-            acc = acc + p;
-          }
-        }
-      }
-      for (; kk < n; ++kk) {
-        const float p = Elem<XT>::load(xr + kk) * wr[kk];
-        acc = acc + p;
-      }
-    }
-  }
-
-  // adj = (raw + bias[e]) (+ concept[e]), moe.rs:126-133.
-  float adj = 0.0f;
-  if (valid) {
-    adj = acc + bias[e];
-    if (concept != nullptr && e < n_concept) adj = adj + concept[e];
-    if (logits != nullptr) logits[(size_t)t * E + e] = acc;
-  }
+  if (valid && logits != nullptr) logits[(size_t)t * E + e] = acc;
 
   int nan_any = valid && (adj != adj);
   for (int m = 1; m < lpt; m <<= 1) nan_any |= __shfl_xor(nan_any, m, lpt);
@@ -138,8 +74,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
           const int ov = __shfl_xor(cv, m, lpt);
           const float oval = __shfl_xor(cval, m, lpt);
           const int oidx = __shfl_xor(cidx, m, lpt);
-          const bool better =
-              ov && (!cv || oval > cval || (oval == cval && oidx < cidx));
+          const bool better = ov && (!cv || oval > cval || (oval == cval && oidx < cidx));
           if (better) {
             cv = ov;
             cval = oval;
@@ -151,29 +86,37 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
       }
     }
   } else {
-    // Some adjusted logit is NaN: replay the reference's small-slice stable
-    // sort (insertion sort, is_less(a, b) == a > b) on the group's values.
-    float vals[PRICHS_MAX_EXPERTS];
-    int ord[PRICHS_MAX_EXPERTS];
-    for (int i = 0; i < E; ++i) {
-      vals[i] = __shfl(adj, i, lpt);
-      ord[i] = i;
+    // Some adjusted logit is NaN.  The reference's small-slice stable sort is
+    // an insertion sort whose comparison (a > b) is false against a NaN, so a
+    // NaN never moves and nothing crosses it: the result is each NaN-free
+    // segment sorted stably in descending order, NaNs in place.  Position of
+    // expert e: its own index if NaN, else segment start + its rank in the
+    // segment.
+    const bool is_nan = valid && (adj != adj);
+    int s0 = 0, s1 = E;
+    for (int j = 0; j < lpt; ++j) {
+      const float vj = __shfl(adj, j, lpt);
+      const bool nj = j < E && (vj != vj);
+      if (nj && j < e) s0 = j + 1;
+      if (nj && j > e && s1 == E) s1 = j;
     }
-    for (int i = 1; i < E; ++i) {
-      const float vi = vals[i];
-      const int oi = ord[i];
-      int j = i;
-      while (j > 0 && vi > vals[j - 1]) {
-        vals[j] = vals[j - 1];
-        ord[j] = ord[j - 1];
-        --j;
-      }
-      vals[j] = vi;
-      ord[j] = oi;
+    int rank = 0;
+    for (int j = 0; j < lpt; ++j) {
+      const float vj = __shfl(adj, j, lpt);
+      if (j >= s0 && j < s1 && (vj > adj || (vj == adj && j < e))) ++rank;
     }
+    const int pos = is_nan ? e : s0 + rank;
 #pragma unroll
-    for (int s = 0; s < PRICHS_MAX_TOPK; ++s)
-      if (s < k) sel[s] = ord[s];
+    for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+      if (s < k) {
+        int who = 0;
+        for (int j = 0; j < lpt; ++j) {
+          const int pj = __shfl(pos, j, lpt);
+          if (j < E && pj == s) who = j;
+        }
+        sel[s] = who;
+      }
+    }
   }
 
   // Softmax over the RAW logits of the selected experts (ops.rs:233-245).
@@ -208,8 +151,304 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Staged router: the block's x rows and router weights go through
+// double-buffered LDS in K chunks of KC (coalesced 16-byte loads by all 256
+// threads, one chunk in flight while the previous one is summed), and each
+// lane then sums its (token, expert) dot product over k in ascending order,
+// product rounded then sum rounded -- the reference CPU GEMM's order
+// (crates/prichs-core/src/ops.rs:49-56).  LPT lanes per token (LPT >= E).
+// Requires d % 8 == 0 and 16-byte aligned x and W.
+// ---------------------------------------------------------------------------
+template <typename XT, int LPT, int KC> struct StagedRouter {
+  static constexpr int kTpb = kRouterThreads / LPT;  // tokens per block
+  static constexpr int kVe = 16 / (int)sizeof(XT);   // x elements per 16-byte load
+  static constexpr int kXStride = KC + 4;            // f32 x row in LDS (16-byte pad)
+  static constexpr int kWStride = KC + 4;            // W^T row in LDS
+  static constexpr int kXTot = kTpb * KC / kVe;      // x vectors per chunk
+  static constexpr int kXVec = (kXTot + kRouterThreads - 1) / kRouterThreads;
+  static constexpr int kWVec = (KC * LPT / 4 + kRouterThreads - 1) / kRouterThreads;
+  static constexpr size_t kXBytes = (size_t)kTpb * kXStride * sizeof(float);
+  static constexpr size_t kWBytes = (size_t)LPT * kWStride * sizeof(float);
+  static constexpr size_t kLds = 2 * (kXBytes + kWBytes);
+  static_assert(KC % 8 == 0 && (KC / kVe) > 0, "chunks of whole 16-byte vectors");
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Global -> registers: x rows tok0.. of chunk k0 and the chunk's W rows [n][E]
+// as float4s.  No load is predicated (a predicated load makes the compiler
+// drain every load in flight at the join): rows past T read row T-1, vectors
+// past the chunk re-read the chunk's last vector, and the values so fetched
+// are never summed.
+template <typename XT, int LPT, int KC>
+__device__ inline void router_fetch(const XT *__restrict__ x, const float *__restrict__ w,
+                                    int tid, int tok0, int T, int d, int E, int k0, int n,
+                                    u32x4 (&rx)[StagedRouter<XT, LPT, KC>::kXVec],
+                                    f32x4 (&rw)[StagedRouter<XT, LPT, KC>::kWVec]) {
+  using Cf = StagedRouter<XT, LPT, KC>;
+  constexpr int vpr = KC / Cf::kVe;
+#pragma unroll
+  for (int i = 0; i < Cf::kXVec; ++i) {
+    const int v = min(tid + kRouterThreads * i, Cf::kXTot - 1);
+    const int r = v / vpr, cv = v % vpr;
+    const int row = min(tok0 + r, T - 1);
+    const int col = min(cv * Cf::kVe, n - Cf::kVe);
+    rx[i] = *reinterpret_cast<const u32x4 *>(x + (size_t)row * d + k0 + col);
+  }
+  const int nw = n * E / 4;  // n is a multiple of 8, so whole float4s
+#pragma unroll
+  for (int i = 0; i < Cf::kWVec; ++i) {
+    const int v = min(tid + kRouterThreads * i, nw - 1);
+    rw[i] = *reinterpret_cast<const f32x4 *>(w + (size_t)k0 * E + 4 * v);
+  }
+}
+
+// Registers -> LDS: x as f32 rows (bf16 widened once here rather than by each
+// of the token's lanes), W transposed to [e][k].
+template <typename XT, int LPT, int KC>
+__device__ inline void router_stash(float *__restrict__ xs, float *__restrict__ ws, int tid, int E,
+                                    int n, const u32x4 (&rx)[StagedRouter<XT, LPT, KC>::kXVec],
+                                    const f32x4 (&rw)[StagedRouter<XT, LPT, KC>::kWVec]) {
+  using Cf = StagedRouter<XT, LPT, KC>;
+  constexpr int vpr = KC / Cf::kVe;
+#pragma unroll
+  for (int i = 0; i < Cf::kXVec; ++i) {
+    const int v = tid + kRouterThreads * i;
+    const int r = v / vpr, cv = v % vpr;
+    if (v < Cf::kXTot && cv * Cf::kVe < n) {
+      float *dst = xs + r * Cf::kXStride + cv * Cf::kVe;
+      if constexpr (sizeof(XT) == 2) {
+        f32x4 lo, hi;
+        lo.x = __uint_as_float(rx[i].x << 16);
+        lo.y = __uint_as_float(rx[i].x & 0xffff0000u);
+        lo.z = __uint_as_float(rx[i].y << 16);
+        lo.w = __uint_as_float(rx[i].y & 0xffff0000u);
+        hi.x = __uint_as_float(rx[i].z << 16);
+        hi.y = __uint_as_float(rx[i].z & 0xffff0000u);
+        hi.z = __uint_as_float(rx[i].w << 16);
+        hi.w = __uint_as_float(rx[i].w & 0xffff0000u);
+        *reinterpret_cast<f32x4 *>(dst) = lo;
+        *reinterpret_cast<f32x4 *>(dst + 4) = hi;
+      } else {
+        f32x4 v4;
+        v4.x = __uint_as_float(rx[i].x);
+        v4.y = __uint_as_float(rx[i].y);
+        v4.z = __uint_as_float(rx[i].z);
+        v4.w = __uint_as_float(rx[i].w);
+        *reinterpret_cast<f32x4 *>(dst) = v4;
+      }
+    }
+  }
+  const int nw = n * E / 4;
+#pragma unroll
+  for (int i = 0; i < Cf::kWVec; ++i) {
+    const int v = tid + kRouterThreads * i;
+    if (v < nw) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int f = 4 * v + j;  // flat index in [n][E]
+        const int kk = f / E, ee = f - kk * E;
+        ws[ee * Cf::kWStride + kk] = rw[i][j];
+      }
+    }
+  }
+}
+
+// acc + x[0]*w[0] + ... + x[3]*w[3], each product and each sum rounded in turn.
+__device__ inline float router_dot4(float acc, const float *xr, const float *wr) {
+#pragma clang fp contract(off)
+  const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr);
+  const f32x4 wv = *reinterpret_cast<const f32x4 *>(wr);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float p = xv[q] * wv[q];
+    acc = acc + p;
+  }
+  return acc;
+}
+
+// Sum over one whole chunk, fully unrolled so the chunk's LDS reads are issued
+// ahead of the dependent adds (at one wave per SIMD nothing else covers their
+// latency).  PRICHS_ROUTER_PIPE=1 instead pins a read-ahead interleave with
+// sched_group_barrier (masks: 0x100 LDS read, 0x2 VALU).  Either way the
+// arithmetic order is the reference's: each product rounded, then each sum.
+#ifndef PRICHS_ROUTER_PIPE
+#define PRICHS_ROUTER_PIPE 0
+#endif
+template <int KC>
+__device__ inline float router_dot_chunk(float acc, const float *xr, const float *wr) {
+#pragma clang fp contract(off)
+  constexpr int kG = KC / 4;
+#if PRICHS_ROUTER_PIPE
+  constexpr int kAhead = kG < 6 ? kG : 6;
+  __builtin_amdgcn_sched_barrier(0);
+#endif
+#pragma unroll
+  for (int g = 0; g < kG; ++g) {
+    const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr + 4 * g);
+    const f32x4 wv = *reinterpret_cast<const f32x4 *>(wr + 4 * g);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float p = xv[q] * wv[q];
+      acc = acc + p;
+    }
+  }
+#if PRICHS_ROUTER_PIPE
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * kAhead, 0);
+#pragma unroll
+  for (int g = 0; g < kG; ++g) {
+    __builtin_amdgcn_sched_group_barrier(0x2, 8, 0);
+    if (g + kAhead < kG) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#endif
+  return acc;
+}
+
+// waves_per_eu: the dynamic LDS holds a CU to a few blocks, so the compiler may
+// spend registers on the read-ahead.
+template <typename XT, int LPT, int KC>
+__global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(1, 3))) void
+router_topk_staged_kernel(
+    const XT *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
+    const float *__restrict__ concept, int n_concept, int T, int d, int E, int k,
+    float *__restrict__ logits, int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
+    int32_t *__restrict__ block_counts) {
+#pragma clang fp contract(off)
+  using Cf = StagedRouter<XT, LPT, KC>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ int cnt_s[PRICHS_MAX_EXPERTS];
+  float *const xs0 = reinterpret_cast<float *>(smem);
+  float *const ws0 = reinterpret_cast<float *>(smem + Cf::kXBytes);
+  constexpr size_t kBuf = (Cf::kXBytes + Cf::kWBytes) / sizeof(float);
+
+  const int tid = threadIdx.x;
+  const int e = tid & (LPT - 1);
+  const int tl = tid / LPT;
+  const int tok0 = blockIdx.x * Cf::kTpb;
+  const int t = tok0 + tl;
+  const bool valid = (t < T) && (e < E);
+  if (tid < E) cnt_s[tid] = 0;
+  const int n_chunks = (d + KC - 1) / KC;
+
+  // Register ring of kRing chunks in flight: with one wave per SIMD at the
+  // headline shape, nothing else hides HBM latency.
+  constexpr int kRing = 4;
+  u32x4 rx[kRing][Cf::kXVec];
+  f32x4 rw[kRing][Cf::kWVec];
+  auto chunk_len = [&](int c) { return min(KC, d - c * KC); };
+  // Chunks past the end are fetched as the last chunk (unpredicated loads).
+  auto fetch = [&](int c, u32x4(&rxs)[Cf::kXVec], f32x4(&rws)[Cf::kWVec]) {
+    const int cc = min(c, n_chunks - 1);
+    router_fetch<XT, LPT, KC>(x, w, tid, tok0, T, d, E, cc * KC, chunk_len(cc), rxs, rws);
+  };
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) fetch(j, rx[j], rw[j]);
+  router_stash<XT, LPT, KC>(xs0, ws0, tid, E, chunk_len(0), rx[0], rw[0]);
+  fetch(kRing, rx[0], rw[0]);
+  __syncthreads();
+
+  // Iteration c sums chunk c from LDS, stashes chunk c + 1 from its register
+  // slot into the other LDS buffer and refills that slot with chunk
+  // c + 1 + kRing.  The refill is issued on every path (only LDS work is
+  // guarded) so the compiler's wait before each stash counts exactly the
+  // loads issued after the slot's own.
+  float acc = 0.0f;
+  for (int c0 = 0; c0 < n_chunks; c0 += kRing) {
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) {
+      const int c = c0 + j;
+      const int jn = (j + 1) % kRing;  // slot holding chunk c + 1
+      if (valid && c < n_chunks) {
+        const int n = chunk_len(c);
+        const size_t off = (c & 1) * kBuf;
+        const float *xr = xs0 + off + tl * Cf::kXStride;
+        const float *wr = ws0 + off + e * Cf::kWStride;
+        if (n == KC) {
+          acc = router_dot_chunk<KC>(acc, xr, wr);
+        } else {
+          for (int kk = 0; kk < n; kk += 4) acc = router_dot4(acc, xr + kk, wr + kk);
+        }
+      }
+      if (c + 1 < n_chunks) {
+        const size_t noff = ((c + 1) & 1) * kBuf;
+        router_stash<XT, LPT, KC>(xs0 + noff, ws0 + noff, tid, E, chunk_len(c + 1), rx[jn],
+                                  rw[jn]);
+      }
+      fetch(c + 1 + kRing, rx[jn], rw[jn]);
+      __syncthreads();
+    }
+  }
+
+  // adj = (raw + bias[e]) (+ concept[e]), moe.rs:126-133.
+  float adj = 0.0f;
+  if (valid) {
+    adj = acc + bias[e];
+    if (concept != nullptr && e < n_concept) adj = adj + concept[e];
+  }
+  topk_epilogue(acc, adj, valid, e, t, T, E, k, LPT, logits, topk_idx, topk_w, cnt_s);
   __syncthreads();
   if (tid < E) block_counts[(size_t)blockIdx.x * E + tid] = cnt_s[tid];
+}
+
+// ---------------------------------------------------------------------------
+// Simple router (any d): W chunks in LDS, x read straight from global.
+// ---------------------------------------------------------------------------
+template <typename XT>
+__global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
+    const XT *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
+    const float *__restrict__ concept, int n_concept, int T, int d, int E, int k, int lpt_log2,
+    int kc, float *__restrict__ logits, int32_t *__restrict__ topk_idx,
+    float *__restrict__ topk_w, int32_t *__restrict__ block_counts) {
+#pragma clang fp contract(off)
+  extern __shared__ float w_s[];  // [E][kc + 4]
+  __shared__ int cnt_s[PRICHS_MAX_EXPERTS];
+
+  const int lpt = 1 << lpt_log2;
+  const int tpb = kRouterThreads >> lpt_log2;
+  const int tid = threadIdx.x;
+  const int e = tid & (lpt - 1);
+  const int t = blockIdx.x * tpb + (tid >> lpt_log2);
+  const bool valid = (t < T) && (e < E);
+  const int kcp = kc + 4;
+  if (tid < E) cnt_s[tid] = 0;
+
+  float acc = 0.0f;
+  for (int k0 = 0; k0 < d; k0 += kc) {
+    const int n = min(kc, d - k0);
+    __syncthreads();
+    for (int i = tid; i < n * E; i += kRouterThreads) {
+      const int kk = i / E;
+      const int ee = i - kk * E;
+      w_s[ee * kcp + kk] = w[(size_t)(k0 + kk) * E + ee];
+    }
+    __syncthreads();
+    if (valid) {
+      const XT *xr = x + (size_t)t * d + k0;
+      const float *wr = w_s + e * kcp;
+      for (int kk = 0; kk < n; ++kk) {
+        const float p = Elem<XT>::load(xr + kk) * wr[kk];
+        acc = acc + p;
+      }
+    }
+  }
+
+  float adj = 0.0f;
+  if (valid) {
+    adj = acc + bias[e];
+    if (concept != nullptr && e < n_concept) adj = adj + concept[e];
+  }
+  topk_epilogue(acc, adj, valid, e, t, T, E, k, lpt, logits, topk_idx, topk_w, cnt_s);
+  __syncthreads();
+  if (tid < E) block_counts[(size_t)blockIdx.x * E + tid] = cnt_s[tid];
+}
+
+__global__ void fill_i32_kernel(int32_t *p, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 __global__ __launch_bounds__(256) void permute_kernel(
@@ -251,22 +490,73 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __syncthreads();
   const int t0 = b * tpb;
   const int t1 = min(T, t0 + tpb);
-  if (tid < E) {
-    int r = base_s[tid];
-    for (int t = t0; t < t1; ++t) {
-      for (int s = 0; s < k; ++s) {
-        const size_t ts = (size_t)t * k + s;
-        if (topk_idx[ts] == tid) {
-          row_token[r] = t;
-          row_weight[r] = topk_w[ts];
-          token_row[ts] = r;
-          ++r;
-        }
+  // The block's (token, slot) entries in (t, s) order, one 64-wide window per
+  // wave step.  An expert occurs at most once per token, so (t, s) order
+  // within one expert is token order; each entry's place is the expert's
+  // running base plus the number of earlier entries of that expert in the
+  // window (a ballot per expert).  The 64-lane windows are taken in order by
+  // wave 0 alone, which keeps the running bases sequential.
+  if (tid < 64) {
+    const int lane = tid;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int base = lane < E ? base_s[lane] : 0;  // running base of expert `lane`
+    const size_t s0 = (size_t)t0 * k, s1 = (size_t)t1 * k;
+    for (size_t w0 = s0; w0 < s1; w0 += 64) {
+      const size_t ts = w0 + lane;
+      const bool live = ts < s1;
+      const int e_me = live ? topk_idx[ts] : -1;
+      const float wt = live ? topk_w[ts] : 0.0f;
+      int r = -1;
+      for (int e = 0; e < E; ++e) {
+        const uint64_t m = __ballot(e_me == e);
+        const int be = __shfl(base, e);
+        if (e_me == e) r = be + __popcll(m & lt);
+        if (lane == e) base += __popcll(m);
+      }
+      if (live && r >= 0) {
+        row_token[r] = (int32_t)(ts / k);
+        row_weight[r] = wt;
+        token_row[ts] = r;
       }
     }
   }
   // Shared-expert rows follow the routed rows in token order.
   for (int t = t0 + tid; t < t1; t += blockDim.x) row_token[(size_t)T * k + t] = t;
+}
+
+template <typename XT, int LPT, int KC>
+int launch_staged_t(const XT *x, const float *w, const float *bias, const float *concept, int nc,
+                    int T, int d, int E, int k, float *logits, int32_t *idx, float *wt,
+                    int32_t *bc, int nb, hipStream_t s) {
+  using Cf = StagedRouter<XT, LPT, KC>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    PRICHS_HIP_TRY(hipFuncSetAttribute(
+                       reinterpret_cast<const void *>(&router_topk_staged_kernel<XT, LPT, KC>),
+                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::kLds),
+                   "router: set LDS size");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((router_topk_staged_kernel<XT, LPT, KC>), dim3(nb), dim3(kRouterThreads),
+                     Cf::kLds, s, x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc);
+  return PRICHS_OK;
+}
+
+// K chunk per lanes-per-token: both LDS buffers within ~42 KB (three blocks
+// per CU) and at most 8 x vectors and 4 W float4s staged per thread.
+template <typename XT>
+int launch_staged(int lg, const XT *x, const float *w, const float *bias, const float *concept,
+                  int nc, int T, int d, int E, int k, float *logits, int32_t *idx, float *wt,
+                  int32_t *bc, int nb, hipStream_t s) {
+  switch (lg) {
+    case 0: return launch_staged_t<XT, 1, 16>(x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc, nb, s);
+    case 1: return launch_staged_t<XT, 2, 32>(x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc, nb, s);
+    case 2: return launch_staged_t<XT, 4, 64>(x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc, nb, s);
+    case 3: return launch_staged_t<XT, 8, 128>(x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc, nb, s);
+    case 4: return launch_staged_t<XT, 16, 128>(x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc, nb, s);
+    case 5: return launch_staged_t<XT, 32, 128>(x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc, nb, s);
+    default: return launch_staged_t<XT, 64, 64>(x, w, bias, concept, nc, T, d, E, k, logits, idx, wt, bc, nb, s);
+  }
 }
 
 }  // namespace
@@ -302,23 +592,32 @@ extern "C" int prichs_router_topk(const void *x, int x_dtype, const float *w_rou
   const int lg = lanes_per_token_log2((int)E);
   const int tpb = kRouterThreads >> lg;
   const int nb = (int)cdiv(T, (size_t)tpb);
-  const int kc = router_chunk((int)d, (int)E);
-  const size_t lds = (size_t)E * (kc + 4) * sizeof(float);
-  const bool vec = (d % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
   hipStream_t s = as_stream(stream);
   const int nc = (int)(n_concept < E ? n_concept : E);
-  if (x_dtype == PRICHS_DTYPE_BF16) {
-    auto kern = vec ? router_topk_kernel<bf16_t, true> : router_topk_kernel<bf16_t, false>;
-    hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), lds, s,
-                       static_cast<const bf16_t *>(x), w_router, router_bias, concept_bias, nc,
-                       (int)T, (int)d, (int)E, (int)k, lg, kc, logits, topk_idx, topk_w,
-                       block_counts);
+  const bool staged = (d % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                      (reinterpret_cast<uintptr_t>(w_router) % 16 == 0);
+  if (staged) {
+    int rc = x_dtype == PRICHS_DTYPE_BF16
+                 ? launch_staged<bf16_t>(lg, static_cast<const bf16_t *>(x), w_router,
+                                         router_bias, concept_bias, nc, (int)T, (int)d, (int)E,
+                                         (int)k, logits, topk_idx, topk_w, block_counts, nb, s)
+                 : launch_staged<float>(lg, static_cast<const float *>(x), w_router, router_bias,
+                                        concept_bias, nc, (int)T, (int)d, (int)E, (int)k, logits,
+                                        topk_idx, topk_w, block_counts, nb, s);
+    if (rc) return rc;
   } else {
-    auto kern = vec ? router_topk_kernel<float, true> : router_topk_kernel<float, false>;
-    hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), lds, s,
-                       static_cast<const float *>(x), w_router, router_bias, concept_bias, nc,
-                       (int)T, (int)d, (int)E, (int)k, lg, kc, logits, topk_idx, topk_w,
-                       block_counts);
+    const int kc = router_chunk((int)d, (int)E);
+    const size_t lds = (size_t)E * (kc + 4) * sizeof(float);
+    if (x_dtype == PRICHS_DTYPE_BF16)
+      hipLaunchKernelGGL(router_topk_kernel<bf16_t>, dim3(nb), dim3(kRouterThreads), lds, s,
+                         static_cast<const bf16_t *>(x), w_router, router_bias, concept_bias, nc,
+                         (int)T, (int)d, (int)E, (int)k, lg, kc, logits, topk_idx, topk_w,
+                         block_counts);
+    else
+      hipLaunchKernelGGL(router_topk_kernel<float>, dim3(nb), dim3(kRouterThreads), lds, s,
+                         static_cast<const float *>(x), w_router, router_bias, concept_bias, nc,
+                         (int)T, (int)d, (int)E, (int)k, lg, kc, logits, topk_idx, topk_w,
+                         block_counts);
   }
   PRICHS_LAUNCH_CHECK("router_topk launch");
   return PRICHS_OK;
@@ -337,7 +636,9 @@ extern "C" int prichs_permute(const int32_t *topk_idx, const float *topk_w,
   hipStream_t s = as_stream(stream);
   if (T == 0) {
     // Empty batch: every group is empty.
-    PRICHS_HIP_TRY(hipMemsetAsync(offsets, 0, sizeof(int32_t) * (E + 2), s), "permute memset");
+    // (A fill kernel rather than hipMemsetAsync, which is unsafe in captured graphs.)
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(128), 0, s, offsets, (int)(E + 2), 0);
+    PRICHS_LAUNCH_CHECK("permute fill");
     return PRICHS_OK;
   }
   PRICHS_REQUIRE(topk_idx && topk_w && block_counts && row_token && row_weight && token_row,

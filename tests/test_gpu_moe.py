@@ -47,18 +47,41 @@ def test_router_bit_exact(cuda, orc, cfg):
     assert rel_err(host(w), rw) <= 1e-6
 
 
+# Staged kernel (d % 8 == 0; whole and partial K chunks, 1..64 lanes per
+# token) and the simple kernel (d % 8 != 0, or x not 16-byte aligned).
 @pytest.mark.parametrize("E,k,T,d", [(4, 2, 77, 64), (8, 1, 33, 96), (16, 3, 200, 128),
-                                     (64, 8, 129, 40), (3, 3, 5, 8), (1, 1, 9, 16)])
-def test_router_shapes(cuda, orc, E, k, T, d):
+                                     (64, 8, 129, 40), (3, 3, 5, 8), (1, 1, 9, 16),
+                                     (8, 2, 300, 200), (2, 2, 500, 104), (32, 4, 70, 328),
+                                     (6, 2, 100, 37), (8, 2, 64, 13)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_router_shapes(cuda, orc, E, k, T, d, dtype):
     rng = np.random.default_rng(E * 100 + k)
     x = rng.standard_normal((T, d)).astype(np.float32)
+    if dtype == "bf16":
+        x = synth.round_bf16(x)
     wr = (0.1 * rng.standard_normal((d, E))).astype(np.float32)
     b = (0.05 * rng.standard_normal(E)).astype(np.float32)
-    logits, idx, w, _ = ops.router_topk(dev(x), dev(wr), dev(b), k)
+    logits, idx, w, _ = ops.router_topk(dev(x, dtype), dev(wr), dev(b), k)
     rl, rs, rw = orc.route(x, wr, b, k)
     np.testing.assert_array_equal(host(logits).view(np.uint32), rl.view(np.uint32))
     np.testing.assert_array_equal(host(idx), rs)
     assert rel_err(host(w), rw) <= 1e-6
+
+
+def test_router_unaligned_x(cuda, orc):
+    # x starts 4 bytes past a 16-byte boundary: the simple kernel serves it.
+    T, d, E, k = 40, 64, 8, 2
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    wr = (0.1 * rng.standard_normal((d, E))).astype(np.float32)
+    b = np.zeros(E, np.float32)
+    buf = torch.zeros(T * d + 1, dtype=torch.float32, device="cuda")
+    xv = buf[1:].view(T, d)
+    xv.copy_(dev(x))
+    logits, idx, w, _ = ops.router_topk(xv, dev(wr), dev(b), k)
+    rl, rs, rw = orc.route(x, wr, b, k)
+    np.testing.assert_array_equal(host(logits).view(np.uint32), rl.view(np.uint32))
+    np.testing.assert_array_equal(host(idx), rs)
 
 
 def test_router_ties_nan_and_concept_bias(cuda, orc):
