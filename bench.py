@@ -137,6 +137,29 @@ def main():
     def gbps(b, stage):
         return b / (ms[stage] / 1e3) / 1e9 if ms[stage] > 0 else None
 
+    kernel = "grouped gate/up GEMM + fused SwiGLU (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, true>)"
+    if T * k < 64 * E:  # fewer than 64 rows per routed expert on average
+        # Decode shape: every touched expert's gate/up weights are streamed once
+        # for a handful of rows, so the launch is bound by HBM, not MFMA.
+        sel = eng.stash()["selected_experts"].cpu().numpy()
+        touched = len(set(sel.reshape(-1).tolist())) + S
+        gu_bytes = touched * d * 2 * f * es + rows * d * es + rows * f * es
+        bw = gu_bytes / t_gu / 1e9
+        roofline = {"kernel": kernel, "bound": "hbm", "achieved": bw, "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": bw / PEAK_HBM_GBPS, "traffic": None,
+                    "algorithmic_bytes_per_launch": gu_bytes, "experts_touched": touched,
+                    "avg_launch_ms": ms["gate_up"]}
+    else:
+        roofline = {
+            "kernel": kernel, "bound": "mfma", "achieved": gu_tflops, "peak": peak,
+            "unit": "TFLOP/s", "frac": gu_tflops / peak,
+            "traffic": measured_traffic() if args.config == 2 else None,
+            "traffic_source": "profiles/pmc_config2_gate_up_traffic.txt (rocprofv3 --pmc "
+                              "FETCH_SIZE, WRITE_SIZE, copy-calibrated)" if args.config == 2 else None,
+            "algorithmic_flops_per_launch": flops_gate_up,
+            "avg_launch_ms": ms["gate_up"],
+        }
+
     res = {
         "metric": METRIC,
         "value": T * args.steps / elapsed,
@@ -152,19 +175,7 @@ def main():
         "data": "synthetic (seeded SplitMix64 + Box-Muller, seed 0)",
         "config": {"workload": WORKLOADS[args.config], "tokens": T, "d_model": d, "d_ffn": f,
                    "routed_experts": E, "shared_experts": S, "top_k": k},
-        "roofline": {
-            "kernel": "grouped gate/up GEMM + fused SwiGLU (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, true>)",
-            "bound": "mfma",
-            "achieved": gu_tflops,
-            "peak": peak,
-            "unit": "TFLOP/s",
-            "frac": gu_tflops / peak,
-            "traffic": measured_traffic() if args.config == 2 else None,
-            "traffic_source": "profiles/pmc_config2_gate_up_traffic.txt (rocprofv3 --pmc "
-                              "FETCH_SIZE, WRITE_SIZE, copy-calibrated)" if args.config == 2 else None,
-            "algorithmic_flops_per_launch": flops_gate_up,
-            "avg_launch_ms": ms["gate_up"],
-        },
+        "roofline": roofline,
         "expert_gemm": {"tflops": gemm_tflops, "frac_of_peak": gemm_tflops / peak,
                         "gate_up_ms": ms["gate_up"], "down_ms": ms["down"],
                         "down_tflops": flops_down / t_dn / 1e12},
@@ -221,6 +232,7 @@ def measured_traffic():
 def bench_block(args):
     """Config 5: one PrichsBlock forward per step (tokens/s), with the attention
     kernel timed on its own over the same rows (causal TFLOP/s)."""
+    import numpy as np
     import torch
 
     from prichs_amd import block, ops, synth
@@ -255,6 +267,29 @@ def bench_block(args):
     e1.record()
     torch.cuda.synchronize()
     att_ms = e0.elapsed_time(e1) / args.steps
+
+    def event_ms(fn, reps=args.steps):
+        for _ in range(3):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    # HBM-bound sub-layers alone at the block's shapes: RMSNorm of x [T, d]
+    # (bf16 in/out, f32 weight) and RoPE in place on Q [T, 12, 128] and K [T, 3, 128].
+    w_norm = torch.from_numpy(np.ascontiguousarray(inp.input_norm, np.float32)).to("cuda")
+    rn_ms = event_ms(lambda: ops.rmsnorm(x, w_norm, want_rstd=False))
+    cos, sin = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to("cuda")
+                for a in synth.rope_cache(S, hd, inp.rope_theta))
+    qr = q.contiguous().view(B, S, Hq, hd)
+    kr = k.contiguous().view(B, S, Hkv, hd)
+    rope_ms = event_ms(lambda: (ops.rope_(qr, cos, sin, S, B, S), ops.rope_(kr, cos, sin, S, B, S)))
+    rn_bytes = 2 * T * d * 2 + d * 4
+    rope_bytes = 2 * T * (Hq + Hkv) * hd * 2 + 2 * S * (hd // 2) * 4
     att_flops = B * Hq * 4.0 * hd * S * (S + 1) / 2  # causal QK^T + PV
     moe_flops = 6.0 * d * inp.moe.f * T * (inp.moe.k + 1)
     proj_flops = 2.0 * T * d * (d + 2 * Hkv * hd) + 2.0 * T * d * d
@@ -272,6 +307,12 @@ def bench_block(args):
                      "traffic": None, "algorithmic_flops_per_launch": att_flops,
                      "avg_launch_ms": att_ms},
         "block_tflops": (att_flops + moe_flops + proj_flops) / (ms * 1e-3) / 1e12,
+        "memory_bound_stages": {
+            "rmsnorm": {"ms": rn_ms, "GB/s": rn_bytes / (rn_ms * 1e-3) / 1e9, "bytes": rn_bytes},
+            "rope_q_and_k": {"ms": rope_ms, "GB/s": rope_bytes / (rope_ms * 1e-3) / 1e9,
+                             "bytes": rope_bytes},
+            "peak_GB/s": PEAK_HBM_GBPS,
+        },
         "device": torch.cuda.get_device_name(0),
         "cpu_baseline": None,
     }

@@ -272,11 +272,12 @@ __device__ inline float router_dot4(float acc, const float *xr, const float *wr)
 
 // Sum over one whole chunk, fully unrolled so the chunk's LDS reads are issued
 // ahead of the dependent adds (at one wave per SIMD nothing else covers their
-// latency).  PRICHS_ROUTER_PIPE=1 instead pins a read-ahead interleave with
-// sched_group_barrier (masks: 0x100 LDS read, 0x2 VALU).  Either way the
-// arithmetic order is the reference's: each product rounded, then each sum.
+// latency).  With PRICHS_ROUTER_PIPE=1 (default; ~5% faster at config 2) a
+// sched_group_barrier sequence also pins a read-ahead interleave (masks: 0x100
+// LDS read, 0x2 VALU).  Either way the arithmetic order is the reference's:
+// each product rounded, then each sum.
 #ifndef PRICHS_ROUTER_PIPE
-#define PRICHS_ROUTER_PIPE 0
+#define PRICHS_ROUTER_PIPE 1
 #endif
 template <int KC>
 __device__ inline float router_dot_chunk(float acc, const float *xr, const float *wr) {
