@@ -167,7 +167,12 @@ int prichs_permute(const int32_t *topk_idx, const float *topk_w,
  *   column il*b + q - il of up (q >= il), zero when that column is >= f.
  * down, one expert: packed [roundup(d, 256), K = f] = W_down^T, zero rows
  *   past d.
- * Element type: dtype (bf16 by round-to-nearest-even from f32). */
+ * Element type: dtype (bf16 by round-to-nearest-even from f32).
+ * Storage order of a packed [Np, K]: f32 row-major (element (n, k) at
+ *   n*K + k); bf16 fragment-major, the operand layout of the MFMA
+ *   v_mfma_f32_16x16x32_bf16: element (n, k) at
+ *   ((n/16 * K/32 + k/32) * 64 + n%16 + 16*((k%32)/8)) * 8 + k%8,
+ *   so each 16-row x 32-k fragment is one contiguous KiB. */
 size_t prichs_gate_up_interleave(int dtype);
 size_t prichs_packed_gate_up_elems(size_t d, size_t f, int dtype);
 size_t prichs_packed_down_elems(size_t d, size_t f, int dtype);
@@ -187,7 +192,9 @@ int prichs_pack_down(const float *down, size_t d, size_t f, int dtype,
  * experts (g < E) and the shared expert (g = E, its weights packed last).
  * x [T, d], act [offsets[G], f] and the weights share `dtype`; fp32
  * accumulation.  Requires d % 64 == 0 and f % 64 == 0 for bf16, d % 16 == 0
- * and f % 16 == 0 for f32.  max_rows bounds offsets[G] (sizes the launch). */
+ * and f % 16 == 0 for f32.  max_rows bounds offsets[G] (sizes the launch);
+ * bf16 launches with max_rows <= 64 stream the weights through a skinny
+ * (decode) kernel instead of the 256x256-tiled one. */
 int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_token,
                                   const int32_t *offsets, size_t G,
                                   size_t max_rows, const void *w_packed,
@@ -248,7 +255,8 @@ int prichs_add(const void *a, int a_dtype, const void *b, int b_dtype,
 /* Dense GEMM C[M, N] = A[M, K] @ W on the bf16 (or f32) MFMA kernel of the
  * grouped GEMMs: replaces matmul_2d's device dispatch / forward_gemm
  * (crates/prichs-core/src/ops.rs:24-31; crates/prichs-cuda/src/engine.rs:
- * 757-826) for the block's projections.  W comes from prichs_pack_weight.
+ * 757-826) for the block's projections.  W comes from prichs_pack_weight
+ * (the packed-down storage order above: [roundup(N, 256), K] = W^T).
  * Row strides lda (multiple of 8) and ldc (multiple of 4); K and N multiples
  * of 64 (bf16) or 16 (f32); fp32 accumulation. */
 size_t prichs_packed_weight_elems(size_t K, size_t N, int dtype);

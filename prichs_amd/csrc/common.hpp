@@ -100,4 +100,15 @@ __device__ inline float silu_fast(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// prichs_grouped_gate_up_swiglu / prichs_grouped_down with a tighter bound on
+// every group's row count (a caller that knows T passes T): decode-sized
+// groups then take the skinny weight-streaming kernel.
+int grouped_gate_up_swiglu_rows(const void *x, const int32_t *row_token, const int32_t *offsets,
+                                size_t G, size_t max_rows, size_t max_group_rows,
+                                const void *w_packed, size_t d, size_t f, int dtype, void *act,
+                                void *stream);
+int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t max_rows,
+                      size_t max_group_rows, const void *w_packed, size_t d, size_t f, int dtype,
+                      void *y, void *stream);
+
 }  // namespace prichs

@@ -271,12 +271,13 @@ extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, 
                       eng->offsets, eng->row_token, eng->row_weight, eng->token_row, stream);
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[2], s), "engine_forward: event");
-  rc = prichs_grouped_gate_up_swiglu(x, eng->row_token, eng->offsets, G, rows, eng->w_gate_up,
-                                     eng->d, eng->f, eng->dtype, eng->act, stream);
+  // No group holds more than T rows (a token picks an expert at most once).
+  rc = grouped_gate_up_swiglu_rows(x, eng->row_token, eng->offsets, G, rows, T, eng->w_gate_up,
+                                   eng->d, eng->f, eng->dtype, eng->act, stream);
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[3], s), "engine_forward: event");
-  rc = prichs_grouped_down(eng->act, eng->offsets, G, rows, eng->w_down, eng->d, eng->f,
-                           eng->dtype, eng->y, stream);
+  rc = grouped_down_rows(eng->act, eng->offsets, G, rows, T, eng->w_down, eng->d, eng->f,
+                         eng->dtype, eng->y, stream);
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[4], s), "engine_forward: event");
   rc = prichs_moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T,

@@ -240,7 +240,8 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
   // Fragment reads: lane l reads row l%16 of a 16-row block, chunk l/16.
   const int fr = lane & 15;
   const int a_rd = lds_off(wm * WM + fr, lane >> 4);
-  const int b_rd = lds_off(wn * WN + fr, lane >> 4);
+  // B stage: whole packed fragments in weight order, lane-major (1 KiB each).
+  const int b_rd = wn * WN * BK + lane * 8;
 
   const int nblk = gridDim.x;
   for (int t = xcd_block_id(); t < total; t += nblk) {
@@ -263,8 +264,10 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     }
 #pragma unroll
     for (int i = 0; i < kInstB; ++i) {
-      const int nr = n0 + (wave * kInstB + i) * kRowsPerInst + dma_row;
-      b_goff[i] = (uint32_t)nr * (uint32_t)K + (uint32_t)(dma_chunk * 8);
+      // Instruction i moves fragment (16-row block nb, K-step kt): 1 KiB at
+      // (nb * KT + kt) * 512 elements, lane l's 16 bytes at l * 8.
+      const int nb = n0 / kRowsPerInst + wave * kInstB + i;
+      b_goff[i] = (uint32_t)nb * (uint32_t)KT * 512u + (uint32_t)(lane * 8);
     }
     const bf16_t *Bg = B + (long long)g * b_group_stride;
 
@@ -286,7 +289,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     _Pragma("unroll") for (int i_ = 0; i_ < kInstA; ++i_)                            \
         dma_16b(A + a_goff[i_] + k0_, st_ + (wave * kInstA + i_) * kRowsPerInst * BK); \
     _Pragma("unroll") for (int i_ = 0; i_ < kInstB; ++i_)                            \
-        dma_16b(Bg + b_goff[i_] + k0_, st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK); \
+        dma_16b(Bg + b_goff[i_] + (kt_) * 512, st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK); \
   } while (0)
 
     // Prologue: stages 0..3 in flight; stage 0 lands and is read.
@@ -560,6 +563,190 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
 }
 }  // namespace fp
 
+// ------------------------------------------------------------------------
+// Skinny grouped GEMM for decode-sized groups (at most kSkinnyRows rows per
+// group per M-tile).  With a handful of rows per expert there is no weight
+// reuse to stage through LDS: the launch is bound by streaming the touched
+// experts' packed weights from HBM once.  One workgroup of 4 waves covers
+// (group, 64 packed weight rows, 32 token rows); each wave streams its own 16
+// packed rows (K-contiguous, 16 bytes per lane per K-step) straight into MFMA
+// operand registers, with kSkU K-steps per chunk double-buffered in registers,
+// and reads the activation fragments of the (at most 32) rows from the cache.
+// MFMA operands as in the tiled kernel: weights are operand A (row n = lane &
+// 15, k = 8 * (lane >> 4)), activations operand B, so lane (m = lane & 15)
+// ends with output columns 4 * (lane >> 4) + r, r = 0..3.
+// ------------------------------------------------------------------------
+namespace skinny {
+constexpr int kThreads = 256;
+constexpr int BM = 32;           // token rows per M-tile (two 16-row MFMA tiles)
+constexpr int BN = 64;           // packed weight rows per workgroup (16 per wave)
+constexpr int kSkinnyRows = 64;  // engine uses this path when every group has <= this many rows
+
+// The wave's weight fragments of K-steps s0 .. s0+U-1 (1 KiB apart in the
+// fragment-major packing).
+template <int U>
+__device__ inline void load_w(const bf16_t *__restrict__ wp, int s0, bf16x8 (&w)[U]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) w[u] = *reinterpret_cast<const bf16x8 *>(wp + (s0 + u) * 512);
+}
+
+// GATEUP: C = act [rows][ldc], packed rows [64s, 64s + 64) are one [32 gate |
+// 32 up] block (the packing interleave), so N-waves 0/1 (gate) pair with
+// N-waves 2/3 (up) lane for lane.  Otherwise C = y [rows][ldc].  The workgroup
+// is 4 x SK waves: N-wave wn = wave & 3 covers packed rows 16 wn.., K-slice
+// ks = wave >> 2 covers K [ks K/SK, (ks+1) K/SK) (more waves, so more weight
+// bytes in flight per CU); slice partial sums are added in slice order.
+// Activations go through LDS: per chunk of U K-steps, the 4 waves of a slice
+// load its [32 rows][32 U] tile once (16 bytes per load) into one of two
+// buffers, and every N-wave reads its MFMA fragments from there.
+// (K / SK) % (32 * U) == 0.
+template <bool GATEUP, int U, int SK>
+__global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
+    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
+    const bf16_t *__restrict__ B, long long b_stride, int K, bf16_t *__restrict__ C, int ldc,
+    int n_store, const int32_t *__restrict__ offsets) {
+  constexpr int kRow = 32 * U + 8;                 // LDS row (16-byte pad: conflict-free reads)
+  constexpr int kSegs = BM * 4 * U;                // 16-byte segments of one chunk tile
+  constexpr int kSegPerThread = kSegs / kThreads;  // U / 2
+  static_assert(kSegs % kThreads == 0, "whole segments per thread");
+  __shared__ __attribute__((aligned(16))) bf16_t a_s[SK][2][BM * kRow];
+  __shared__ f32x4 red_s[SK > 1 ? SK - 1 : 1][4][2][64];  // [slice-1][N-wave][tile][lane]
+  __shared__ f32x4 gate_s[2][2][64];                      // [gate wave][tile][lane]
+  const int g = blockIdx.y;
+  const int r1 = offsets[g + 1];
+  const int m0 = offsets[g] + (int)blockIdx.z * BM;
+  if (m0 >= r1) return;  // uniform: this M-tile of the group is empty
+  const int mrows = min(BM, r1 - m0);
+  const bool two = mrows > 16;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wn = wave & 3, ks = wave >> 2;
+  const int st = threadIdx.x & (kThreads - 1);  // thread within the slice
+  const int Ks = K / SK;
+  const int nc = Ks / (32 * U);
+  // Fragment (16-row block nb, K-step ks * Ks / 32 + s) of the packed weights.
+  const int nb = blockIdx.x * (BN / 16) + wn;
+  const bf16_t *wp =
+      B + g * b_stride + ((long long)nb * (K / 32) + ks * (Ks / 32)) * 512 + lane * 8;
+
+  // Activation staging: segment i = st + kThreads * j is (row i / (4U), 16-byte
+  // column i % (4U)) of the chunk tile; rows past the group re-read its last
+  // row (their outputs are never stored).
+  const bf16_t *asrc[kSegPerThread];
+  int adst[kSegPerThread];
+#pragma unroll
+  for (int j = 0; j < kSegPerThread; ++j) {
+    const int i = st + kThreads * j;
+    const int r = i / (4 * U), sc = i % (4 * U);
+    int src = min(m0 + r, r1 - 1);
+    if (a_rows != nullptr) src = a_rows[src];
+    asrc[j] = A + (long long)src * lda + ks * Ks + sc * 8;
+    adst[j] = r * kRow + sc * 8;
+  }
+  bf16x8 areg[kSegPerThread];
+  auto load_a = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < kSegPerThread; ++j)
+      areg[j] = *reinterpret_cast<const bf16x8 *>(asrc[j] + c * 32 * U);
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kSegPerThread; ++j)
+      *reinterpret_cast<bf16x8 *>(&a_s[ks][buf][adst[j]]) = areg[j];
+  };
+  const int rd = (lane & 15) * kRow + 8 * (lane >> 4);  // fragment read offset, tile 0
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const bf16x8(&w)[U], int buf) {
+    const bf16_t *as = &a_s[ks][buf][rd];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      acc0 = mfma_bf16(w[u], *reinterpret_cast<const bf16x8 *>(as + 32 * u), acc0);
+      if (two) acc1 = mfma_bf16(w[u], *reinterpret_cast<const bf16x8 *>(as + 16 * kRow + 32 * u), acc1);
+    }
+  };
+
+  // Chunk c: A(c) is stored to buffer c & 1 during iteration c - 1; W(c) sits
+  // in w0 (c even) or w1 (c odd).  Loads of chunk c + 2 are issued in
+  // iteration c, A before W, unconditionally (clamped to the last chunk), so
+  // the compiler's waits count exactly the loads issued after each one's.
+  bf16x8 w0[U], w1[U];
+  load_a(0);
+  load_w<U>(wp, 0, w0);
+  store_a(0);
+  load_a(min(1, nc - 1));
+  load_w<U>(wp, min(1, nc - 1) * U, w1);
+  __syncthreads();
+  for (int c = 0; c < nc; c += 2) {
+    mma(w0, 0);
+    if (c + 1 < nc) store_a(1);
+    load_a(min(c + 2, nc - 1));
+    load_w<U>(wp, min(c + 2, nc - 1) * U, w0);
+    __syncthreads();
+    if (c + 1 < nc) {
+      mma(w1, 1);
+      if (c + 2 < nc) store_a(0);
+    }
+    load_a(min(c + 3, nc - 1));
+    load_w<U>(wp, min(c + 3, nc - 1) * U, w1);
+    __syncthreads();
+  }
+
+  if (SK > 1) {
+    if (ks > 0) {
+      red_s[ks - 1][wn][0][lane] = acc0;
+      red_s[ks - 1][wn][1][lane] = acc1;
+    }
+    __syncthreads();
+    if (ks == 0) {
+#pragma unroll
+      for (int j = 0; j < SK - 1; ++j) {
+        acc0 += red_s[j][wn][0][lane];
+        acc1 += red_s[j][wn][1][lane];
+      }
+    }
+  }
+
+  const int cq = 4 * (lane >> 4);
+  const int mr = m0 + (lane & 15);
+  if (GATEUP) {
+    if (ks == 0 && wn < 2) {
+      gate_s[wn][0][lane] = acc0;
+      gate_s[wn][1][lane] = acc1;
+    }
+    __syncthreads();
+    if (ks == 0 && wn >= 2) {
+      const int col = blockIdx.x * (BN / 2) + (wn - 2) * 16 + cq;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int m = mr + 16 * t;
+        if (m < r1 && col < n_store) {
+          const f32x4 gv = gate_s[wn - 2][t][lane];
+          const f32x4 uv = t == 0 ? acc0 : acc1;
+          uint32_t h[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(PRICHS_BF16_SILU(gv[r]) * uv[r]);
+          *reinterpret_cast<u32x2 *>(C + (long long)m * ldc + col) =
+              u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+      }
+    }
+  } else if (ks == 0) {
+    const int col = blockIdx.x * BN + wn * 16 + cq;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int m = mr + 16 * t;
+      if (m < r1 && col < n_store) {
+        const f32x4 v = t == 0 ? acc0 : acc1;
+        uint32_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(v[r]);
+        *reinterpret_cast<u32x2 *>(C + (long long)m * ldc + col) =
+            u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      }
+    }
+  }
+}
+}  // namespace skinny
+
 size_t il_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)Bf16::kIl : (size_t)fp::kIl; }
 size_t bn_of(int dtype) { return dtype == PRICHS_DTYPE_BF16 ? (size_t)Bf16::BN : (size_t)fp::BN; }
 
@@ -580,6 +767,18 @@ template <> void put<bf16_t>(void *out, size_t i, float v) {
   static_cast<bf16_t *>(out)[i] = f32_to_bf16(v);
 }
 
+// Element (n, k) of a packed [Np, K] weight.  f32: row-major.  bf16:
+// fragment-major, the operand layout of v_mfma_f32_16x16x32_bf16: fragment
+// (n / 16, k / 32) is 1 KiB contiguous, lane l = n % 16 + 16 * ((k % 32) / 8)
+// holding k % 8 = 0..7 in 16 bytes, fragments of one 16-row block ordered by k.
+// A wave instruction then moves one whole fragment (one contiguous KiB), to
+// LDS in the tiled kernel and straight into registers in the skinny one.
+inline size_t packed_index(size_t n, size_t k, size_t K, bool bf16) {
+  if (!bf16) return n * K + k;
+  const size_t lane = (n & 15) + 16 * ((k & 31) >> 3);
+  return (((n >> 4) * (K >> 5) + (k >> 5)) * 64 + lane) * 8 + (k & 7);
+}
+
 // Packed gate/up rows: the [il gate | il up] blocks covering f columns,
 // padded with zero rows to a multiple of the kernel's N tile.
 size_t gate_up_np(size_t f, int dtype) { return roundup(2 * roundup(f, il_of(dtype)), bn_of(dtype)); }
@@ -593,14 +792,16 @@ void pack_gate_up_impl(const float *gate, const float *up, size_t d, size_t f, i
     const size_t b = p / (2 * il), q = p % (2 * il);
     const float *src = q < il ? gate : up;
     const size_t col = il * b + (q < il ? q : q - il);
-    for (size_t k = 0; k < d; ++k) put<T>(out, p * d + k, col < f ? src[k * f + col] : 0.0f);
+    for (size_t k = 0; k < d; ++k)
+      put<T>(out, packed_index(p, k, d, sizeof(T) == 2), col < f ? src[k * f + col] : 0.0f);
   }
 }
 
 template <typename T> void pack_down_impl(const float *down, size_t d, size_t f, void *out) {
   const size_t np = roundup(d, kPadRowsDown);
   for (size_t n = 0; n < np; ++n)
-    for (size_t k = 0; k < f; ++k) put<T>(out, n * f + k, n < d ? down[k * d + n] : 0.0f);
+    for (size_t k = 0; k < f; ++k)
+      put<T>(out, packed_index(n, k, f, sizeof(T) == 2), n < d ? down[k * d + n] : 0.0f);
 }
 
 template <class Cf, bool GATEUP>
@@ -626,10 +827,70 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
   return PRICHS_OK;
 }
 
+template <bool GATEUP, int U, int SK>
+int launch_skinny_u(const void *A, const int32_t *a_rows, int lda, const void *B,
+                    long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
+                    const int32_t *offsets, int G, int mtiles, hipStream_t s) {
+  static_assert(Bf16::kIl == skinny::BN / 2, "a skinny slab is one [gate | up] block");
+  hipLaunchKernelGGL((skinny::skinny_gemm_kernel<GATEUP, U, SK>),
+                     dim3(Np / skinny::BN, G, mtiles), dim3(skinny::kThreads * SK), 0, s,
+                     static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
+                     b_stride, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets);
+  PRICHS_LAUNCH_CHECK("skinny grouped gemm launch");
+  return PRICHS_OK;
+}
+
+// K split SK <= PRICHS_SKINNY_SK and K-steps per chunk U <= PRICHS_SKINNY_U,
+// each the largest that divides K evenly (every slice a whole number of
+// chunks; K is a multiple of 64).  Combinations whose LDS would exceed
+// ~70 KB (U = 8 with SK = 4) are not instantiated.  Measured at the decode
+// shape (T = 32, d = 1536, f = 1280): SK = 1, U = 4 is fastest (gate/up 17.0
+// us vs 18-23 us for SK = 2 or 4 and U = 2 or 8).
+#ifndef PRICHS_SKINNY_SK
+#define PRICHS_SKINNY_SK 1
+#endif
+#ifndef PRICHS_SKINNY_U
+#define PRICHS_SKINNY_U 4
+#endif
+template <bool GATEUP>
+int launch_skinny(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
+                  int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
+                  size_t max_group_rows, hipStream_t s) {
+  const int mtiles = (int)std::max<size_t>(1, (max_group_rows + skinny::BM - 1) / skinny::BM);
+  int sk = PRICHS_SKINNY_SK;
+  while (sk > 1 && K % (sk * 64) != 0) sk /= 2;
+  int u = PRICHS_SKINNY_U;
+  while (u > 2 && (K / sk) % (32 * u) != 0) u /= 2;
+  if (u == 8 && sk == 4) u = 4;
+#define PRICHS_SKINNY(U_, SK_)                                                                   \
+  if (u == U_ && sk == SK_)                                                                     \
+  return launch_skinny_u<GATEUP, U_, SK_>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store, \
+                                          offsets, G, mtiles, s)
+  PRICHS_SKINNY(2, 1);
+  PRICHS_SKINNY(4, 1);
+  PRICHS_SKINNY(8, 1);
+  PRICHS_SKINNY(2, 2);
+  PRICHS_SKINNY(4, 2);
+  PRICHS_SKINNY(8, 2);
+  PRICHS_SKINNY(2, 4);
+  PRICHS_SKINNY(4, 4);
+#undef PRICHS_SKINNY
+  return fail(PRICHS_ERR_UNSUPPORTED, "skinny gemm: no kernel for K=%d", K);
+}
+
+// max_group_rows bounds every group's row count (offsets[g+1] - offsets[g]);
+// bf16 launches whose groups all fit the skinny kernel's reach take it.
 int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, const void *B,
                    long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
                    const int32_t *offsets, int G, int dense_m, size_t max_rows, int dtype,
-                   hipStream_t s) {
+                   hipStream_t s, size_t max_group_rows) {
+  if (dtype == PRICHS_DTYPE_BF16 && dense_m == 0 && max_group_rows <= (size_t)skinny::kSkinnyRows &&
+      K % kBf16KMultiple == 0 && Np % skinny::BN == 0) {
+    return gateup ? launch_skinny<true>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
+                                        offsets, G, max_group_rows, s)
+                  : launch_skinny<false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
+                                         offsets, G, max_group_rows, s);
+  }
   const int cus = device_cu_count();
   if (cus <= 0) return fail(PRICHS_ERR_HIP, "grouped gemm: cannot query the device");
   if (dtype == PRICHS_DTYPE_BF16) {
@@ -690,10 +951,11 @@ extern "C" int prichs_pack_down(const float *down, size_t d, size_t f, int dtype
   return PRICHS_OK;
 }
 
-extern "C" int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_token,
-                                             const int32_t *offsets, size_t G, size_t max_rows,
-                                             const void *w_packed, size_t d, size_t f, int dtype,
-                                             void *act, void *stream) {
+namespace prichs {
+int grouped_gate_up_swiglu_rows(const void *x, const int32_t *row_token, const int32_t *offsets,
+                                size_t G, size_t max_rows, size_t max_group_rows,
+                                const void *w_packed, size_t d, size_t f, int dtype, void *act,
+                                void *stream) {
   if (int rc = check_gemm_shape(d, f, dtype, "gate_up")) return rc;
   PRICHS_REQUIRE(G >= 1 && G <= (size_t)kMaxGroups, "gate_up: G=%zu outside [1, %d]", G,
                  kMaxGroups);
@@ -702,12 +964,12 @@ extern "C" int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_t
   const size_t np = gate_up_np(f, dtype);
   return launch_grouped(true, x, row_token, (int)d, w_packed, (long long)(np * d), (int)np,
                         (int)d, act, (int)f, (int)f, offsets, (int)G, 0, max_rows, dtype,
-                        as_stream(stream));
+                        as_stream(stream), std::min(max_rows, max_group_rows));
 }
 
-extern "C" int prichs_grouped_down(const void *act, const int32_t *offsets, size_t G,
-                                   size_t max_rows, const void *w_packed, size_t d, size_t f,
-                                   int dtype, void *y, void *stream) {
+int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t max_rows,
+                      size_t max_group_rows, const void *w_packed, size_t d, size_t f, int dtype,
+                      void *y, void *stream) {
   if (int rc = check_gemm_shape(d, f, dtype, "down")) return rc;
   PRICHS_REQUIRE(G >= 1 && G <= (size_t)kMaxGroups, "down: G=%zu outside [1, %d]", G,
                  kMaxGroups);
@@ -716,7 +978,24 @@ extern "C" int prichs_grouped_down(const void *act, const int32_t *offsets, size
   const size_t np = roundup(d, kPadRowsDown);
   return launch_grouped(false, act, nullptr, (int)f, w_packed, (long long)(np * f), (int)np,
                         (int)f, y, (int)d, (int)d, offsets, (int)G, 0, max_rows, dtype,
-                        as_stream(stream));
+                        as_stream(stream), std::min(max_rows, max_group_rows));
+}
+}  // namespace prichs
+
+// A group can hold all max_rows rows, so the public entry points take that as
+// the per-group bound.
+extern "C" int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_token,
+                                             const int32_t *offsets, size_t G, size_t max_rows,
+                                             const void *w_packed, size_t d, size_t f, int dtype,
+                                             void *act, void *stream) {
+  return grouped_gate_up_swiglu_rows(x, row_token, offsets, G, max_rows, max_rows, w_packed, d,
+                                     f, dtype, act, stream);
+}
+
+extern "C" int prichs_grouped_down(const void *act, const int32_t *offsets, size_t G,
+                                   size_t max_rows, const void *w_packed, size_t d, size_t f,
+                                   int dtype, void *y, void *stream) {
+  return grouped_down_rows(act, offsets, G, max_rows, max_rows, w_packed, d, f, dtype, y, stream);
 }
 
 extern "C" size_t prichs_packed_weight_elems(size_t K, size_t N, int dtype) {
@@ -749,5 +1028,5 @@ extern "C" int prichs_gemm(const void *a, size_t lda, size_t M, size_t K, const 
   const size_t np = roundup(N, kPadRowsDown);
   return launch_grouped(false, a, nullptr, (int)lda, w_packed, (long long)(np * K), (int)np,
                         (int)K, c, (int)ldc, (int)N, nullptr, 1, (int)M, M, dtype,
-                        as_stream(stream));
+                        as_stream(stream), M);
 }

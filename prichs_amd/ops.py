@@ -91,7 +91,8 @@ def _np_dtype(code):
 
 
 def pack_gate_up(gate: np.ndarray, up: np.ndarray, dtype) -> np.ndarray:
-    """prichs_pack_gate_up (host): packed [Np, d] (bf16 bits as uint16, or f32)."""
+    """prichs_pack_gate_up (host): packed [Np, d] (bf16 bits as uint16, or f32;
+    bf16 is fragment-tiled, see packed_rows)."""
     lib = L.load()
     code = dtype_code(dtype)
     d, f = gate.shape
@@ -104,7 +105,8 @@ def pack_gate_up(gate: np.ndarray, up: np.ndarray, dtype) -> np.ndarray:
 
 
 def pack_down(down: np.ndarray, dtype) -> np.ndarray:
-    """prichs_pack_down (host): packed [roundup(d, 256), f]."""
+    """prichs_pack_down (host): packed [roundup(d, 256), f] (bf16 fragment-tiled,
+    see packed_rows)."""
     lib = L.load()
     code = dtype_code(dtype)
     f, d = down.shape
@@ -113,6 +115,17 @@ def pack_down(down: np.ndarray, dtype) -> np.ndarray:
     w = np.ascontiguousarray(down, dtype=np.float32)
     L.check(lib.prichs_pack_down(w.ctypes.data, d, f, code, out.ctypes.data))
     return out.reshape(-1, f)
+
+
+def packed_rows(packed: np.ndarray, dtype) -> np.ndarray:
+    """Logical [Np, K] rows of a packed weight.  f32 packing is row-major; bf16
+    packing is fragment-major: fragment (n // 16, k // 32) is 512 contiguous
+    elements, lane n % 16 + 16 * ((k % 32) // 8) holding k % 8 in 8 of them."""
+    np_, K = packed.shape
+    if dtype_code(dtype) != L.DTYPE_BF16:
+        return packed
+    t = packed.reshape(np_ // 16, K // 32, 4, 16, 8)      # [nb][ks][kq][nr][e]
+    return t.transpose(0, 3, 1, 2, 4).reshape(np_, K)      # [nb][nr][ks][kq][e]
 
 
 def to_device_packed(packed: list, dtype, device="cuda") -> torch.Tensor:

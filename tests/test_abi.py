@@ -137,7 +137,8 @@ def test_pack_gate_up_layout(lib, dtype):
     # whole [il gate | il up] blocks, zero-padded to the kernel's N tile
     assert np_ % (2 * il) == 0 and np_ >= 2 * (-(-f // il) * il)
     assert np_ % (256 if dtype == L.DTYPE_BF16 else 128) == 0
-    vals = synth.from_bf16_bits(packed) if dtype == L.DTYPE_BF16 else packed
+    vals = ops.packed_rows(packed, dtype)
+    vals = synth.from_bf16_bits(vals) if dtype == L.DTYPE_BF16 else vals
     rnd = synth.round_bf16 if dtype == L.DTYPE_BF16 else (lambda a: a)
     for p in range(np_):
         b, q = divmod(p, 2 * il)
@@ -155,7 +156,8 @@ def test_pack_down_layout(lib, dtype):
     down = rng.standard_normal((f, d)).astype(np.float32)
     packed = ops.pack_down(down, dtype)
     assert packed.shape == (512, f)
-    vals = synth.from_bf16_bits(packed) if dtype == L.DTYPE_BF16 else packed
+    vals = ops.packed_rows(packed, dtype)
+    vals = synth.from_bf16_bits(vals) if dtype == L.DTYPE_BF16 else vals
     rnd = synth.round_bf16 if dtype == L.DTYPE_BF16 else (lambda a: a)
     np.testing.assert_array_equal(vals[:d], rnd(down.T.copy()))
     assert not vals[d:].any()
@@ -170,5 +172,5 @@ def test_bf16_rounding_matches_numpy_model(lib):
     d = 64
     gate = np.zeros((d, 64), np.float32)
     gate[: len(vals), 0] = vals
-    packed = ops.pack_gate_up(gate, gate, L.DTYPE_BF16)
+    packed = ops.packed_rows(ops.pack_gate_up(gate, gate, L.DTYPE_BF16), L.DTYPE_BF16)
     np.testing.assert_array_equal(synth.from_bf16_bits(packed[0]), synth.round_bf16(gate[:, 0]))

@@ -170,6 +170,54 @@ def test_grouped_gemms_against_oracle(cuda, orc, cfg):
         assert rel_err(h_y[sel], y_ref) <= tol, ("y", g)
 
 
+# Decode-sized groups (every group <= 64 rows) take the skinny weight-streaming
+# kernel: empty groups, one 16-row MFMA tile, two tiles, two 32-row M-tiles;
+# K with 8, 4 and 2 K-steps per chunk (K % 256, % 128, % 64).
+@pytest.mark.parametrize("d,f,counts", [(1536, 1280, [0, 40, 3, 0, 16, 5]),
+                                        (320, 384, [17, 1, 0, 32, 14]),
+                                        (256, 192, [64]), (1536, 1280, [1, 0, 0, 0, 0, 0, 0, 0, 1])])
+def test_skinny_grouped_gemms(cuda, orc, d, f, counts):
+    rng = np.random.default_rng(d + f + len(counts))
+    G, rows = len(counts), sum(counts)
+    Tx = 100
+    x = synth.round_bf16(rng.standard_normal((Tx, d)))
+    gate = [synth.round_bf16(0.03 * rng.standard_normal((d, f))) for _ in range(G)]
+    up = [synth.round_bf16(0.03 * rng.standard_normal((d, f))) for _ in range(G)]
+    down = [synth.round_bf16(0.03 * rng.standard_normal((f, d))) for _ in range(G)]
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    row_token = rng.integers(0, Tx, rows).astype(np.int32)
+    gu = ops.to_device_packed([ops.pack_gate_up(gate[g], up[g], "bf16") for g in range(G)], "bf16")
+    dn = ops.to_device_packed([ops.pack_down(down[g], "bf16") for g in range(G)], "bf16")
+    off_d = torch.from_numpy(offsets).to("cuda")
+    rt_d = torch.from_numpy(row_token).to("cuda")
+    say("skinny", d, f, counts)
+    act = ops.grouped_gate_up_swiglu(dev(x, "bf16"), rt_d, off_d, G, rows, gu, d, f)
+    y = ops.grouped_down(act, off_d, G, rows, dn, d, f)
+    h_act, h_y = host(act), host(y)
+    for g in range(G):
+        r0, r1 = offsets[g], offsets[g + 1]
+        if r1 == r0:
+            continue
+        xr = x[row_token[r0:r1]]
+        a_ref = orc.swiglu(orc.matmul_2d(xr, gate[g]), orc.matmul_2d(xr, up[g]))
+        assert rel_err(h_act[r0:r1], a_ref) <= 2e-2, ("act", g)
+        assert rel_err(h_y[r0:r1], orc.matmul_2d(h_act[r0:r1], down[g])) <= 2e-2, ("y", g)
+
+
+@pytest.mark.parametrize("T", [1, 17, 33, 64])
+def test_moe_layer_decode_shapes(cuda, orc, T):
+    # The engine bounds every group by T, so these take the skinny kernels.
+    inp = synth.config_inputs(4, T=T)
+    say("layer decode", T)
+    layer = moe.MoELayer.from_inputs(inp)
+    out, stash = layer.forward_train(inp.x)
+    r = orc.moe_forward(inp)
+    np.testing.assert_array_equal(stash.selected_experts, r["sel"])
+    np.testing.assert_array_equal(stash.row_token, r["row_token"])
+    assert rel_err(out, r["out"]) <= TOL["bf16"]
+    layer.engine.close()
+
+
 # ------------------------------------------------------------- full layer --
 @pytest.mark.parametrize("cfg", [1, 2, 4])
 def test_moe_layer_full_against_oracle(cuda, orc, cfg):
