@@ -145,15 +145,20 @@ def main():
         touched = len(set(sel.reshape(-1).tolist())) + S
         gu_bytes = touched * d * 2 * f * es + rows * d * es + rows * f * es
         bw = gu_bytes / t_gu / 1e9
+        kernel = "grouped gate/up GEMM + fused SwiGLU, decode shape (skinny::skinny_gemm_kernel<true, 4, 1>)"
+        tfile = "pmc_config4_skinny_traffic.txt"
         roofline = {"kernel": kernel, "bound": "hbm", "achieved": bw, "peak": PEAK_HBM_GBPS,
-                    "unit": "GB/s", "frac": bw / PEAK_HBM_GBPS, "traffic": None,
+                    "unit": "GB/s", "frac": bw / PEAK_HBM_GBPS,
+                    "traffic": measured_traffic(tfile) if args.config == 4 else None,
+                    "traffic_source": f"profiles/{tfile} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE, "
+                                      "copy-calibrated)" if args.config == 4 else None,
                     "algorithmic_bytes_per_launch": gu_bytes, "experts_touched": touched,
                     "avg_launch_ms": ms["gate_up"]}
     else:
         roofline = {
             "kernel": kernel, "bound": "mfma", "achieved": gu_tflops, "peak": peak,
             "unit": "TFLOP/s", "frac": gu_tflops / peak,
-            "traffic": measured_traffic() if args.config == 2 else None,
+            "traffic": measured_traffic("pmc_config2_gate_up_traffic.txt") if args.config == 2 else None,
             "traffic_source": "profiles/pmc_config2_gate_up_traffic.txt (rocprofv3 --pmc "
                               "FETCH_SIZE, WRITE_SIZE, copy-calibrated)" if args.config == 2 else None,
             "algorithmic_flops_per_launch": flops_gate_up,
@@ -215,10 +220,10 @@ def copy_calibration():
     del src, dst
 
 
-def measured_traffic():
-    """HBM bytes per gate/up launch from the committed rocprofv3 --pmc summary
+def measured_traffic(name):
+    """HBM bytes per gate/up launch from a committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration), or None."""
-    path = os.path.join(ROOT, "profiles", "pmc_config2_gate_up_traffic.txt")
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as fh:
             for line in fh:

@@ -57,7 +57,39 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_host(verbose)
     return LIB
+
+
+HOST = os.path.join(HERE, "host")
+HOST_LIB = os.path.join(HERE, "libprichs_host.so")
+HOST_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_gpu_model_engine.cpp")
+HOST_TEST_BIN = os.path.join(ROOT, "tests", "cpp", "test_gpu_model_engine")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+
+def _gxx(args, what):
+    cxx = os.environ.get("CXX", "g++")
+    r = subprocess.run([cxx, *args], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{r.stderr}")
+
+
+def build_host(verbose: bool = False) -> str:
+    """The C++ host mirror of GpuModelEngine (libprichs_host.so, over the C ABI
+    of libprichs_hip.so) and its C++ test program; plain host C++ with the HIP
+    runtime, so g++ builds it.  rpaths are relative ($ORIGIN) so both travel
+    with the tree."""
+    flags = ["-std=c++17", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__",
+             "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"), "-I", HOST]
+    rocm_lib = ["-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"]
+    _gxx([*flags, "-fPIC", "-shared", os.path.join(HOST, "gpu_model_engine.cpp"), "-L", HERE,
+          "-lprichs_hip", *rocm_lib, "-Wl,-rpath,$ORIGIN", "-o", HOST_LIB], "libprichs_host.so")
+    _gxx([*flags, HOST_TEST_SRC, "-L", HERE, "-lprichs_host", "-lprichs_hip", *rocm_lib,
+          "-Wl,-rpath,$ORIGIN/../../prichs_amd", "-o", HOST_TEST_BIN], "test_gpu_model_engine")
+    if verbose:
+        print(f"built {HOST_LIB} and {HOST_TEST_BIN}")
+    return HOST_LIB
 
 
 if __name__ == "__main__":

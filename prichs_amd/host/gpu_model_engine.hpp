@@ -1,0 +1,159 @@
+// gpu_model_engine.hpp -- C++ host mirror of the reference's GpuModelEngine
+// hot-path interface (crates/prichs-cuda/src/engine.rs), over the C ABI of
+// libprichs_hip.so (include/prichs_hip.h).
+//
+// The reference engine is Rust; no Rust toolchain exists in this build, so
+// this mirror keeps its method names, argument meaning and error behaviour in
+// C++: a parameter registry over one flat f32 device buffer
+// (ParamMetadata, engine.rs:274-282), host slices in and host vectors out,
+// fixed workspace capacities checked before any device work, and every
+// failure reported as an error value rather than a crash (Rust's
+// anyhow::bail! becomes a thrown prichs_host::Error here).
+//
+// The methods that mirror the reference are the compatibility path (they
+// copy across PCIe like the originals).  gpu_moe_forward is the fast path:
+// the whole MoE layer on device buffers through the library's MoE engine.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <vector>
+
+struct prichs_moe_engine;
+
+namespace prichs_host {
+
+// anyhow::Error of the reference: a message, thrown where Rust returns Err.
+class Error : public std::runtime_error {
+ public:
+  explicit Error(const std::string &msg) : std::runtime_error(msg) {}
+};
+
+// engine.rs:274-282.
+struct ParamMetadata {
+  size_t id = 0;
+  size_t offset = 0;  // in f32 elements of the flat weight buffer
+  size_t len = 0;
+  size_t rows = 0;
+  size_t cols = 0;
+  bool apply_weight_decay = false;
+};
+
+// Workspace sizes in f32 elements (the reference fixes them in new(),
+// engine.rs:363-649).  The defaults cover T = 16384 rows at d = 1536 and
+// f = 1280; configuration 2 of the benchmark fits.
+struct Capacity {
+  size_t act_in = 16384 * 1536;   // normed2 / GEMM input
+  size_t act_out = 16384 * 2560;  // GEMM output
+  size_t moe_dim = 16384 * 1280;  // [rows, f] intermediates
+  size_t rope_cache = 4096 * 64;  // cos / sin entries
+  size_t max_rows = 16384;        // RMSNorm rows (rstd)
+};
+
+// (x, gate, up, act, out) of gpu_moe_forward_expert; the shared form has no x.
+using SharedOut = std::tuple<std::vector<float>, std::vector<float>, std::vector<float>,
+                             std::vector<float>>;
+using ExpertOut = std::tuple<std::vector<float>, std::vector<float>, std::vector<float>,
+                             std::vector<float>, std::vector<float>>;
+
+class GpuModelEngine {
+ public:
+  // engine.rs:363: one (rows, cols, apply_weight_decay) triple per parameter.
+  explicit GpuModelEngine(const std::vector<std::tuple<size_t, size_t, bool>> &param_shapes,
+                          const Capacity &cap = Capacity());
+  ~GpuModelEngine();
+  GpuModelEngine(const GpuModelEngine &) = delete;
+  GpuModelEngine &operator=(const GpuModelEngine &) = delete;
+
+  const std::vector<ParamMetadata> &params() const { return meta_; }
+
+  // engine.rs:668-689 / 691-708: one host slice per parameter, reference layout.
+  void upload_weights(const std::vector<std::vector<float>> &param_slices);
+  void download_weights(std::vector<std::vector<float>> &param_slices) const;
+
+  // engine.rs:757-826: out[m, n] = x[m, k] @ W[param_id] ([k, n]).
+  void forward_gemm(size_t param_id, const std::vector<float> &x, std::vector<float> &out,
+                    size_t m, size_t k, size_t n);
+
+  // engine.rs:1788-1846: out = (x * rstd) * w per row, rstd = 1/sqrt(mean(x^2) + eps).
+  void gpu_rmsnorm_forward(const std::vector<float> &x, size_t param_id, std::vector<float> &out,
+                           std::vector<float> &rstd, size_t seq_len, size_t hidden_dim,
+                           float eps);
+
+  // engine.rs:1162-1179.
+  void upload_rope_cache(const std::vector<float> &cos_cache, const std::vector<float> &sin_cache);
+
+  // engine.rs:1917-2051: the shared expert on all rows of normed2, which stays
+  // resident for the routed experts; its output starts the MoE accumulator.
+  SharedOut gpu_moe_forward_shared(const std::vector<float> &normed2, size_t gate_id,
+                                   size_t up_id, size_t down_id, size_t seq_len,
+                                   size_t hidden_dim, size_t intermediate_dim);
+
+  // engine.rs:2054-2223: one routed expert on the rows token_indices of the
+  // resident normed2; accum[token] += weight * out[row].
+  ExpertOut gpu_moe_forward_expert(const std::vector<int32_t> &token_indices,
+                                   const std::vector<float> &weights, size_t gate_id,
+                                   size_t up_id, size_t down_id, size_t hidden_dim,
+                                   size_t intermediate_dim);
+
+  // engine.rs:2226-2239: the accumulated MoE output.
+  void gpu_moe_finalize_forward(std::vector<float> &total_out) const;
+
+  // engine.rs:2694-2702.
+  void sync_stream() const;
+
+  // ---- Fast path (no reference counterpart): the fused MoE layer on device
+  // buffers.  Builds a libprichs_hip MoE engine from registered parameters:
+  // router [d, E], the shared expert's (gate, up, down) and each routed
+  // expert's, with dtype PRICHS_DTYPE_BF16 or PRICHS_DTYPE_F32.  Returns a
+  // layer id.
+  size_t create_moe_layer(size_t router_id, const std::vector<float> &router_bias,
+                          size_t shared_gate, size_t shared_up, size_t shared_down,
+                          const std::vector<std::tuple<size_t, size_t, size_t>> &experts,
+                          size_t top_k, int dtype, size_t max_tokens);
+  // x [T, d] and out [T, d] are device pointers of the layer's dtype; enqueued
+  // on `stream` (a hipStream_t; null = default stream), nothing allocated.
+  void gpu_moe_forward(size_t layer_id, const void *x_dev, size_t T, void *out_dev,
+                       void *stream = nullptr);
+  // The aux-free bias update of moe.rs:228-245 reaches the device this way.
+  void set_moe_router_bias(size_t layer_id, const std::vector<float> &router_bias);
+
+ private:
+  struct PackedGemm;  // f32 weights packed for prichs_gemm (zero-padded to 16)
+  struct MoeLayer {
+    prichs_moe_engine *eng = nullptr;
+    size_t d = 0, E = 0;
+    int dtype = 0;
+  };
+
+  void release();  // frees every device buffer and engine (destructor, failed constructor)
+
+  void gemm_dev(size_t param_id, const float *x_dev, size_t ldx, float *out_dev, size_t ldo,
+                size_t m);
+  const PackedGemm &packed(size_t param_id);
+  void check_param(size_t id, const char *who) const;
+
+  std::vector<ParamMetadata> meta_;
+  Capacity cap_;
+  float *dev_weights_ = nullptr;
+  // Workspace (f32): GEMM staging with padded leading dimensions.
+  float *dev_act_in_ = nullptr;   // normed2, resident between shared and experts
+  float *dev_act_out_ = nullptr;  // forward_gemm / rmsnorm output
+  float *dev_x_ = nullptr;        // gathered expert rows
+  float *dev_gate_ = nullptr, *dev_up_ = nullptr, *dev_act_ = nullptr;
+  float *dev_out_ = nullptr;      // expert output rows
+  float *dev_moe_out_ = nullptr;  // MoE accumulator
+  float *dev_rstd_ = nullptr;
+  float *dev_cos_ = nullptr, *dev_sin_ = nullptr;
+  int32_t *dev_idx_ = nullptr;
+  float *dev_w_ = nullptr;
+  size_t moe_rows_ = 0, moe_ld_ = 0, moe_d_ = 0;  // layout of the accumulator
+  size_t act_in_ld_ = 0;                         // leading dimension of normed2
+  std::vector<PackedGemm *> packed_;
+  std::vector<MoeLayer> layers_;
+};
+
+}  // namespace prichs_host
