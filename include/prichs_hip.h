@@ -322,6 +322,17 @@ int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_router,
 int prichs_moe_engine_set_router_bias(prichs_moe_engine *eng,
                                       const float *router_bias);
 
+/* The aux-loss-free bias update on device: MoELayer::update_aux_free_bias
+ * (crates/prichs-model/src/moe.rs:228-245) as its call site drives it
+ * (crates/prichs-model/src/model.rs:1541-1547): counts = assignments per
+ * expert in the last forward (the permutation's group sizes), total_tokens =
+ * that forward's T; bias[i] += gamma * (k/E - counts[i]/T) in f32.  Enqueued
+ * on `stream` after the forward; no-op after a forward of T = 0. */
+int prichs_moe_engine_update_router_bias(prichs_moe_engine *eng, float gamma,
+                                         void *stream);
+/* Copies the current router bias f32 [E] to host memory (synchronous). */
+int prichs_moe_engine_get_router_bias(const prichs_moe_engine *eng, float *out);
+
 /* Full MoELayer forward (moe.rs:93-225) on device: x [T, d] of the engine's
  * dtype (device), optional concept bias f32 [n_concept] (device, may be
  * NULL), out [T, d] of out_dtype (device).  T <= max_tokens. */

@@ -70,6 +70,8 @@ def lib():
                                         sz, _f32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p,
                                         _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.orc_block_forward.restype = C.c_int
+        L.orc_update_aux_free_bias.argtypes = [_f32p, C.c_void_p, sz, sz, sz, C.c_float]
+        L.orc_update_aux_free_bias.restype = None
         L.orc_num_threads.restype = C.c_int
         L.orc_set_num_threads.argtypes = [C.c_int]
         L.orc_set_num_threads.restype = None
@@ -160,6 +162,15 @@ def bin_tokens(sel, gw, E):
     token_row = np.empty(T * k, np.int32)
     lib().orc_bin_tokens(sel, gw, T, E, k, offsets, row_token, row_weight, token_row)
     return offsets, row_token, row_weight, token_row
+
+
+def update_aux_free_bias(bias, counts, top_k, total_tokens, gamma):
+    """MoELayer::update_aux_free_bias (moe.rs:228-245) on a copy of bias."""
+    b = _c(bias).copy()
+    cnt = np.ascontiguousarray(counts, dtype=np.int64)
+    lib().orc_update_aux_free_bias(b, cnt.ctypes.data, b.size, top_k, total_tokens,
+                                   C.c_float(gamma))
+    return b
 
 
 def moe_forward(inp, concept_bias=None):

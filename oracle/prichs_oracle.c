@@ -39,6 +39,9 @@
  *                            row 0 attends only to itself.
  *   orc_block_forward        float64 re-assembly of the block from the pinned
  *                            pieces (RMSNorm, attention, MoE, residuals).
+ *   orc_update_aux_free_bias float64 closed form; the update sums to ~0 over
+ *                            the experts (sum of counts = k * T); balanced
+ *                            routing leaves the bias unchanged; T = 0 no-op.
  */
 #include <math.h>
 #include <stddef.h>
@@ -255,6 +258,26 @@ static int orc_expert_ffn(const float *xin, size_t m, size_t d, size_t f,
   free(g);
   free(u);
   return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MoELayer::update_aux_free_bias: crates/prichs-model/src/moe.rs:228-245.    */
+/* target = top_k / E; per expert actual = counts[i] / total_tokens,          */
+/* diff = target - actual, bias[i] += gamma * diff (all f32, usize -> f32     */
+/* conversions rounded to nearest).  Returns without change when             */
+/* total_tokens == 0 or E == 0.  The reference's training step passes the    */
+/* per-expert assignment counts of the last batch and its token count         */
+/* (model.rs:1541-1547).                                                      */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_update_aux_free_bias(float *bias, const int64_t *counts, size_t E,
+                                      size_t top_k, size_t total_tokens, float gamma) {
+  if (total_tokens == 0 || E == 0) return;
+  const float target = (float)top_k / (float)E;
+  for (size_t i = 0; i < E; ++i) {
+    const float actual = (float)counts[i] / (float)total_tokens;
+    const float diff = target - actual;
+    bias[i] += gamma * diff;
+  }
 }
 
 /* ------------------------------------------------------------------------ */

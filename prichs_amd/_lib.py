@@ -110,6 +110,8 @@ SIGNATURES = {
     "prichs_moe_engine_destroy": (_i, [_vp]),
     "prichs_moe_engine_upload": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "prichs_moe_engine_set_router_bias": (_i, [_vp, _vp]),
+    "prichs_moe_engine_update_router_bias": (_i, [_vp, _f, _vp]),
+    "prichs_moe_engine_get_router_bias": (_i, [_vp, _vp]),
     "prichs_moe_engine_forward": (_i, [_vp, _vp, _sz, _vp, _sz, _vp, _i, _vp]),
     "prichs_moe_engine_stash": (_i, [_vp, C.POINTER(MoEStash)]),
     "prichs_moe_engine_set_timing": (_i, [_vp, _i]),

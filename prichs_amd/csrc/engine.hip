@@ -237,6 +237,51 @@ extern "C" int prichs_moe_engine_set_router_bias(prichs_moe_engine *eng, const f
   return PRICHS_OK;
 }
 
+namespace prichs {
+namespace {
+// MoELayer::update_aux_free_bias (crates/prichs-model/src/moe.rs:228-245) with
+// the counts of its call site (model.rs:1541-1547: assignments per expert over
+// the last batch, = offsets[e+1] - offsets[e]) and total_tokens = T.  f32
+// arithmetic in the reference's order: target = k / E, actual = count / T,
+// diff = target - actual, bias += gamma * diff (division correctly rounded,
+// no contraction).
+__global__ void aux_free_bias_kernel(float *bias, const int32_t *offsets, int E, int T, int k,
+                                     float gamma) {
+#pragma clang fp contract(off)
+  const int i = threadIdx.x;
+  if (i >= E) return;
+  const float target = (float)k / (float)E;
+  const float actual = (float)(offsets[i + 1] - offsets[i]) / (float)T;
+  const float diff = target - actual;
+  const float step = gamma * diff;
+  bias[i] = bias[i] + step;
+}
+}  // namespace
+}  // namespace prichs
+
+extern "C" int prichs_moe_engine_update_router_bias(prichs_moe_engine *eng, float gamma,
+                                                    void *stream) {
+  PRICHS_REQUIRE(eng != nullptr, "engine_update_router_bias: null engine");
+  if (!eng->uploaded) return fail(PRICHS_ERR_STATE, "engine_update_router_bias: weights not uploaded");
+  if (eng->last_T == 0) return PRICHS_OK;  // the reference returns on total_tokens == 0
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_update_router_bias: cannot select device");
+  hipLaunchKernelGGL(aux_free_bias_kernel, dim3(1), dim3(PRICHS_MAX_EXPERTS), 0, as_stream(stream),
+                     eng->router_bias, eng->offsets, (int)eng->E, (int)eng->last_T, (int)eng->k,
+                     gamma);
+  PRICHS_LAUNCH_CHECK("engine_update_router_bias");
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_get_router_bias(const prichs_moe_engine *eng, float *out) {
+  PRICHS_REQUIRE(eng && out, "engine_get_router_bias: null pointer argument");
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_get_router_bias: cannot select device");
+  PRICHS_HIP_TRY(hipMemcpy(out, eng->router_bias, sizeof(float) * eng->E, hipMemcpyDeviceToHost),
+                 "engine_get_router_bias");
+  return PRICHS_OK;
+}
+
 extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, size_t T,
                                          const float *concept_bias, size_t n_concept, void *out,
                                          int out_dtype, void *stream) {

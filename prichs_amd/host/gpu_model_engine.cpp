@@ -442,4 +442,18 @@ void GpuModelEngine::set_moe_router_bias(size_t layer_id, const std::vector<floa
          "prichs_moe_engine_set_router_bias");
 }
 
+void GpuModelEngine::update_moe_router_bias(size_t layer_id, float gamma, void *stream) {
+  if (layer_id >= layers_.size()) bail(fmt("update_moe_router_bias: no MoE layer %zu", layer_id));
+  lib_ok(prichs_moe_engine_update_router_bias(layers_[layer_id].eng, gamma, stream),
+         "prichs_moe_engine_update_router_bias");
+}
+
+std::vector<float> GpuModelEngine::moe_router_bias(size_t layer_id) const {
+  if (layer_id >= layers_.size()) bail(fmt("moe_router_bias: no MoE layer %zu", layer_id));
+  std::vector<float> b(layers_[layer_id].E);
+  lib_ok(prichs_moe_engine_get_router_bias(layers_[layer_id].eng, b.data()),
+         "prichs_moe_engine_get_router_bias");
+  return b;
+}
+
 }  // namespace prichs_host

@@ -118,8 +118,12 @@ class GpuModelEngine {
   // on `stream` (a hipStream_t; null = default stream), nothing allocated.
   void gpu_moe_forward(size_t layer_id, const void *x_dev, size_t T, void *out_dev,
                        void *stream = nullptr);
-  // The aux-free bias update of moe.rs:228-245 reaches the device this way.
+  // The aux-free bias (moe.rs:60) of a layer: set from the host, updated on
+  // device from the last forward's routing (moe.rs:228-245 as model.rs:
+  // 1541-1547 drives it), read back.
   void set_moe_router_bias(size_t layer_id, const std::vector<float> &router_bias);
+  void update_moe_router_bias(size_t layer_id, float gamma, void *stream = nullptr);
+  std::vector<float> moe_router_bias(size_t layer_id) const;
 
  private:
   struct PackedGemm;  // f32 weights packed for prichs_gemm (zero-padded to 16)

@@ -88,6 +88,17 @@ class MoEEngine:
         b = np.ascontiguousarray(bias, dtype=np.float32)
         L.check(self.lib.prichs_moe_engine_set_router_bias(self.handle, b.ctypes.data))
 
+    def update_router_bias(self, gamma: float, stream=None):
+        """prichs_moe_engine_update_router_bias: the aux-loss-free update
+        (moe.rs:228-245) from the last forward's routing, on device."""
+        L.check(self.lib.prichs_moe_engine_update_router_bias(self.handle, C.c_float(gamma),
+                                                              ops._stream(stream)))
+
+    def router_bias(self) -> np.ndarray:
+        out = np.empty(self.E, dtype=np.float32)
+        L.check(self.lib.prichs_moe_engine_get_router_bias(self.handle, out.ctypes.data))
+        return out
+
     def forward(self, x: torch.Tensor, concept_bias: torch.Tensor | None = None,
                 out: torch.Tensor | None = None, out_dtype=None, stream=None) -> torch.Tensor:
         if ops.dtype_code(x) != self.dtype:
@@ -232,6 +243,15 @@ class MoELayer:
             row_token=h["row_token"][: T * k], row_weight=h["row_weight"], act=act[: T * k],
             routed_out=y[: T * k], shared_out=y[T * k:] if S else None)
         return out, stash
+
+    def update_aux_free_bias_on_device(self, gamma: float = 0.001):
+        """The update of the reference's training step (model.rs:1541-1547:
+        counts of the last forward's selected experts, total = its tokens,
+        gamma 0.001) computed on device from the permutation's group sizes;
+        the host copy of the bias follows."""
+        self.engine.update_router_bias(gamma)
+        torch.cuda.synchronize()
+        self.router_bias = self.engine.router_bias()
 
     def update_aux_free_bias(self, expert_token_counts, total_tokens: int, gamma: float):
         """moe.rs:228-245 (host arithmetic in f32), then pushes the bias to the engine."""

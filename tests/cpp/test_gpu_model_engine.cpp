@@ -8,7 +8,7 @@
 //                                              without a device fails cleanly
 //        test_gpu_model_engine FIXTURE_DIR    also the config-1 parity test on
 //                                              oracle fixtures (see
-//                                              tests/test_gpu_host_cpp.py)
+//                                              tests/test_host_cpp.py)
 // Exit status 0 when every test passed.
 #include <hip/hip_runtime.h>
 
@@ -281,6 +281,20 @@ void test_moe_config1_parity(const std::string &dir) {
   const double e_fused = rel_err(fused, fx.f32.at("out"));
   std::printf("    fused MoE output rel err %.2e\n", e_fused);
   CHECK(e_fused <= 1e-4, "fused MoE output rel err %.3e > 1e-4", e_fused);
+
+  // The aux-loss-free update of the training step (model.rs:1541-1547,
+  // moe.rs:228-245) on device, against the same f32 steps on the host.
+  engine.update_moe_router_bias(layer, 0.001f);
+  const std::vector<float> b = engine.moe_router_bias(layer);
+  const std::vector<float> &b0 = fx.f32.at("router_bias");
+  for (size_t e = 0; e < E; ++e) {
+    const float target = (float)k / (float)E;
+    const float actual = (float)(off[e + 1] - off[e]) / (float)T;
+    const float diff = target - actual;
+    const float step = 0.001f * diff;
+    const float want = b0[e] + step;
+    CHECK(b[e] == want, "bias[%zu] %.9g vs %.9g", e, b[e], want);
+  }
 }
 
 }  // namespace

@@ -218,6 +218,28 @@ def test_moe_layer_decode_shapes(cuda, orc, T):
     layer.engine.close()
 
 
+def test_aux_free_bias_update_on_device(cuda, orc):
+    # moe.rs:228-245 driven as model.rs:1541-1547 drives it, on device; then the
+    # next forward routes with the new bias exactly as the oracle does.
+    inp = synth.config_inputs(2, T=2048)
+    layer = moe.MoELayer.from_inputs(inp)
+    _, stash = layer.forward_train(inp.x)
+    bias0 = layer.router_bias.copy()
+    counts = np.bincount(stash.selected_experts.reshape(-1), minlength=inp.E)
+    layer.update_aux_free_bias_on_device(0.001)
+    expect = orc.update_aux_free_bias(bias0, counts, inp.k, inp.T, 0.001)
+    np.testing.assert_array_equal(layer.router_bias.view(np.uint32), expect.view(np.uint32))
+    assert not np.array_equal(expect, bias0)
+    _, stash2 = layer.forward_train(inp.x)
+    _, sel2, _ = orc.route(inp.x, inp.w_router, expect, inp.k)
+    np.testing.assert_array_equal(stash2.selected_experts, sel2)
+    # After a forward of zero tokens the update is a no-op (total_tokens == 0).
+    layer.engine.forward(torch.empty((0, inp.d), dtype=torch.bfloat16, device="cuda"))
+    layer.update_aux_free_bias_on_device(0.001)
+    np.testing.assert_array_equal(layer.router_bias, expect)
+    layer.engine.close()
+
+
 # ------------------------------------------------------------- full layer --
 @pytest.mark.parametrize("cfg", [1, 2, 4])
 def test_moe_layer_full_against_oracle(cuda, orc, cfg):

@@ -376,3 +376,23 @@ def test_block_forward_float64_reassembly(orc):
     ref_moe = orc.moe_forward(moe_in)
     assert rel_err(r["moe"], _moe_float64(moe_in, ref_moe["sel"], ref_moe["gw"])) < 1e-4
     assert rel_err(r["out"], x1 + r["moe"]) < 1e-6
+
+
+def test_update_aux_free_bias(orc):
+    # moe.rs:228-245: float64 closed form, invariants and the no-op cases.
+    rng = np.random.default_rng(3)
+    E, k, T, gamma = 8, 2, 512, 0.001
+    bias = (0.01 * rng.standard_normal(E)).astype(np.float32)
+    counts = rng.multinomial(k * T, np.full(E, 1.0 / E))
+    got = orc.update_aux_free_bias(bias, counts, k, T, gamma)
+    ref = bias.astype(np.float64) + gamma * (k / E - counts / T)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-7)
+    # counts sum to k*T, so the increments cancel over the experts
+    assert abs(float((got.astype(np.float64) - bias).sum())) < 1e-7
+    # overloaded experts go down, underloaded ones up
+    assert np.all(np.sign(got - bias)[counts > k * T / E] < 0)
+    assert np.all(np.sign(got - bias)[counts < k * T / E] > 0)
+    # balanced routing leaves the bias bit-identical; T = 0 is a no-op
+    bal = orc.update_aux_free_bias(bias, np.full(E, k * T // E), k, T, gamma)
+    np.testing.assert_array_equal(bal, bias)
+    np.testing.assert_array_equal(orc.update_aux_free_bias(bias, counts, k, 0, gamma), bias)
