@@ -7,8 +7,11 @@
 // materialised: each workgroup streams 64-row K/V blocks through LDS and
 // keeps an online softmax (running max m and partial sums l per query row).
 //
-// Layout per workgroup: one (sequence b, query head h, 128-query block);
-// 4 wave64s, each owning 32 query rows (two 16-row MFMA blocks).
+// Layout per workgroup: 4 wave64s, each owning 32 query rows (two 16-row
+// MFMA blocks) of one query head.  With HPW heads per workgroup the 4 waves
+// are HPW heads of one kv group x (4 / HPW) row blocks, so the workgroup
+// covers 128 / HPW queries and every K/V tile it stages in LDS serves HPW
+// query heads (HPW = 4 at 12 Q / 3 KV heads: the whole group shares a tile).
 //   S^T = K Q^T     v_mfma_f32_16x16x32_bf16(K frag, Q frag): the lane owning
 //                   query column q = lane % 16 holds the scores of kv rows
 //                   4*(lane/16) + r of every 16-row kv block;
@@ -32,7 +35,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHd = 128;      // head dim supported by this kernel
-constexpr int kBQ = 128;      // query rows per workgroup
 constexpr int kBKV = 64;      // kv rows per block
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
@@ -50,30 +52,32 @@ __device__ __forceinline__ int k_off(int kv, int c) { return kv * kHd + ((c ^ (k
 // V^T tile: element offset of (d row, 8-byte chunk c in 0..15) of 64 kv.
 __device__ __forceinline__ int vt_off(int d, int c) { return d * kBKV + ((c ^ (d & 15)) << 2); }
 
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-}
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) { return pack_bf16x2(a, b); }
 
 // q/k/v/o: row r of sequence b is row b*S + r; head h of q/o starts at column
 // h*128, kv head j of k/v at column j*128 (leading dimensions ldq/ldk/ldv/ldo).
+template <int HPW>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const bf16_t *__restrict__ q, int ldq, const bf16_t *__restrict__ k, int ldk,
     const bf16_t *__restrict__ v, int ldv, bf16_t *__restrict__ o, int ldo, int S, int Hq,
     int group, float scale_log2) {
+  static_assert(kWaves % HPW == 0, "whole row blocks per head");
+  constexpr int kRowsWg = 32 * kWaves / HPW;  // query rows per workgroup
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   bf16_t *ks = lds;
   bf16_t *vts = lds + kKElems;
 
-  // Grid (head, sequence, query block): blocks are dispatched x-fastest, so
-  // every head's longest causal rows (the last query block) go first.
-  const int n_qb = (S + kBQ - 1) / kBQ;
-  const int h = blockIdx.x;
+  // Grid (head set, sequence, query block): blocks are dispatched x-fastest,
+  // so every head set's longest causal rows (the last query block) go first.
+  const int n_qb = (S + kRowsWg - 1) / kRowsWg;
+  const int sets = group / HPW;  // head sets per kv group
+  const int kvh = blockIdx.x / sets;
   const int b = blockIdx.y;
   const int qb = n_qb - 1 - (int)blockIdx.z;
-  const int kvh = h / group;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int h = kvh * group + (blockIdx.x - kvh * sets) * HPW + wave % HPW;
   const int g = lane >> 4;    // 0..3
   const int l16 = lane & 15;  // 0..15
 
@@ -82,7 +86,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   const bf16_t *vbase = v + seq0 * ldv + (size_t)kvh * kHd;
 
   // Query rows of this wave: q0 + 16*nb + l16 (nb = 0, 1).
-  const int q0 = qb * kBQ + wave * 32;
+  const int q0 = qb * kRowsWg + (wave / HPW) * 32;
 
   // Q fragments (B operand of S^T = K Q^T): lane holds Q[q][32kk + 8g .. +8].
   bf16x8 qf[2][4];
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   float l_part[2] = {0.f, 0.f};              // this lane's share of the row sum
 
   // kv blocks up to the last query row of the workgroup (causal).
-  const int q_last = min(S, (qb + 1) * kBQ) - 1;
+  const int q_last = min(S, (qb + 1) * kRowsWg) - 1;
   const int n_kvb = q_last / kBKV + 1;
 
   for (int kb = 0; kb < n_kvb; ++kb) {
@@ -158,6 +162,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     // Online softmax.  st[c][nb][r] = score of (query q0 + 16nb + l16,
     // kv kv0 + 16c + 4g + r).
     u32x4 pf[2][2];  // P fragments: [nb][32-row kv step]
+    // Only blocks reaching past this wave's first query row or the sequence
+    // end need the causal / length mask (wave-uniform test).
+    const bool masked = kv0 + kBKV - 1 > q0 || kv0 + kBKV > S;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const int qrow = q0 + 16 * nb + l16;
@@ -169,7 +176,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
         for (int r = 0; r < 4; ++r) {
           const int kv = kv0 + 16 * c + 4 * g + r;
           float x = st[c][nb][r] * scale_log2;
-          x = (kv <= qrow && kv < S) ? x : -INFINITY;
+          if (masked) x = (kv <= qrow && kv < S) ? x : -INFINITY;
           s[4 * c + r] = x;
           mloc = fmaxf(mloc, x);
         }
@@ -188,8 +195,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
         psum += p;
       }
       l_part[nb] = l_part[nb] * alpha + psum;
+      // Rescale the output rows only when some row's running max moved
+      // (alpha == 1 exactly otherwise, so skipping changes nothing).
+      if (__any(alpha != 1.0f)) {
 #pragma unroll
-      for (int jd = 0; jd < 8; ++jd) oacc[jd][nb] = oacc[jd][nb] * alpha;
+        for (int jd = 0; jd < 8; ++jd) oacc[jd][nb] = oacc[jd][nb] * alpha;
+      }
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
         // k slots 0..3: kv block 2 ks2 (rows 4g + r); slots 4..7: block 2 ks2 + 1.
@@ -268,15 +279,20 @@ extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k
   const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
   PRICHS_REQUIRE(al % 16 == 0, "attention: q/k/v/o must be 16-byte aligned");
-  const int n_qb = (int)cdiv(seq_len, (size_t)kBQ);
+  const int group = (int)(n_heads / n_kv_heads);
+  // Heads per workgroup: the largest of 4, 2, 1 dividing the GQA group.
+  const int hpw = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+  const int rows_wg = 32 * kWaves / hpw;
+  const int n_qb = (int)cdiv(seq_len, (size_t)rows_wg);
   const float scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.4426950408889634f;
   PRICHS_REQUIRE(n_qb <= 65535, "attention: seq_len too large");
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)n_heads, (unsigned)batch, (unsigned)n_qb),
-                     dim3(kThreads), kLdsBytes, as_stream(stream),
+  const dim3 grid((unsigned)(n_heads / hpw), (unsigned)batch, (unsigned)n_qb);
+  auto kern = hpw == 4 ? attn_fwd_kernel<4> : hpw == 2 ? attn_fwd_kernel<2> : attn_fwd_kernel<1>;
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), kLdsBytes, as_stream(stream),
                      static_cast<const bf16_t *>(q), (int)ldq, static_cast<const bf16_t *>(k),
                      (int)ldk, static_cast<const bf16_t *>(v), (int)ldv,
-                     static_cast<bf16_t *>(o), (int)ldo, (int)seq_len, (int)n_heads,
-                     (int)(n_heads / n_kv_heads), scale_log2);
+                     static_cast<bf16_t *>(o), (int)ldo, (int)seq_len, (int)n_heads, group,
+                     scale_log2);
   PRICHS_LAUNCH_CHECK("attention launch");
   return PRICHS_OK;
 }

@@ -100,6 +100,15 @@ __device__ inline float silu_fast(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// Two floats -> two bf16 (round to nearest even) packed low/high in 32 bits:
+// one v_cvt_pk_bf16_f32 (the software f32_to_bf16 agrees on every non-NaN).
+typedef float prichs_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 prichs_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const prichs_f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, prichs_bf16x2));
+}
+
 // prichs_grouped_gate_up_swiglu / prichs_grouped_down with a tighter bound on
 // every group's row count (a caller that knows T passes T): decode-sized
 // groups then take the skinny weight-streaming kernel.

@@ -382,11 +382,12 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
           for (int j = 0; j < NJ / 2; ++j) {
             const int col = cbase + 16 * j;
             if (col < n_store) {
-              uint32_t h[4];
+              float h[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                h[r] = f32_to_bf16(PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r]);
-              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+                h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r];
+              *reinterpret_cast<u32x2 *>(crow + col) =
+                  u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
             }
           }
         }
@@ -402,10 +403,9 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
           for (int j = 0; j < NJ; ++j) {
             const int col = cbase + 16 * j;
             if (col < n_store) {
-              uint32_t h[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(acc[i][j][r]);
-              *reinterpret_cast<u32x2 *>(crow + col) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+              const f32x4 a = acc[i][j];
+              *reinterpret_cast<u32x2 *>(crow + col) =
+                  u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
             }
           }
         }
@@ -721,11 +721,11 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
         if (m < r1 && col < n_store) {
           const f32x4 gv = gate_s[wn - 2][t][lane];
           const f32x4 uv = t == 0 ? acc0 : acc1;
-          uint32_t h[4];
+          float h[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(PRICHS_BF16_SILU(gv[r]) * uv[r]);
+          for (int r = 0; r < 4; ++r) h[r] = PRICHS_BF16_SILU(gv[r]) * uv[r];
           *reinterpret_cast<u32x2 *>(C + (long long)m * ldc + col) =
-              u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+              u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
         }
       }
     }
@@ -736,11 +736,8 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
       const int m = mr + 16 * t;
       if (m < r1 && col < n_store) {
         const f32x4 v = t == 0 ? acc0 : acc1;
-        uint32_t h[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16(v[r]);
         *reinterpret_cast<u32x2 *>(C + (long long)m * ldc + col) =
-            u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       }
     }
   }

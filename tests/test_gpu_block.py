@@ -79,8 +79,11 @@ def _attention_f64(q, k, v, B, S, Hq, Hkv, heads=None, seqs=None):
     return out
 
 
+# GQA groups of 1, 2 and 4 query heads per kv head (1, 2 or 4 heads share a
+# workgroup's K/V tiles), ragged and single-row sequences.
 @pytest.mark.parametrize("B,S,Hq,Hkv", [(2, 200, 4, 2), (1, 128, 2, 1), (1, 64, 1, 1),
-                                        (2, 333, 3, 3), (1, 1, 2, 1)])
+                                        (2, 333, 3, 3), (1, 1, 2, 1), (1, 100, 8, 2),
+                                        (2, 257, 4, 1), (1, 31, 12, 3)])
 def test_attention_kernel(cuda, B, S, Hq, Hkv):
     rng = np.random.default_rng(B * 1000 + S + Hq)
     hd = 128
