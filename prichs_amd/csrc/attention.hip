@@ -21,9 +21,16 @@
 //                   each 32-row step (g = lane / 16), and the V^T fragment
 //                   reads the same kv rows -- so no lane exchange is needed,
 //                   and the lane that owns query q also owns its output row.
-// K sits in LDS row-major ([kv][128], 16-byte chunks XOR-swizzled by row);
-// V is written transposed ([128 d][64 kv], 8-byte chunks XOR-swizzled by
-// row) so both fragment reads are bank-conflict free.
+// K and V go straight from global memory to LDS (global_load_lds, no VGPR
+// round trip) into two stage buffers, so the next block's tiles stream in
+// while this block is computed.  Both tiles are row-major [64 kv][128 d] with
+// their 16-byte chunks XOR-swizzled per row (the DMA lane for LDS slot s of
+// row r fetches logical chunk s ^ key(r)): K fragments are plain 16-byte
+// reads, and the V^T fragments of the P.V product come from the transposing
+// LDS read ds_read_b64_tr_b16 -- within each 16-lane group it hands lane i
+// element j = M[4j + i/4][i % 4] of the group's 16 x 4 loaded elements, so
+// lanes reading rows r0 + m/4, columns 4 (m % 4).. of a 16-column block give
+// lane i that column's 4 consecutive kv values.
 #include "common.hpp"
 
 namespace prichs {
@@ -38,19 +45,43 @@ constexpr int kHd = 128;      // head dim supported by this kernel
 constexpr int kBKV = 64;      // kv rows per block
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kKElems = kBKV * kHd;   // K tile [64][128]
-constexpr int kVElems = kHd * kBKV;   // V^T tile [128][64]
-constexpr size_t kLdsBytes = (size_t)(kKElems + kVElems) * sizeof(bf16_t);
+constexpr int kTileElems = kBKV * kHd;                   // one K or V tile [64][128]
+constexpr int kStageElems = 2 * kTileElems;              // K then V
+constexpr size_t kLdsBytes = 2 * (size_t)kStageElems * sizeof(bf16_t);  // two stages
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// K tile: element offset of (kv row, 16-byte chunk c in 0..15).
-__device__ __forceinline__ int k_off(int kv, int c) { return kv * kHd + ((c ^ (kv & 15)) << 3); }
-// V^T tile: element offset of (d row, 8-byte chunk c in 0..15) of 64 kv.
-__device__ __forceinline__ int vt_off(int d, int c) { return d * kBKV + ((c ^ (d & 15)) << 2); }
+// Chunk keys: K fragment reads (16 kv rows, one chunk) and V transposing
+// reads (4 rows x 2 chunks per 16-lane group) both land on distinct banks.
+__device__ __forceinline__ int k_key(int kv) { return kv & 15; }
+__device__ __forceinline__ int v_key(int kv) { return (2 * kv) & 15; }
+// Element offset of (kv row, logical 16-byte chunk c) in a K / V tile.
+__device__ __forceinline__ int k_off(int kv, int c) { return kv * kHd + ((c ^ k_key(kv)) << 3); }
+__device__ __forceinline__ int v_off(int kv, int c) { return kv * kHd + ((c ^ v_key(kv)) << 3); }
+
+__device__ __forceinline__ void dma_16b(const bf16_t *src, bf16_t *lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, lds_dst, 16, 0, 0);
+}
+// ds_read_b64_tr_b16 as inline asm: the builtin form makes the compiler wait
+// for every DMA in flight (it cannot tell the read from the DMA's target).
+// The result is pending until lds_wait_tied() below, which takes the
+// registers as operands so no use can be scheduled before the wait.
+__device__ __forceinline__ u32x2 ds_read_tr16(const bf16_t *p) {
+  const uint32_t a = (uint32_t)(size_t)(const __attribute__((address_space(3))) bf16_t *)p;
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ void lds_wait_tied(u32x2 &a, u32x2 &b, u32x2 &c, u32x2 &d, u32x2 &e,
+                                              u32x2 &f, u32x2 &g, u32x2 &h) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h)
+               :
+               : "memory");
+}
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) { return pack_bf16x2(a, b); }
 
@@ -64,8 +95,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   static_assert(kWaves % HPW == 0, "whole row blocks per head");
   constexpr int kRowsWg = 32 * kWaves / HPW;  // query rows per workgroup
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  bf16_t *ks = lds;
-  bf16_t *vts = lds + kKElems;
 
   // Grid (head set, sequence, query block): blocks are dispatched x-fastest,
   // so every head set's longest causal rows (the last query block) go first.
@@ -111,35 +140,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   const int q_last = min(S, (qb + 1) * kRowsWg) - 1;
   const int n_kvb = q_last / kBKV + 1;
 
+  // DMA of one K/V block into stage buffer `st`: wave w moves rows
+  // 16 w .. 16 w + 15 of each tile, 4 rows (1 KiB) per instruction; the lane
+  // for LDS slot (row, s) fetches logical chunk s ^ key(row).  Rows past the
+  // sequence repeat its last row (their scores are masked).
+  auto issue_block = [&](int kb, int st) {
+    bf16_t *kst = lds + st * kStageElems;
+    bf16_t *vst = kst + kTileElems;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * wave + 4 * i + (lane >> 4);
+      const int slot = lane & 15;
+      const int src = min(kb * kBKV + row, S - 1);
+      const int base = (16 * wave + 4 * i) * kHd;  // wave-uniform LDS destination
+      dma_16b(kbase + (size_t)src * ldk + 8 * (slot ^ k_key(row)), kst + base);
+      dma_16b(vbase + (size_t)src * ldv + 8 * (slot ^ v_key(row)), vst + base);
+    }
+  };
+  issue_block(0, 0);
+
   for (int kb = 0; kb < n_kvb; ++kb) {
     const int kv0 = kb * kBKV;
-    __syncthreads();  // previous block's K / V^T reads are done
-    // K tile: 64 rows x 16 chunks of 16 B; thread covers chunks t + 256 i.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + kThreads * i;
-      const int kr = c >> 4, ch = c & 15;
-      int src = kv0 + kr;
-      src = src < S ? src : S - 1;
-      const u32x4 val = *reinterpret_cast<const u32x4 *>(kbase + (size_t)src * ldk + 8 * ch);
-      *reinterpret_cast<u32x4 *>(ks + k_off(kr, ch)) = val;
-    }
-    // V^T tile: lane = kv row, wave w + 4i picks 8 d columns; 8 transposed writes.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d0 = 8 * (wave + kWaves * i);
-      int src = kv0 + lane;
-      src = src < S ? src : S - 1;
-      const u32x4 val = *reinterpret_cast<const u32x4 *>(vbase + (size_t)src * ldv + d0);
-      const int kc = lane >> 2, kin = lane & 3;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t w32 = val[e >> 1];
-        const bf16_t hv = (e & 1) ? (bf16_t)(w32 >> 16) : (bf16_t)(w32 & 0xffffu);
-        vts[vt_off(d0 + e, kc) + kin] = hv;
-      }
-    }
+    const bf16_t *ks = lds + (kb & 1) * kStageElems;
+    const bf16_t *vs = ks + kTileElems;
+    // This block's tiles have landed (every wave waits for its own DMA, the
+    // barrier for the others'), and every wave is done with the other stage
+    // buffer (block kb - 1), which now takes block kb + 1.
+    // s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
+    // lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     __syncthreads();
+    if (kb + 1 < n_kvb) issue_block(kb + 1, (kb + 1) & 1);
 
     // S^T = K Q^T for 4 kv blocks x 2 query blocks.
     f32x4 st[4][2];
@@ -214,16 +245,29 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     // O^T += V^T P^T: d blocks jd, 32-row kv steps ks2.
 #pragma unroll
     for (int ks2 = 0; ks2 < 2; ++ks2) {
+      // Lane m of each 16-lane group reads row r0 + m/4 (r0 = 32 ks2 + 4 g, and
+      // 16 rows on for the upper half), columns 16 jd + 4 (m % 4) .. + 3;
+      // four d blocks per batch of transposing reads.
+      const int vr = 32 * ks2 + 4 * g + (l16 >> 2);
+      const int ve = 4 * (l16 & 3);  // element within the 16-column block
 #pragma unroll
-      for (int jd = 0; jd < 8; ++jd) {
-        const int dr = 16 * jd + l16;
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vts + vt_off(dr, 8 * ks2 + g));
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vts + vt_off(dr, 8 * ks2 + 4 + g));
-        const u32x4 vv = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+      for (int j0 = 0; j0 < 8; j0 += 4) {
+        u32x2 lo[4], hi[4];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          oacc[jd][nb] = mfma_bf16(vf, __builtin_bit_cast(bf16x8, pf[nb][ks2]), oacc[jd][nb]);
+        for (int t = 0; t < 4; ++t) {
+          const int col = 16 * (j0 + t) + ve;
+          lo[t] = ds_read_tr16(vs + v_off(vr, col >> 3) + (col & 7));
+          hi[t] = ds_read_tr16(vs + v_off(vr + 16, col >> 3) + (col & 7));
+        }
+        lds_wait_tied(lo[0], hi[0], lo[1], hi[1], lo[2], hi[2], lo[3], hi[3]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo[t][0], lo[t][1], hi[t][0], hi[t][1]});
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb)
+            oacc[j0 + t][nb] =
+                mfma_bf16(vf, __builtin_bit_cast(bf16x8, pf[nb][ks2]), oacc[j0 + t][nb]);
+        }
       }
     }
   }
