@@ -192,9 +192,13 @@ template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
 #ifndef PRICHS_DOWN_BM
 #define PRICHS_DOWN_BM 256
 #endif
+#ifndef PRICHS_DOWN_BN
+#define PRICHS_DOWN_BN 256
+#endif
 using Bf16 = Bf16Cfg<256, 256, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
-using Bf16Down = Bf16Cfg<PRICHS_DOWN_BM, 256, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
-static_assert(Bf16::BN == Bf16Down::BN, "both bf16 GEMMs pad packed weights to the same N tile");
+using Bf16Down = Bf16Cfg<PRICHS_DOWN_BM, PRICHS_DOWN_BN, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
+static_assert(Bf16::BN % Bf16Down::BN == 0,
+              "packed weights are padded to Bf16::BN rows, a whole number of down N tiles");
 
 // C[m, n] = sum_k A[row(m), k] * B[n, k] for the rows of each group, with
 // B = packed weights [Np, K] of group g.  The MFMA takes the weight fragment
