@@ -5,7 +5,10 @@
 // kv head h / (Hq / Hkv): scores = (q . k) * scale over j <= i, softmax over
 // the causal row, out = sum_j p_j v_j.  The T x T score matrix is never
 // materialised: each workgroup streams 64-row K/V blocks through LDS and
-// keeps an online softmax (running max m and partial sums l per query row).
+// keeps an online softmax per query row: a reference max m, raised only when
+// a block's max passes it by more than 2^8 in p (so the output is rescaled a
+// few times per row), and the row sum l = sum p, accumulated by MFMA as P
+// times a ones fragment next to O += P V.
 //
 // Layout per workgroup: 4 wave64s, each owning 32 query rows (two 16-row
 // MFMA blocks) of one query head.  With HPW heads per workgroup the 4 waves
@@ -33,6 +36,9 @@
 // lane i that column's 4 consecutive kv values.
 #include "common.hpp"
 
+#include <type_traits>
+#include <utility>
+
 namespace prichs {
 namespace {
 
@@ -48,6 +54,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kTileElems = kBKV * kHd;                   // one K or V tile [64][128]
 constexpr int kStageElems = 2 * kTileElems;              // K then V
 constexpr size_t kLdsBytes = 2 * (size_t)kStageElems * sizeof(bf16_t);  // two stages
+constexpr float kLazy = 8.0f;  // log2 headroom of the lazily raised softmax max
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -62,17 +69,28 @@ __device__ __forceinline__ int v_key(int kv) { return (2 * kv) & 15; }
 __device__ __forceinline__ int k_off(int kv, int c) { return kv * kHd + ((c ^ k_key(kv)) << 3); }
 __device__ __forceinline__ int v_off(int kv, int c) { return kv * kHd + ((c ^ v_key(kv)) << 3); }
 
-__device__ __forceinline__ void dma_16b(const bf16_t *src, bf16_t *lds_dst) {
-  __builtin_amdgcn_global_load_lds(src, lds_dst, 16, 0, 0);
+// Buffer resource over `bytes` bytes from `base` (raw: stride 0, gfx9 word 3).
+// Loads at offsets at or past `bytes` return zeros instead of reading memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+// 16 bytes per lane from buffer offset voff straight into LDS at lds_dst +
+// 16 * lane (lds_dst wave-uniform).
+__device__ __forceinline__ void dma_16b(__amdgpu_buffer_rsrc_t r, uint32_t voff, bf16_t *lds_dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void *)lds_dst, 16, voff, 0, 0, 0);
 }
 // ds_read_b64_tr_b16 as inline asm: the builtin form makes the compiler wait
 // for every DMA in flight (it cannot tell the read from the DMA's target).
-// The result is pending until lds_wait_tied() below, which takes the
-// registers as operands so no use can be scheduled before the wait.
-__device__ __forceinline__ u32x2 ds_read_tr16(const bf16_t *p) {
-  const uint32_t a = (uint32_t)(size_t)(const __attribute__((address_space(3))) bf16_t *)p;
+// OFF is the instruction's immediate byte offset.  The result is pending
+// until lds_wait_tied() below, which takes the registers as operands so no
+// use can be scheduled before the wait.
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr16(uint32_t lds_byte_addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
   u32x2 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(lds_byte_addr), "n"(OFF));
   return r;
 }
 __device__ __forceinline__ void lds_wait_tied(u32x2 &a, u32x2 &b, u32x2 &c, u32x2 &d, u32x2 &e,
@@ -85,8 +103,39 @@ __device__ __forceinline__ void lds_wait_tied(u32x2 &a, u32x2 &b, u32x2 &c, u32x
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) { return pack_bf16x2(a, b); }
 
+// Max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane groups
+// sharing a query column): v_permlane16_swap exchanges odd and even 16-lane
+// rows, v_permlane32_swap the two wave halves.
+// The maxima are IEEE 754-2019 maximum (v_maximum3_f32 on gfx950: NaN
+// propagates, so no operand needs the canonicalising pass that fmaxf's
+// maxNum semantics put before each raw MFMA result).
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max_across_groups(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t w = __float_as_uint(x);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+template <bool B> using bool_c = std::integral_constant<bool, B>;
+template <int I> using int_c = std::integral_constant<int, I>;
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(int_c<I>{}), ...);
+}
+// f(int_c<0>), ..., f(int_c<N - 1>): loop indices usable as template arguments.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+constexpr uint32_t kTileBytes = kTileElems * sizeof(bf16_t);
+constexpr uint32_t kStageBytes = kStageElems * sizeof(bf16_t);
+
 // q/k/v/o: row r of sequence b is row b*S + r; head h of q/o starts at column
-// h*128, kv head j of k/v at column j*128 (leading dimensions ldq/ldk/ldv/ldo).
+// h*128, kv head j of k/v at column j*128 (leading dimensions ldq/ldk/ldv/ldo;
+// 64 rows of k or v span less than 4 GiB).
 template <int HPW>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const bf16_t *__restrict__ q, int ldq, const bf16_t *__restrict__ k, int ldk,
@@ -105,7 +154,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   const int qb = n_qb - 1 - (int)blockIdx.z;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = kvh * group + (blockIdx.x - kvh * sets) * HPW + wave % HPW;
   const int g = lane >> 4;    // 0..3
   const int l16 = lane & 15;  // 0..15
@@ -133,36 +182,75 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   for (int jd = 0; jd < 8; ++jd)
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) oacc[jd][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY};  // running max (log2 units) of row q
-  float l_part[2] = {0.f, 0.f};              // this lane's share of the row sum
+  // Reference max (log2 units) of row q: p = exp2(s - m_ref).  It is only
+  // raised when a block's max exceeds it by more than kLazy, so p <= 2^kLazy
+  // and the output rows are rescaled a few times per row, not per block.
+  float m_ref[2] = {-INFINITY, -INFINITY};
+  // Row sums of P, accumulated by MFMA against a ones fragment (every element
+  // of lsum[nb] holds the sum of query row q0 + 16 nb + lane % 16).
+  f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u,
+                                                        0x3f803f80u});
 
   // kv blocks up to the last query row of the workgroup (causal).
   const int q_last = min(S, (qb + 1) * kRowsWg) - 1;
   const int n_kvb = q_last / kBKV + 1;
 
-  // DMA of one K/V block into stage buffer `st`: wave w moves rows
-  // 16 w .. 16 w + 15 of each tile, 4 rows (1 KiB) per instruction; the lane
-  // for LDS slot (row, s) fetches logical chunk s ^ key(row).  Rows past the
-  // sequence repeat its last row (their scores are masked).
-  auto issue_block = [&](int kb, int st) {
-    bf16_t *kst = lds + st * kStageElems;
+  // Loop-invariant LDS byte addresses of this lane's fragment reads within a
+  // stage; rows 16c (K) and 32 ks2 / +16 (V) on share the chunk key and
+  // become the instructions' immediate offsets, the stage a register add.
+  //   K fragment: kv row l16 (+16c), logical chunk 4kk + g.
+  //   V^T read:   kv row 4g + l16/4 (+32 ks2, +16), column 16 jd + 4 (l16 % 4).
+  uint32_t k_addr[4], v_addr[8];
+  const uint32_t lds_base =
+      (uint32_t)(size_t)(const __attribute__((address_space(3))) bf16_t *)lds;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) k_addr[kk] = 2u * (uint32_t)k_off(l16, 4 * kk + g);
+#pragma unroll
+  for (int jd = 0; jd < 8; ++jd) {
+    const int col = 16 * jd + 4 * (l16 & 3);
+    v_addr[jd] = lds_base + 2u * (uint32_t)(v_off(4 * g + (l16 >> 2), col >> 3) + (col & 7));
+  }
+  // Loop-invariant byte offsets of this lane's DMA sources within a 64-row
+  // block: wave w moves rows 16 w .. 16 w + 15 of each tile, 4 rows
+  // (1 KiB) per instruction, and the lane for LDS slot (row, s) fetches
+  // logical chunk s ^ key(row).
+  uint32_t dk[4], dv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 4 * i + g;
+    dk[i] = 2u * ((uint32_t)row * (uint32_t)ldk + 8u * (uint32_t)(l16 ^ k_key(row)));
+    dv[i] = 2u * ((uint32_t)row * (uint32_t)ldv + 8u * (uint32_t)(l16 ^ v_key(row)));
+  }
+
+  // DMA of K/V block kb into stage buffer `stage`.  The buffer resources end
+  // after the sequence's last row, so rows past it (last block only) load as
+  // zeros; their scores are masked.
+  auto issue_block = [&](int kb, int stage) {
+    bf16_t *kst = lds + stage * kStageElems;
     bf16_t *vst = kst + kTileElems;
+    const uint64_t last_row = (uint64_t)(S - 1 - kb * kBKV);
+    const uint64_t kbytes = last_row * 2 * (uint64_t)ldk + 2 * kHd;
+    const uint64_t vbytes = last_row * 2 * (uint64_t)ldv + 2 * kHd;
+    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(
+        kbase + (size_t)kb * kBKV * ldk, kbytes > 0xffffffffull ? 0xffffffffu : (uint32_t)kbytes);
+    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(
+        vbase + (size_t)kb * kBKV * ldv, vbytes > 0xffffffffull ? 0xffffffffu : (uint32_t)vbytes);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = 16 * wave + 4 * i + (lane >> 4);
-      const int slot = lane & 15;
-      const int src = min(kb * kBKV + row, S - 1);
       const int base = (16 * wave + 4 * i) * kHd;  // wave-uniform LDS destination
-      dma_16b(kbase + (size_t)src * ldk + 8 * (slot ^ k_key(row)), kst + base);
-      dma_16b(vbase + (size_t)src * ldv + 8 * (slot ^ v_key(row)), vst + base);
+      dma_16b(rk, dk[i], kst + base);
+      dma_16b(rv, dv[i], vst + base);
     }
   };
-  issue_block(0, 0);
 
-  for (int kb = 0; kb < n_kvb; ++kb) {
+  // One 64-row kv block from stage ST; MASKED applies the causal / length
+  // mask (blocks reaching past this wave's first query row or the sequence
+  // end).
+  auto run_block = [&](int kb, auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
+    const uint32_t stage_off = (uint32_t)(kb & 1) * kStageBytes;
     const int kv0 = kb * kBKV;
-    const bf16_t *ks = lds + (kb & 1) * kStageElems;
-    const bf16_t *vs = ks + kTileElems;
     // This block's tiles have landed (every wave waits for its own DMA, the
     // barrier for the others'), and every wave is done with the other stage
     // buffer (block kb - 1), which now takes block kb + 1.
@@ -178,86 +266,87 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) st[c][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const char *kbytes = reinterpret_cast<const char *>(lds) + stage_off;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       bf16x8 kf[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        kf[c] = *reinterpret_cast<const bf16x8 *>(ks + k_off(16 * c + l16, 4 * kk + g));
+        kf[c] = *reinterpret_cast<const bf16x8 *>(kbytes + 16 * kHd * 2 * c + k_addr[kk]);
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) st[c][nb] = mfma_bf16(kf[c], qf[nb][kk], st[c][nb]);
     }
 
-    // Online softmax.  st[c][nb][r] = score of (query q0 + 16nb + l16,
-    // kv kv0 + 16c + 4g + r).
+    // Online softmax on st[c][nb][r] = raw score of (query q0 + 16nb + l16,
+    // kv kv0 + 16c + 4g + r).  The block max is taken on raw scores (the
+    // scale is positive, and rounding is monotone, so max(fl(s * c)) =
+    // fl(max(s) * c)) and p = exp2(s * scale_log2 - m_ref) is one fma per score.
     u32x4 pf[2][2];  // P fragments: [nb][32-row kv step]
-    // Only blocks reaching past this wave's first query row or the sequence
-    // end need the causal / length mask (wave-uniform test).
-    const bool masked = kv0 + kBKV - 1 > q0 || kv0 + kBKV > S;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      const int qrow = q0 + 16 * nb + l16;
-      float s[16];
+      if constexpr (kMasked) {
+        // Valid iff kv <= query row and kv < S, i.e. 16c + r <= lim.
+        const int lim = min(q0 + 16 * nb + l16, S - 1) - kv0 - 4 * g;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (16 * c + r > lim) st[c][nb][r] = -INFINITY;
+      }
       float mloc = -INFINITY;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
+        mloc = vmax(vmax(vmax(mloc, st[c][nb][0]), st[c][nb][1]),
+                    vmax(st[c][nb][2], st[c][nb][3]));
+      mloc = max_across_groups(mloc);
+      const float m_blk = mloc * scale_log2;
+      // -inf + kLazy stays -inf: a row's first valid score always raises it.
+      const bool raise = m_blk > m_ref[nb] + kLazy;
+      const float m_new = raise ? m_blk : m_ref[nb];
+      const float alpha = raise ? fast_exp2(m_ref[nb] - m_new) : 1.0f;
+      m_ref[nb] = m_new;
+      float m_use = m_new;
+      // Rows with no valid score yet keep m = -inf; exp2(-inf - -inf) would
+      // be NaN.  Only a masked block can leave a row without one.
+      if constexpr (kMasked) m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float neg_m = -m_use;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kv = kv0 + 16 * c + 4 * g + r;
-          float x = st[c][nb][r] * scale_log2;
-          if (masked) x = (kv <= qrow && kv < S) ? x : -INFINITY;
-          s[4 * c + r] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_run[nb], mloc);
-      // Rows with no valid score yet keep m = -inf; exp2(-inf - -inf) would be NaN.
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run[nb] - m_use);
-      m_run[nb] = m_new;
-      float psum = 0.f;
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = fast_exp2(s[i] - m_use);
-        s[i] = p;
-        psum += p;
-      }
-      l_part[nb] = l_part[nb] * alpha + psum;
-      // Rescale the output rows only when some row's running max moved
-      // (alpha == 1 exactly otherwise, so skipping changes nothing).
-      if (__any(alpha != 1.0f)) {
+        for (int r = 0; r < 4; ++r)
+          st[c][nb][r] = fast_exp2(fmaf(st[c][nb][r], scale_log2, neg_m));
+      if (__any(raise)) {
 #pragma unroll
         for (int jd = 0; jd < 8; ++jd) oacc[jd][nb] = oacc[jd][nb] * alpha;
+        lsum[nb] = lsum[nb] * alpha;
       }
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
         // k slots 0..3: kv block 2 ks2 (rows 4g + r); slots 4..7: block 2 ks2 + 1.
-        const float *a0 = s + 4 * (2 * ks2);
-        const float *a1 = s + 4 * (2 * ks2 + 1);
+        const f32x4 a0 = st[2 * ks2][nb], a1 = st[2 * ks2 + 1][nb];
         pf[nb][ks2] = u32x4{pack_bf16(a0[0], a0[1]), pack_bf16(a0[2], a0[3]),
                             pack_bf16(a1[0], a1[1]), pack_bf16(a1[2], a1[3])};
       }
     }
 
-    // O^T += V^T P^T: d blocks jd, 32-row kv steps ks2.
-#pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
-      // Lane m of each 16-lane group reads row r0 + m/4 (r0 = 32 ks2 + 4 g, and
-      // 16 rows on for the upper half), columns 16 jd + 4 (m % 4) .. + 3;
-      // four d blocks per batch of transposing reads.
-      const int vr = 32 * ks2 + 4 * g + (l16 >> 2);
-      const int ve = 4 * (l16 & 3);  // element within the 16-column block
+    // O^T += V^T P^T: d blocks jd, 32-row kv steps ks2.  Lane m of each
+    // 16-lane group reads row 32 ks2 + 4g + m/4 (and 16 rows on for the
+    // upper half), columns 16 jd + 4 (m % 4) .. + 3; four d blocks per batch
+    // of transposing reads.
+    static_for<2>([&](auto ks2_c) {
+      constexpr int ks2 = decltype(ks2_c)::value;
+      constexpr int kLo = (int)kTileBytes + 2 * 32 * ks2 * kHd;  // rows 32 ks2 + ...
+      constexpr int kHi = kLo + 2 * 16 * kHd;                    // rows 32 ks2 + 16 + ...
 #pragma unroll
       for (int j0 = 0; j0 < 8; j0 += 4) {
         u32x2 lo[4], hi[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int col = 16 * (j0 + t) + ve;
-          lo[t] = ds_read_tr16(vs + v_off(vr, col >> 3) + (col & 7));
-          hi[t] = ds_read_tr16(vs + v_off(vr + 16, col >> 3) + (col & 7));
+          const uint32_t a = v_addr[j0 + t] + stage_off;
+          lo[t] = ds_read_tr16<kLo>(a);
+          hi[t] = ds_read_tr16<kHi>(a);
         }
         lds_wait_tied(lo[0], hi[0], lo[1], hi[1], lo[2], hi[2], lo[3], hi[3]);
 #pragma unroll
@@ -269,16 +358,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
                 mfma_bf16(vf, __builtin_bit_cast(bf16x8, pf[nb][ks2]), oacc[j0 + t][nb]);
         }
       }
-    }
-  }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        lsum[nb] = mfma_bf16(ones, __builtin_bit_cast(bf16x8, pf[nb][ks2]), lsum[nb]);
+    });
+  };
+
+  // Blocks whose kv rows all lie at or before this wave's first query row
+  // and inside the sequence run unmasked; the rest (the diagonal and the
+  // ragged tail) run masked.
+  const int n_full = min(min(q0 + 1, S) / kBKV, n_kvb);
+  issue_block(0, 0);
+  int kb = 0;
+  for (; kb < n_full; ++kb) run_block(kb, bool_c<false>{});
+  for (; kb < n_kvb; ++kb) run_block(kb, bool_c<true>{});
 
   // Normalise by the row sum and store: lane holds O[q][16 jd + 4g + r].
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    float l = l_part[nb];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    const float inv = 1.0f / fmaxf(l, 1e-30f);
+    const float inv = 1.0f / fmaxf(lsum[nb][0], 1e-30f);
     const int qrow = q0 + 16 * nb + l16;
     if (qrow < S) {
       bf16_t *orow = o + (seq0 + qrow) * ldo + (size_t)h * kHd + 4 * g;
@@ -315,9 +413,11 @@ extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k
   PRICHS_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0,
                  "attention: leading dimensions must be multiples of 8 elements");
   PRICHS_REQUIRE(batch * seq_len <= (size_t)INT32_MAX && n_heads <= 65535 && batch <= 65535 &&
-                     ldq <= (size_t)INT32_MAX && ldk <= (size_t)INT32_MAX &&
-                     ldv <= (size_t)INT32_MAX && ldo <= (size_t)INT32_MAX,
+                     ldq <= (size_t)INT32_MAX && ldo <= (size_t)INT32_MAX,
                  "attention: shape too large");
+  // The kernel addresses a 64-row K/V block with 32-bit byte offsets.
+  PRICHS_REQUIRE(ldk < ((size_t)1 << 25) && ldv < ((size_t)1 << 25),
+                 "attention: ldk / ldv must be below 2^25 elements");
   if (batch == 0 || seq_len == 0) return PRICHS_OK;
   PRICHS_REQUIRE(q && k && v && o, "attention: null pointer argument");
   const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
