@@ -223,50 +223,40 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     dv[i] = 2u * ((uint32_t)row * (uint32_t)ldv + 8u * (uint32_t)(l16 ^ v_key(row)));
   }
 
-  // DMA of K/V block kb into stage buffer `stage`.  The buffer resources end
-  // after the sequence's last row, so rows past it (last block only) load as
-  // zeros; their scores are masked.
-  auto issue_block = [&](int kb, int stage) {
-    bf16_t *kst = lds + stage * kStageElems;
-    bf16_t *vst = kst + kTileElems;
-    const uint64_t last_row = (uint64_t)(S - 1 - kb * kBKV);
-    const uint64_t kbytes = last_row * 2 * (uint64_t)ldk + 2 * kHd;
-    const uint64_t vbytes = last_row * 2 * (uint64_t)ldv + 2 * kHd;
-    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(
-        kbase + (size_t)kb * kBKV * ldk, kbytes > 0xffffffffull ? 0xffffffffu : (uint32_t)kbytes);
-    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(
-        vbase + (size_t)kb * kBKV * ldv, vbytes > 0xffffffffull ? 0xffffffffu : (uint32_t)vbytes);
+  // Block kb's K tile lives in stage buffer kb & 1 of K, its V tile in stage
+  // buffer kb & 1 of V.  K runs one block ahead of V: iteration kb computes
+  // S for block kb + 1 (MFMA) while the softmax of block kb (VALU) and then
+  // its P.V product run, so the matrix and vector pipes overlap within a wave.
+  // The buffer resources end after the sequence's last row, so rows past it
+  // (last block only) load as zeros; their scores are masked.
+  auto issue_tile = [&](int kb, const bf16_t *src, int ld, const uint32_t (&off)[4],
+                        int tile) {
+    bf16_t *dst = lds + (kb & 1) * kStageElems + tile * kTileElems;
+    const uint64_t bytes = (uint64_t)(S - 1 - kb * kBKV) * 2 * (uint64_t)ld + 2 * kHd;
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(
+        src + (size_t)kb * kBKV * ld, bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int base = (16 * wave + 4 * i) * kHd;  // wave-uniform LDS destination
-      dma_16b(rk, dk[i], kst + base);
-      dma_16b(rv, dv[i], vst + base);
-    }
+    for (int i = 0; i < 4; ++i) dma_16b(r, off[i], dst + (16 * wave + 4 * i) * kHd);
   };
-
-  // One 64-row kv block from stage ST; MASKED applies the causal / length
-  // mask (blocks reaching past this wave's first query row or the sequence
-  // end).
-  auto run_block = [&](int kb, auto masked_c) {
-    constexpr bool kMasked = decltype(masked_c)::value;
-    const uint32_t stage_off = (uint32_t)(kb & 1) * kStageBytes;
-    const int kv0 = kb * kBKV;
-    // This block's tiles have landed (every wave waits for its own DMA, the
-    // barrier for the others'), and every wave is done with the other stage
-    // buffer (block kb - 1), which now takes block kb + 1.
-    // s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
-    // lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
+  auto issue_k = [&](int kb) { issue_tile(kb, kbase, ldk, dk, 0); };
+  auto issue_v = [&](int kb) { issue_tile(kb, vbase, ldv, dv, 1); };
+  // Every wave's DMAs issued so far have landed (each wave waits for its own,
+  // the barrier for the others'), and every wave is past the reads before it.
+  // s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
+  // lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
+  auto sync_tiles = [&]() {
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     __syncthreads();
-    if (kb + 1 < n_kvb) issue_block(kb + 1, (kb + 1) & 1);
+  };
 
-    // S^T = K Q^T for 4 kv blocks x 2 query blocks.
-    f32x4 st[4][2];
+  // S^T = K Q^T of block kb: 4 kv blocks x 2 query blocks; sacc[c][nb][r] =
+  // raw score of (query q0 + 16nb + l16, kv 64 kb + 16c + 4g + r).
+  auto compute_s = [&](int kb, f32x4 (&sacc)[4][2]) {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) st[c][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const char *kbytes = reinterpret_cast<const char *>(lds) + stage_off;
+      for (int nb = 0; nb < 2; ++nb) sacc[c][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const char *kbytes = reinterpret_cast<const char *>(lds) + (uint32_t)(kb & 1) * kStageBytes;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       bf16x8 kf[4];
@@ -276,14 +266,31 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) st[c][nb] = mfma_bf16(kf[c], qf[nb][kk], st[c][nb]);
+        for (int nb = 0; nb < 2; ++nb) sacc[c][nb] = mfma_bf16(kf[c], qf[nb][kk], sacc[c][nb]);
     }
+  };
 
-    // Online softmax on st[c][nb][r] = raw score of (query q0 + 16nb + l16,
-    // kv kv0 + 16c + 4g + r).  The block max is taken on raw scores (the
-    // scale is positive, and rounding is monotone, so max(fl(s * c)) =
-    // fl(max(s) * c)) and p = exp2(s * scale_log2 - m_ref) is one fma per score.
+  // Iteration kb: S of block kb + 1 into snext (past the last block the
+  // stale tile it reads gives a result nobody uses), then the softmax and
+  // P.V of block kb from scur.  MASKED applies the causal / length mask
+  // (blocks reaching past this wave's first query row or the sequence end).
+  auto run_iter = [&](int kb, auto masked_c, f32x4 (&scur)[4][2], f32x4 (&snext)[4][2]) {
+    constexpr bool kMasked = decltype(masked_c)::value;
+    const int kv0 = kb * kBKV;
+    // K of block kb + 1 and V of block kb have landed; the buffers of K kb
+    // and V kb - 1 are free for K kb + 2 and V kb + 1.
+    sync_tiles();
+    if (kb + 2 < n_kvb) issue_k(kb + 2);
+    if (kb + 1 < n_kvb) issue_v(kb + 1);
+
+    compute_s(kb + 1, snext);
+
+    // Online softmax.  The block max is taken on raw scores (the scale is
+    // positive, and rounding is monotone, so max(fl(s * c)) = fl(max(s) * c))
+    // and p = exp2(s * scale_log2 - m_ref) is one fma per score.
     u32x4 pf[2][2];  // P fragments: [nb][32-row kv step]
+    float alpha[2];
+    bool raise[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       if constexpr (kMasked) {
@@ -293,19 +300,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
         for (int c = 0; c < 4; ++c)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (16 * c + r > lim) st[c][nb][r] = -INFINITY;
+            if (16 * c + r > lim) scur[c][nb][r] = -INFINITY;
       }
       float mloc = -INFINITY;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        mloc = vmax(vmax(vmax(mloc, st[c][nb][0]), st[c][nb][1]),
-                    vmax(st[c][nb][2], st[c][nb][3]));
+        mloc = vmax(vmax(vmax(mloc, scur[c][nb][0]), scur[c][nb][1]),
+                    vmax(scur[c][nb][2], scur[c][nb][3]));
       mloc = max_across_groups(mloc);
       const float m_blk = mloc * scale_log2;
       // -inf + kLazy stays -inf: a row's first valid score always raises it.
-      const bool raise = m_blk > m_ref[nb] + kLazy;
-      const float m_new = raise ? m_blk : m_ref[nb];
-      const float alpha = raise ? fast_exp2(m_ref[nb] - m_new) : 1.0f;
+      raise[nb] = m_blk > m_ref[nb] + kLazy;
+      const float m_new = raise[nb] ? m_blk : m_ref[nb];
+      alpha[nb] = raise[nb] ? fast_exp2(m_ref[nb] - m_new) : 1.0f;
       m_ref[nb] = m_new;
       float m_use = m_new;
       // Rows with no valid score yet keep m = -inf; exp2(-inf - -inf) would
@@ -313,21 +320,28 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
       if constexpr (kMasked) m_use = m_new == -INFINITY ? 0.f : m_new;
       const float neg_m = -m_use;
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          st[c][nb][r] = fast_exp2(fmaf(st[c][nb][r], scale_log2, neg_m));
-      if (__any(raise)) {
-#pragma unroll
-        for (int jd = 0; jd < 8; ++jd) oacc[jd][nb] = oacc[jd][nb] * alpha;
-        lsum[nb] = lsum[nb] * alpha;
-      }
-#pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
         // k slots 0..3: kv block 2 ks2 (rows 4g + r); slots 4..7: block 2 ks2 + 1.
-        const f32x4 a0 = st[2 * ks2][nb], a1 = st[2 * ks2 + 1][nb];
-        pf[nb][ks2] = u32x4{pack_bf16(a0[0], a0[1]), pack_bf16(a0[2], a0[3]),
-                            pack_bf16(a1[0], a1[1]), pack_bf16(a1[2], a1[3])};
+        float p[8];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            p[4 * h2 + r] = fast_exp2(fmaf(scur[2 * ks2 + h2][nb][r], scale_log2, neg_m));
+        pf[nb][ks2] = u32x4{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
+                            pack_bf16(p[6], p[7])};
+      }
+    }
+    // Pin the P fragments here: otherwise the compiler sinks the exp work
+    // past the branch below, out of reach of the S MFMAs it should overlap.
+    asm volatile("" ::"v"(pf[0][0]), "v"(pf[0][1]), "v"(pf[1][0]), "v"(pf[1][1]));
+    // Rescale the output rows where the reference max was raised (rare).
+    if (__any(raise[0] || raise[1])) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int jd = 0; jd < 8; ++jd) oacc[jd][nb] = oacc[jd][nb] * alpha[nb];
+        lsum[nb] = lsum[nb] * alpha[nb];
       }
     }
 
@@ -335,6 +349,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     // 16-lane group reads row 32 ks2 + 4g + m/4 (and 16 rows on for the
     // upper half), columns 16 jd + 4 (m % 4) .. + 3; four d blocks per batch
     // of transposing reads.
+    const uint32_t v_stage = (uint32_t)(kb & 1) * kStageBytes;
     static_for<2>([&](auto ks2_c) {
       constexpr int ks2 = decltype(ks2_c)::value;
       constexpr int kLo = (int)kTileBytes + 2 * 32 * ks2 * kHd;  // rows 32 ks2 + ...
@@ -344,7 +359,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
         u32x2 lo[4], hi[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const uint32_t a = v_addr[j0 + t] + stage_off;
+          const uint32_t a = v_addr[j0 + t] + v_stage;
           lo[t] = ds_read_tr16<kLo>(a);
           hi[t] = ds_read_tr16<kHi>(a);
         }
@@ -365,13 +380,36 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
   };
 
   // Blocks whose kv rows all lie at or before this wave's first query row
-  // and inside the sequence run unmasked; the rest (the diagonal and the
+  // and inside the sequence run unmasked (two per loop trip, so the score
+  // registers swap roles without copies); the rest (the diagonal and the
   // ragged tail) run masked.
   const int n_full = min(min(q0 + 1, S) / kBKV, n_kvb);
-  issue_block(0, 0);
+  f32x4 sa[4][2], sb[4][2];
+  issue_k(0);
+  sync_tiles();
+  issue_v(0);
+  if (n_kvb > 1) issue_k(1);
+  compute_s(0, sa);
   int kb = 0;
-  for (; kb < n_full; ++kb) run_block(kb, bool_c<false>{});
-  for (; kb < n_kvb; ++kb) run_block(kb, bool_c<true>{});
+  for (; kb + 2 <= n_full; kb += 2) {
+    run_iter(kb, bool_c<false>{}, sa, sb);
+    run_iter(kb + 1, bool_c<false>{}, sb, sa);
+  }
+  auto take_next = [&]() {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) sa[c][nb] = sb[c][nb];
+  };
+  if (kb < n_full) {
+    run_iter(kb, bool_c<false>{}, sa, sb);
+    take_next();
+    ++kb;
+  }
+  for (; kb < n_kvb; ++kb) {
+    run_iter(kb, bool_c<true>{}, sa, sb);
+    take_next();
+  }
 
   // Normalise by the row sum and store: lane holds O[q][16 jd + 4g + r].
 #pragma unroll

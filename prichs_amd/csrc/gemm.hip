@@ -21,9 +21,12 @@
 // 3 stages ahead of the MFMAs; each stage's MFMAs are split in two halves
 // around the workgroup barrier so the next stage's fragment reads overlap
 // MFMA work.  Workgroups are persistent and walk an XCD-aware tile order.
+// The down / dense epilogue stages the finished tile in LDS and writes whole
+// rows with 16-byte lanes.
 // f32 kernel: 128x128x16 tiles on v_mfma_f32_16x16x4_f32 (the fp32-checked
 // mode; accumulates in fp32 like the reference CPU path).
 #include <algorithm>
+#include <type_traits>
 #include <cstring>
 #include <vector>
 
@@ -37,6 +40,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Native vector types (not HIP's struct-based uint4/uint2), so values stay
 // in registers.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <bool B> using bool_c = std::integral_constant<bool, B>;
 
 constexpr int kMaxGroups = PRICHS_MAX_EXPERTS + 1;
 constexpr int kPadRowsDown = 256;    // packed down weights: rows padded to this
@@ -53,6 +58,11 @@ constexpr int kBf16KMultiple = 64;   // bf16 kernels need d and f to be multiple
 #endif
 #ifndef PRICHS_BF16_WGN
 #define PRICHS_BF16_WGN 4
+#endif
+// Down / dense epilogue through an LDS copy of the tile with 16-byte row
+// stores (1) or direct 8-byte stores from the accumulators (0).
+#ifndef PRICHS_GEMM_STAGE_C
+#define PRICHS_GEMM_STAGE_C 1
 #endif
 // M-tiles per band of the tile order.
 #ifndef PRICHS_BAND_M
@@ -179,7 +189,12 @@ template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
   static constexpr int kInstB = BN / kRowsPerInst / kWaves;
   static constexpr int kInstPerStage = kInstA + kInstB;
   static constexpr int kStageElems = (BM + BN) * BK;
-  static constexpr size_t kLdsBytes = (size_t)kStages * kStageElems * sizeof(bf16_t);
+  static constexpr size_t kRingBytes = (size_t)kStages * kStageElems * sizeof(bf16_t);
+  // Epilogue staging of a finished tile: [BM][BN + 8] bf16 (16-byte row pad)
+  // in the ring's LDS, which no wave reads any more by then.
+  static constexpr int kStgStride = BN + 8;
+  static constexpr size_t kStgBytes = (size_t)BM * kStgStride * sizeof(bf16_t);
+  static constexpr size_t kLdsBytes = kRingBytes > kStgBytes ? kRingBytes : kStgBytes;
   static_assert(WN % 32 == 0 && MI % 2 == 0, "whole gate/up blocks and two A halves per wave");
   static_assert(BN % (2 * kIl) == 0, "packed gate/up rows are padded to a multiple of BN");
   static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
@@ -215,7 +230,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
     bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
-    int G, int dense_m) {
+    int G, int dense_m, int stage_c) {
   constexpr int BM = Cf::BM, BN = Cf::BN, BK = Cf::BK, kStages = Cf::kStages;
   constexpr int WGN = Cf::WGN, WM = Cf::WM, WN = Cf::WN, MI = Cf::MI, NJ = Cf::NJ;
   constexpr int kRowsPerInst = Cf::kRowsPerInst, kInstA = Cf::kInstA, kInstB = Cf::kInstB;
@@ -228,7 +243,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
   const int n_tiles = Np / BN;
   const int m_tiles = tm.prefix[G];
@@ -286,21 +301,27 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     wait_vmcnt(0);
     lds_barrier();
 
-#define PRICHS_ISSUE_STAGE(kt_)                                                       \
-  do {                                                                               \
-    const int k0_ = (kt_) * BK;                                                      \
-    bf16_t *st_ = lds + ((kt_) & (kStages - 1)) * kStageElems;                       \
-    _Pragma("unroll") for (int i_ = 0; i_ < kInstA; ++i_)                            \
-        dma_16b(A + a_goff[i_] + k0_, st_ + (wave * kInstA + i_) * kRowsPerInst * BK); \
-    _Pragma("unroll") for (int i_ = 0; i_ < kInstB; ++i_)                            \
-        dma_16b(Bg + b_goff[i_] + (kt_) * 512, st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK); \
-  } while (0)
+    // DMA instruction `which` of stage kt_: A rows first, then B fragments.
+    auto issue_one = [&](int kt_, int which) {
+      bf16_t *st_ = lds + (kt_ & (kStages - 1)) * kStageElems;
+      if (which < kInstA) {
+        dma_16b(A + a_goff[which] + kt_ * BK, st_ + (wave * kInstA + which) * kRowsPerInst * BK);
+      } else {
+        const int i_ = which - kInstA;
+        dma_16b(Bg + b_goff[i_] + kt_ * 512,
+                st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK);
+      }
+    };
+    auto issue_stage = [&](int kt_) {
+#pragma unroll
+      for (int w = 0; w < kInstPerStage; ++w) issue_one(kt_, w);
+    };
 
     // Prologue: stages 0..3 in flight; stage 0 lands and is read.
-    PRICHS_ISSUE_STAGE(0);
-    if (KT > 1) PRICHS_ISSUE_STAGE(1);
-    if (KT > 2) PRICHS_ISSUE_STAGE(2);
-    if (KT > 3) PRICHS_ISSUE_STAGE(3);
+    issue_stage(0);
+    if (KT > 1) issue_stage(1);
+    if (KT > 2) issue_stage(2);
+    if (KT > 3) issue_stage(3);
     {
       const int ahead = min(3, KT - 1);  // stages issued after stage 0
       if (ahead == 3)
@@ -321,16 +342,18 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     for (int j = 0; j < NJ; ++j)
       wf[j] = *reinterpret_cast<const bf16x8 *>(lds + BM * BK + b_rd + j * 16 * BK);
 
-    for (int kt = 0; kt < KT; ++kt) {
+    // One K-step: MFMAs of stage kt in two halves around the barrier that
+    // hands stage kt's slot to stage kt + 4 (issued here when kDma).
+    auto step = [&](int kt, auto dma_c, auto last_c) {
+      constexpr bool kDma = decltype(dma_c)::value;    // issue stage kt + 4
+      constexpr bool kLast = decltype(last_c)::value;  // kt == KT - 1
       // First half: A fragments 0 .. MI/2-1 of stage kt.
 #pragma unroll
       for (int i = 0; i < MI / 2; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
+        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
 
-      const bool more = kt + 1 < KT;
-      if (more) {
+      if constexpr (!kLast) {
         // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
         const int ahead = min(2, KT - 2 - kt);
         if (ahead == 2)
@@ -342,7 +365,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
         lds_barrier();
         // Every wave has read stage kt (in the previous iteration), so its
         // slot takes stage kt + 4.
-        if (kt + 4 < KT) PRICHS_ISSUE_STAGE(kt + 4);
+        if constexpr (kDma) issue_stage(kt + 4);
         const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
         const bf16_t *bs = as + BM * BK;
 #pragma unroll
@@ -356,9 +379,8 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
 #pragma unroll
       for (int i = MI / 2; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
-      if (more) {
+        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
+      if constexpr (!kLast) {
         const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
 #pragma unroll
         for (int i = MI / 2; i < MI; ++i)
@@ -366,13 +388,51 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
 #pragma unroll
         for (int j = 0; j < NJ; ++j) wf[j] = wn_next[j];
       }
-    }
-#undef PRICHS_ISSUE_STAGE
+    };
+
+    // Steps that refill the ring, then the last three without loads, then the
+    // last step (no next stage).
+    int kt = 0;
+    for (; kt + 4 < KT; ++kt) step(kt, bool_c<true>{}, bool_c<false>{});
+    for (; kt + 1 < KT; ++kt) step(kt, bool_c<false>{}, bool_c<false>{});
+    step(kt, bool_c<false>{}, bool_c<true>{});
 
     // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
     //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
     const int lr = m0 + wm * WM + fr;
     const int cq = 4 * (lane >> 4);
+    if (!GATEUP && stage_c) {
+      // Staged (down / dense): each lane's 8-byte pieces go to a row-major
+      // copy of the tile in LDS, then the workgroup writes whole rows with
+      // 16-byte lanes (a wave store covers 8 full 128-byte lines instead of
+      // 32-byte pieces of 16 rows).  C is 16-byte aligned and ldc, n_store
+      // are multiples of 8.  (The gate/up epilogue writes half as many
+      // columns and gains nothing from it.)
+      constexpr int kS = Cf::kStgStride;
+      lds_barrier();  // every wave is done reading the ring
+      const int tcol = wn * WN + cq;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        bf16_t *srow = lds + (wm * WM + fr + 16 * i) * kS + tcol;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const f32x4 a = acc[i][j];
+          *reinterpret_cast<u32x2 *>(srow + 16 * j) =
+              u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+        }
+      }
+      lds_barrier();
+      constexpr int kChunksRow = BN / 8;  // 16-byte chunks per tile row
+#pragma unroll 4
+      for (int c = tid; c < BM * kChunksRow; c += Cf::kThreads) {
+        const int r = c / kChunksRow, ch = c - r * kChunksRow;
+        const int m = m0 + r, col = n0 + 8 * ch;
+        if (m < mg && col < n_store)
+          *reinterpret_cast<u32x4 *>(C + (long long)(row0 + m) * ldc + col) =
+              *reinterpret_cast<const u32x4 *>(lds + r * kS + 8 * ch);
+      }
+      continue;  // the next tile's barrier keeps the ring refill behind these reads
+    }
     if (GATEUP) {
       // Packed rows [n0 + wn*WN, +WN) are one [kIl gate | kIl up] block:
       // gate column c pairs with up column c in j + NJ/2.
@@ -821,9 +881,15 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
                    "grouped gemm: set LDS size");
     attr_set = true;
   }
+  // Staged 16-byte epilogue stores need C 16-byte aligned and whole 8-column
+  // chunks; otherwise each lane stores its 8-byte pieces directly.
+  const int stage_c = !GATEUP && PRICHS_GEMM_STAGE_C &&
+                      reinterpret_cast<uintptr_t>(Cp) % 16 == 0 && ldc % 8 == 0 &&
+                      n_store % 8 == 0;
   hipLaunchKernelGGL((bf16_gemm_kernel<Cf, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
-                     b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G, dense_m);
+                     b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G, dense_m,
+                     stage_c);
   PRICHS_LAUNCH_CHECK("grouped gemm launch");
   return PRICHS_OK;
 }
