@@ -4,7 +4,7 @@
  *
  * Reference paths below are relative to the PRICHS source tree.
  *
- * Three groups of entry points:
+ * Four groups of entry points:
  *
  *  1. Legacy launchers with the exact signatures of the reference's CUDA
  *     launchers (crates/prichs-cuda/src/kernels.cu; Rust extern block at
@@ -19,7 +19,11 @@
  *
  *  3. An engine handle that owns packed weights and workspace and runs the
  *     whole MoELayer forward (crates/prichs-model/src/moe.rs:93-225) on one
- *     stream with no host round trip and no allocation per call.
+ *     stream with no host round trip and no allocation per call (and a
+ *     PrichsBlock engine around it).
+ *
+ *  4. A reader of the reference's checkpoint files that uploads a block's
+ *     weights into those engines.
  *
  * Conventions:
  *  - Every non-legacy entry point returns PRICHS_OK (0) or a negative status.
@@ -427,6 +431,66 @@ typedef struct prichs_block_stash {
 } prichs_block_stash;
 int prichs_block_engine_stash(const prichs_block_engine *eng,
                               prichs_block_stash *out);
+
+/* ---------------------------------------------------------------------- */
+/* 5. Checkpoint ingestion: the reference's weight files                    */
+/*    (Model::save_checkpoint / load_checkpoint,                            */
+/*    crates/prichs-model/src/model.rs:1648-1736)                           */
+/* ---------------------------------------------------------------------- */
+typedef struct prichs_checkpoint prichs_checkpoint;
+
+/* Opens a weight file and indexes its parameters without reading their
+ * payloads.  PRICHS02 (little endian): "PRICHS02", step u64, loss f32,
+ * count u64, then count x (len u64, len f32) in the order of
+ * Model::get_parameter_tensors (model.rs:312-338).  A legacy "PRICHS_W"
+ * file (model.rs:1707-1729: embedding table and final norm only) opens with
+ * format 1 and no indexed parameters.  A bad magic, a header or payload
+ * running past the end of the file fails with PRICHS_ERR_INVALID_ARGUMENT.
+ * Host only (no GPU needed). */
+int prichs_checkpoint_open(const char *path, prichs_checkpoint **out);
+int prichs_checkpoint_close(prichs_checkpoint *ck);
+/* step and loss from the header, the number of indexed parameters and the
+ * format (2 = PRICHS02, 1 = PRICHS_W); any output pointer may be NULL. */
+int prichs_checkpoint_info(const prichs_checkpoint *ck, uint64_t *step, float *loss,
+                           size_t *n_params, int *format);
+/* Element count of parameter `index`. */
+int prichs_checkpoint_param_len(const prichs_checkpoint *ck, size_t index, size_t *len);
+/* Reads parameter `index` (f32, len must equal its element count) into host
+ * memory. */
+int prichs_checkpoint_read(const prichs_checkpoint *ck, size_t index, float *dst, size_t len);
+
+/* Slots of one block's parameters (model.rs:318-333); routed expert e's
+ * gate / up / down are PRICHS_CKPT_EXPERT0 + 3e + 0 / 1 / 2. */
+enum {
+  PRICHS_CKPT_INPUT_NORM = 0,
+  PRICHS_CKPT_Q_PROJ = 1,
+  PRICHS_CKPT_K_PROJ = 2,
+  PRICHS_CKPT_V_PROJ = 3,
+  PRICHS_CKPT_OUT_PROJ = 4,
+  PRICHS_CKPT_POST_ATTN_NORM = 5,
+  PRICHS_CKPT_ROUTER = 6,
+  PRICHS_CKPT_SHARED_GATE = 7,
+  PRICHS_CKPT_SHARED_UP = 8,
+  PRICHS_CKPT_SHARED_DOWN = 9,
+  PRICHS_CKPT_EXPERT0 = 10
+};
+/* Parameter index of `slot` in block `layer` of a model with E routed
+ * experts: 2 + layer * (10 + 3E) + slot (model.rs:557-562, 1083-1087);
+ * (size_t)-1 when slot >= 10 + 3E. */
+size_t prichs_checkpoint_block_param(size_t layer, size_t E, size_t slot);
+
+/* Uploads the MoE of block `layer` (router, shared expert, routed experts)
+ * into an engine created with the file's d, f, E and n_shared = 1 (the
+ * reference's layer, moe.rs:61); every length is checked against the engine
+ * first.  The aux-free router bias is not a parameter and is not in the
+ * file (moe.rs:60; model.rs:312-338): router_bias f32 [E] (host) or NULL =
+ * zeros, as a freshly built layer has (moe.rs:75).  Synchronous. */
+int prichs_moe_engine_upload_checkpoint(prichs_moe_engine *eng, const prichs_checkpoint *ck,
+                                        size_t layer, const float *router_bias);
+/* The same for a block engine: both norms, the attention projections and
+ * the MoE of block `layer`.  Synchronous. */
+int prichs_block_engine_upload_checkpoint(prichs_block_engine *eng, const prichs_checkpoint *ck,
+                                          size_t layer, const float *router_bias);
 
 #ifdef __cplusplus
 }

@@ -99,6 +99,15 @@ SIGNATURES = {
     "prichs_gemm": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _i, _vp]),
     "prichs_attention_forward": (_i, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
                                       _sz, _i, _vp]),
+    "prichs_checkpoint_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
+    "prichs_checkpoint_close": (_i, [_vp]),
+    "prichs_checkpoint_info": (_i, [_vp, C.POINTER(C.c_uint64), C.POINTER(_f), C.POINTER(_sz),
+                                    C.POINTER(_i)]),
+    "prichs_checkpoint_param_len": (_i, [_vp, _sz, C.POINTER(_sz)]),
+    "prichs_checkpoint_read": (_i, [_vp, _sz, _vp, _sz]),
+    "prichs_checkpoint_block_param": (_sz, [_sz, _sz, _sz]),
+    "prichs_moe_engine_upload_checkpoint": (_i, [_vp, _vp, _sz, _vp]),
+    "prichs_block_engine_upload_checkpoint": (_i, [_vp, _vp, _sz, _vp]),
     "prichs_block_engine_create": (_i, [_sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f,
                                         C.POINTER(_vp)]),
     "prichs_block_engine_destroy": (_i, [_vp]),

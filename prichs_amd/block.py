@@ -64,6 +64,13 @@ class BlockEngine:
             bias.ctypes.data, C.cast(pg, C.c_void_p), C.cast(pu, C.c_void_p),
             C.cast(pd, C.c_void_p)))
 
+    def upload_checkpoint(self, ckpt, layer: int, router_bias=None):
+        """prichs_block_engine_upload_checkpoint: norms, attention and MoE of
+        block `layer` of an open ``checkpoint.Checkpoint``."""
+        b = None if router_bias is None else np.ascontiguousarray(router_bias, dtype=np.float32)
+        L.check(self.lib.prichs_block_engine_upload_checkpoint(
+            self.handle, ckpt.handle, layer, None if b is None else b.ctypes.data))
+
     def forward(self, x: torch.Tensor, batch: int, seq_len: int, pos_offset: int = 0,
                 concept_bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
                 out_dtype=None, stream=None) -> torch.Tensor:

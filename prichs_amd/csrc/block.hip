@@ -194,6 +194,42 @@ extern "C" int prichs_block_engine_upload(prichs_block_engine *eng, const float 
   return PRICHS_OK;
 }
 
+// Block `layer` of a reference weight file (model.rs:312-338): norms and
+// attention projections (slots 0..5), then the MoE; every length is checked
+// before anything is uploaded.
+extern "C" int prichs_block_engine_upload_checkpoint(prichs_block_engine *eng,
+                                                     const prichs_checkpoint *ck, size_t layer,
+                                                     const float *router_bias) {
+  PRICHS_REQUIRE(eng != nullptr && ck != nullptr, "block_upload_checkpoint: null pointer argument");
+  if (eng->S != 1)
+    return fail(PRICHS_ERR_UNSUPPORTED,
+                "block_upload_checkpoint: a checkpoint layer has one shared expert (moe.rs:61), "
+                "the engine has n_shared=%zu",
+                eng->S);
+  const size_t d = eng->d, kvw = eng->Hkv * eng->hd, E = eng->E;
+  struct Part {
+    int slot;
+    size_t len;
+    const char *what;
+  };
+  const Part parts[6] = {{PRICHS_CKPT_INPUT_NORM, d, "input_norm"},
+                         {PRICHS_CKPT_Q_PROJ, d * d, "attention.q_proj"},
+                         {PRICHS_CKPT_K_PROJ, d * kvw, "attention.k_proj"},
+                         {PRICHS_CKPT_V_PROJ, d * kvw, "attention.v_proj"},
+                         {PRICHS_CKPT_OUT_PROJ, d * d, "attention.out_proj"},
+                         {PRICHS_CKPT_POST_ATTN_NORM, d, "post_attn_norm"}};
+  std::vector<float> v[6];
+  for (int i = 0; i < 6; ++i)
+    if (int rc = checkpoint_read_vec(ck, prichs_checkpoint_block_param(layer, E, parts[i].slot),
+                                     parts[i].len, v[i], parts[i].what, layer))
+      return rc;
+  CheckpointMoe w;
+  if (int rc = checkpoint_moe_weights(ck, layer, d, eng->f, E, w)) return rc;
+  return prichs_block_engine_upload(eng, v[0].data(), v[5].data(), v[1].data(), v[2].data(),
+                                    v[3].data(), v[4].data(), w.router.data(), router_bias,
+                                    w.pg.data(), w.pu.data(), w.pd.data());
+}
+
 extern "C" int prichs_block_engine_forward(prichs_block_engine *eng, const void *x, size_t batch,
                                            size_t seq_len, size_t pos_offset,
                                            const float *concept_bias, size_t n_concept, void *out,

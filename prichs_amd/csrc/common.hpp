@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "prichs_hip.h"
 
@@ -119,5 +120,20 @@ int grouped_gate_up_swiglu_rows(const void *x, const int32_t *row_token, const i
 int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t max_rows,
                       size_t max_group_rows, const void *w_packed, size_t d, size_t f, int dtype,
                       void *y, void *stream);
+
+// Checkpoint reading shared by the engines' upload-from-checkpoint entry
+// points: parameter `index` must hold exactly `want` floats (`what` and
+// `layer` name it in the error message).
+int checkpoint_read_vec(const prichs_checkpoint *ck, size_t index, size_t want,
+                        std::vector<float> &out, const char *what, size_t layer);
+// One MoE layer's weights in the reference layouts, shared expert first,
+// with the pointer arrays prichs_moe_engine_upload takes.
+struct CheckpointMoe {
+  std::vector<float> router;
+  std::vector<std::vector<float>> gate, up, down;
+  std::vector<const float *> pg, pu, pd;
+};
+int checkpoint_moe_weights(const prichs_checkpoint *ck, size_t layer, size_t d, size_t f,
+                           size_t E, CheckpointMoe &w);
 
 }  // namespace prichs

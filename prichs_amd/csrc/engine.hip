@@ -227,6 +227,24 @@ extern "C" int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_r
   return PRICHS_OK;
 }
 
+// Block `layer` of a reference weight file (model.rs:312-338) into the
+// engine: lengths are checked against the engine's d, f, E before anything
+// is uploaded.
+extern "C" int prichs_moe_engine_upload_checkpoint(prichs_moe_engine *eng,
+                                                   const prichs_checkpoint *ck, size_t layer,
+                                                   const float *router_bias) {
+  PRICHS_REQUIRE(eng != nullptr && ck != nullptr, "engine_upload_checkpoint: null pointer argument");
+  if (eng->S != 1)
+    return fail(PRICHS_ERR_UNSUPPORTED,
+                "engine_upload_checkpoint: a checkpoint layer has one shared expert (moe.rs:61), "
+                "the engine has n_shared=%zu",
+                eng->S);
+  CheckpointMoe w;
+  if (int rc = checkpoint_moe_weights(ck, layer, eng->d, eng->f, eng->E, w)) return rc;
+  return prichs_moe_engine_upload(eng, w.router.data(), router_bias, w.pg.data(), w.pu.data(),
+                                  w.pd.data());
+}
+
 extern "C" int prichs_moe_engine_set_router_bias(prichs_moe_engine *eng, const float *router_bias) {
   PRICHS_REQUIRE(eng && router_bias, "engine_set_router_bias: null pointer argument");
   DeviceGuard g(eng->device);

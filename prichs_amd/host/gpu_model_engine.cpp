@@ -74,6 +74,38 @@ std::vector<float> d2h_rows(const float *src, size_t ld, size_t rows, size_t col
 
 }  // namespace
 
+Checkpoint load_checkpoint(const std::string &path) {
+  prichs_checkpoint *ck = nullptr;
+  lib_ok(prichs_checkpoint_open(path.c_str(), &ck), "load_checkpoint");
+  Checkpoint out;
+  try {
+    size_t n = 0;
+    int format = 0;
+    lib_ok(prichs_checkpoint_info(ck, &out.step, &out.loss, &n, &format), "load_checkpoint");
+    if (format != 2)
+      bail(fmt("load_checkpoint: %s is a legacy PRICHS_W file (embedding and final norm only)",
+               path.c_str()));
+    out.params.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+      size_t len = 0;
+      lib_ok(prichs_checkpoint_param_len(ck, i, &len), "load_checkpoint");
+      out.params[i].resize(len);
+      lib_ok(prichs_checkpoint_read(ck, i, out.params[i].data(), len), "load_checkpoint");
+    }
+  } catch (...) {
+    prichs_checkpoint_close(ck);
+    throw;
+  }
+  prichs_checkpoint_close(ck);
+  return out;
+}
+
+size_t block_param_index(size_t layer, size_t E, size_t slot) {
+  const size_t i = prichs_checkpoint_block_param(layer, E, slot);
+  if (i == (size_t)-1) bail(fmt("block_param_index: slot %zu outside a block of %zu", slot, 10 + 3 * E));
+  return i;
+}
+
 struct GpuModelEngine::PackedGemm {
   size_t Kp = 0, Np = 0;
   float *dev = nullptr;

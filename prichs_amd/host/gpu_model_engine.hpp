@@ -59,6 +59,20 @@ using SharedOut = std::tuple<std::vector<float>, std::vector<float>, std::vector
 using ExpertOut = std::tuple<std::vector<float>, std::vector<float>, std::vector<float>,
                              std::vector<float>, std::vector<float>>;
 
+// Model::load_checkpoint (crates/prichs-model/src/model.rs:1673-1736) for a
+// PRICHS02 file, through the library's reader: every parameter in the order
+// of get_parameter_tensors (model.rs:312-338), ready for upload_weights.
+// A legacy PRICHS_W file has no indexed parameters and is refused here.
+struct Checkpoint {
+  uint64_t step = 0;
+  float loss = 0.f;
+  std::vector<std::vector<float>> params;
+};
+Checkpoint load_checkpoint(const std::string &path);
+// Index of `slot` of block `layer` with E routed experts: 2 + layer * (10 + 3E)
+// + slot (model.rs:557-562, 1083-1087).  Throws for a slot past the block.
+size_t block_param_index(size_t layer, size_t E, size_t slot);
+
 class GpuModelEngine {
  public:
   // engine.rs:363: one (rows, cols, apply_weight_decay) triple per parameter.

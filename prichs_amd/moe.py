@@ -84,6 +84,13 @@ class MoEEngine:
                                                   C.cast(pg, C.c_void_p), C.cast(pu, C.c_void_p),
                                                   C.cast(pd, C.c_void_p)))
 
+    def upload_checkpoint(self, ckpt, layer: int, router_bias=None):
+        """prichs_moe_engine_upload_checkpoint: the MoE of block `layer` of an
+        open ``checkpoint.Checkpoint`` (the router bias is not in the file)."""
+        b = None if router_bias is None else np.ascontiguousarray(router_bias, dtype=np.float32)
+        L.check(self.lib.prichs_moe_engine_upload_checkpoint(
+            self.handle, ckpt.handle, layer, None if b is None else b.ctypes.data))
+
     def set_router_bias(self, bias):
         b = np.ascontiguousarray(bias, dtype=np.float32)
         L.check(self.lib.prichs_moe_engine_set_router_bias(self.handle, b.ctypes.data))

@@ -4,8 +4,10 @@
 // calls, same tolerances, plus checks of the values the reference only prints.
 //
 // usage: test_gpu_model_engine                run the GPU tests
-//        test_gpu_model_engine --no-gpu       only check that engine creation
-//                                              without a device fails cleanly
+//        test_gpu_model_engine --no-gpu       only the host tests: the
+//                                              checkpoint loader, and engine
+//                                              creation without a device
+//                                              failing cleanly
 //        test_gpu_model_engine FIXTURE_DIR    also the config-1 parity test on
 //                                              oracle fixtures (see
 //                                              tests/test_host_cpp.py)
@@ -21,6 +23,8 @@
 #include <sstream>
 #include <string>
 #include <vector>
+
+#include <unistd.h>
 
 #include "gpu_model_engine.hpp"
 #include "prichs_hip.h"
@@ -299,7 +303,57 @@ void test_moe_config1_parity(const std::string &dir) {
 
 }  // namespace
 
+// Model::save_checkpoint's layout (model.rs:1648-1670), written here byte by
+// byte; load_checkpoint must return every tensor bit for bit, and the block
+// index map must name the right tensors.
+void test_load_checkpoint() {
+  const std::string path = "/tmp/prichs_cpp_ckpt_" + std::to_string(::getpid()) + ".prichs";
+  const size_t E = 2, d = 3;
+  std::vector<std::vector<float>> params;
+  params.push_back({0.5f, -1.f});  // wte
+  params.push_back({1.f, 1.f, 1.f});  // final_norm
+  for (size_t s = 0; s < 10 + 3 * E; ++s) {  // one block, tensor s filled with 100 + s
+    std::vector<float> t(d + s);
+    for (size_t i = 0; i < t.size(); ++i) t[i] = 100.f + (float)s + 0.25f * (float)i;
+    params.push_back(t);
+  }
+  params[3][1] = -0.0f;
+  {
+    std::FILE *fh = std::fopen(path.c_str(), "wb");
+    CHECK(fh != nullptr, "cannot create %s", path.c_str());
+    const uint64_t step = 77, n = params.size();
+    const float loss = 3.5f;
+    std::fwrite("PRICHS02", 1, 8, fh);
+    std::fwrite(&step, 8, 1, fh);
+    std::fwrite(&loss, 4, 1, fh);
+    std::fwrite(&n, 8, 1, fh);
+    for (const auto &t : params) {
+      const uint64_t len = t.size();
+      std::fwrite(&len, 8, 1, fh);
+      std::fwrite(t.data(), 4, t.size(), fh);
+    }
+    std::fclose(fh);
+  }
+  const prichs_host::Checkpoint ck = prichs_host::load_checkpoint(path);
+  CHECK(ck.step == 77 && ck.loss == 3.5f, "header step %llu loss %g", (unsigned long long)ck.step,
+        ck.loss);
+  CHECK(ck.params.size() == params.size(), "%zu parameters", ck.params.size());
+  for (size_t i = 0; i < params.size(); ++i)
+    CHECK(ck.params[i].size() == params[i].size() &&
+              std::memcmp(ck.params[i].data(), params[i].data(), 4 * params[i].size()) == 0,
+          "parameter %zu differs", i);
+  // Block 0: router is slot 6, expert 1's down the last slot.
+  CHECK(ck.params[prichs_host::block_param_index(0, E, 6)][0] == 106.f, "router slot");
+  CHECK(ck.params[prichs_host::block_param_index(0, E, 10 + 3 * 1 + 2)][0] == 115.f, "expert slot");
+  expect_error([&] { prichs_host::block_param_index(0, E, 10 + 3 * E); }, "outside a block");
+  // A truncated copy (wte's payload cut) fails at open with the reader's message.
+  CHECK(::truncate(path.c_str(), 40) == 0, "truncate");
+  expect_error([&] { prichs_host::load_checkpoint(path); }, "load_checkpoint");
+  std::remove(path.c_str());
+}
+
 int main(int argc, char **argv) {
+  run("load_checkpoint", test_load_checkpoint);
   if (argc > 1 && std::strcmp(argv[1], "--no-gpu") == 0) {
     // Without a device the constructor's first allocation fails: an Error, not a crash.
     run("engine_creation_without_device_raises", [] {

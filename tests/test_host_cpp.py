@@ -3,7 +3,9 @@ through its C++ test program (tests/cpp/test_gpu_model_engine.cpp), which is
 written like the reference's engine tests (crates/prichs-cuda/src/engine.rs:
 2876-3182).
 
-The GPU test feeds it config-1 fixtures from the oracle: router logits within
+Both runs check prichs_host::load_checkpoint on a PRICHS02 file the program
+writes byte by byte (model.rs:1648-1670).  The GPU test feeds it config-1
+fixtures from the oracle: router logits within
 1e-5, the stage-by-stage MoE (shared, then each expert on the oracle's token
 lists, then finalize) and the fused device path within 1e-4 (f32).
 """
