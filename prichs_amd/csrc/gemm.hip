@@ -183,7 +183,7 @@ template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int MI = WM / 16, NJ = WN / 16;
-  static constexpr int kIl = WN / 2;         // gate/up interleave: packed blocks [kIl gate | kIl up]
+  static constexpr int kIl = 32;             // gate/up interleave: packed blocks [kIl gate | kIl up]
   static constexpr int kRowsPerInst = 16;    // one wave instruction fills 1 KiB = 16 rows of 64 B
   static constexpr int kInstA = BM / kRowsPerInst / kWaves;
   static constexpr int kInstB = BN / kRowsPerInst / kWaves;
@@ -195,7 +195,8 @@ template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
   static constexpr int kStgStride = BN + 8;
   static constexpr size_t kStgBytes = (size_t)BM * kStgStride * sizeof(bf16_t);
   static constexpr size_t kLdsBytes = kRingBytes > kStgBytes ? kRingBytes : kStgBytes;
-  static_assert(WN % 32 == 0 && MI % 2 == 0, "whole gate/up blocks and two A halves per wave");
+  static_assert(WN % (2 * kIl) == 0 && MI % 2 == 0,
+                "whole [gate | up] blocks and two A halves per wave");
   static_assert(BN % (2 * kIl) == 0, "packed gate/up rows are padded to a multiple of BN");
   static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
                 "the DMA instructions of one stage cover the A and B tiles exactly");
@@ -335,23 +336,40 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     }
     lds_barrier();
 
-    bf16x8 af[MI], wf[NJ], wn_next[NJ];
+    // Fragments of one stage in registers: B (w) and the second half of A
+    // (ahi).  Two sets swap roles from step to step; the first half of A
+    // (alo) is consumed before the barrier, so one set of it is enough.
+    struct Frags {
+      bf16x8 w[NJ], ahi[MI / 2];
+    };
+    Frags fa, fb;
+    bf16x8 alo[MI / 2];
+    auto read_stage = [&](int st, Frags &f) {
+      const bf16_t *as = lds + (st & (kStages - 1)) * kStageElems;
+      const bf16_t *bs = as + BM * BK;
 #pragma unroll
-    for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(lds + a_rd + i * 16 * BK);
+      for (int jj = 0; jj < NJ; ++jj)
+        f.w[jj] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + jj * 16 * BK);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      wf[j] = *reinterpret_cast<const bf16x8 *>(lds + BM * BK + b_rd + j * 16 * BK);
+      for (int ii = 0; ii < MI / 2; ++ii)
+        alo[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + ii * 16 * BK);
+#pragma unroll
+      for (int ii = 0; ii < MI / 2; ++ii)
+        f.ahi[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + (MI / 2 + ii) * 16 * BK);
+    };
+    read_stage(0, fa);
 
-    // One K-step: MFMAs of stage kt in two halves around the barrier that
-    // hands stage kt's slot to stage kt + 4 (issued here when kDma).
-    auto step = [&](int kt, auto dma_c, auto last_c) {
+    // One K-step: MFMAs of stage kt (fragments in cur) in two halves around
+    // the barrier that hands stage kt's slot to stage kt + 4 (issued here
+    // when kDma).  All of stage kt+1's fragments are read right after the
+    // barrier, into nxt and alo, so they land during the second half.
+    auto step = [&](int kt, auto dma_c, auto last_c, Frags &cur, Frags &nxt) {
       constexpr bool kDma = decltype(dma_c)::value;    // issue stage kt + 4
       constexpr bool kLast = decltype(last_c)::value;  // kt == KT - 1
-      // First half: A fragments 0 .. MI/2-1 of stage kt.
 #pragma unroll
       for (int i = 0; i < MI / 2; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
+        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(cur.w[j], alo[i], acc[i][j]);
 
       if constexpr (!kLast) {
         // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
@@ -363,39 +381,44 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
         else
           wait_vmcnt(0);
         lds_barrier();
-        // Every wave has read stage kt (in the previous iteration), so its
-        // slot takes stage kt + 4.
+        // Every wave has read stage kt (in the previous step), so its slot
+        // takes stage kt + 4.
         if constexpr (kDma) issue_stage(kt + 4);
-        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
-        const bf16_t *bs = as + BM * BK;
+        read_stage(kt + 1, nxt);
+        // Keep these reads ahead of the second half's MFMAs (the scheduler
+        // would otherwise sink them next to their use in the next step).
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = 0; i < MI / 2; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-          wn_next[j] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + j * 16 * BK);
-#pragma unroll
-        for (int i = 0; i < MI / 2; ++i)
-          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
-      }
-      // Second half: A fragments MI/2 .. MI-1 of stage kt.
-#pragma unroll
-      for (int i = MI / 2; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(wf[j], af[i], acc[i][j]);
-      if constexpr (!kLast) {
-        const bf16_t *as = lds + ((kt + 1) & (kStages - 1)) * kStageElems;
-#pragma unroll
-        for (int i = MI / 2; i < MI; ++i)
-          af[i] = *reinterpret_cast<const bf16x8 *>(as + a_rd + i * 16 * BK);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) wf[j] = wn_next[j];
-      }
+          acc[MI / 2 + i][j] = mfma_bf16(cur.w[j], cur.ahi[i], acc[MI / 2 + i][j]);
     };
 
-    // Steps that refill the ring, then the last three without loads, then the
-    // last step (no next stage).
+    // Steps that refill the ring (in pairs, the fragment sets swapping
+    // roles), then the ones without loads, then the last step (no next
+    // stage).  An odd leftover step moves its next set into fa once.
     int kt = 0;
-    for (; kt + 4 < KT; ++kt) step(kt, bool_c<true>{}, bool_c<false>{});
-    for (; kt + 1 < KT; ++kt) step(kt, bool_c<false>{}, bool_c<false>{});
-    step(kt, bool_c<false>{}, bool_c<true>{});
+    for (; kt + 5 < KT; kt += 2) {
+      step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
+      step(kt + 1, bool_c<true>{}, bool_c<false>{}, fb, fa);
+    }
+    if (kt + 4 < KT) {
+      step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
+      fa = fb;
+      ++kt;
+    }
+    for (; kt + 2 < KT; kt += 2) {
+      step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
+      step(kt + 1, bool_c<false>{}, bool_c<false>{}, fb, fa);
+    }
+    if (kt + 1 < KT) {
+      step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
+      fa = fb;
+      ++kt;
+    }
+    step(kt, bool_c<false>{}, bool_c<true>{}, fa, fb);
 
     // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
     //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
@@ -434,22 +457,25 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
       continue;  // the next tile's barrier keeps the ring refill behind these reads
     }
     if (GATEUP) {
-      // Packed rows [n0 + wn*WN, +WN) are one [kIl gate | kIl up] block:
-      // gate column c pairs with up column c in j + NJ/2.
-      const int cbase = (n0 + wn * WN) / 2 + cq;
+      // Packed rows [n0 + wn*WN, +WN) are WN / (2 kIl) [kIl gate | kIl up]
+      // blocks: in block q, gate column c (16-column piece jj) pairs with up
+      // column c, kIl / 16 pieces on.
+      constexpr int kPieces = Cf::kIl / 16;  // 16-column pieces per gate (or up) half
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = lr + 16 * i;
         if (m < mg) {
           bf16_t *crow = C + (long long)(row0 + m) * ldc;
 #pragma unroll
-          for (int j = 0; j < NJ / 2; ++j) {
-            const int col = cbase + 16 * j;
+          for (int jg = 0; jg < NJ / 2; ++jg) {
+            const int q = jg / kPieces, jj = jg - q * kPieces;
+            const int j = 2 * kPieces * q + jj;  // gate piece; up piece is j + kPieces
+            const int col = (n0 + wn * WN + 2 * Cf::kIl * q) / 2 + 16 * jj + cq;
             if (col < n_store) {
               float h[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + NJ / 2][r];
+                h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + kPieces][r];
               *reinterpret_cast<u32x2 *>(crow + col) =
                   u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
             }
