@@ -58,6 +58,10 @@ def lib():
                                       C.c_void_p, C.c_void_p, C.c_void_p, _f32p,
                                       _f32p, _i32p, _f32p, _i32p, _i32p, _f32p, _i32p]
         L.orc_moe_forward.restype = C.c_int
+        L.orc_moe_backward.argtypes = [_f32p, _f32p, sz, sz, sz, sz, sz, _f32p, _f32p, C.c_void_p,
+                                       sz, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, _f32p,
+                                       _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_moe_backward.restype = C.c_int
         L.orc_precompute_rope_cache.argtypes = [sz, sz, C.c_float, _f32p, _f32p]
         L.orc_precompute_rope_cache.restype = None
         L.orc_rope_forward_in_place.argtypes = [_f32p, _f32p, _f32p, sz, sz, sz, sz]
@@ -202,6 +206,41 @@ def moe_forward(inp, concept_bias=None):
     return dict(out=out, logits=logits, sel=sel, gw=gw, offsets=offsets,
                 row_token=row_token[: T * k], row_weight=row_weight[: T * k],
                 token_row=token_row[: T * k])
+
+
+def moe_backward(inp, d_out, dx_weighting=2, concept_bias=None, grads=None):
+    """The MoE backward (engine.rs:2242-2789 driven as model.rs:1474-1561; router VJP
+    backward.rs:269-287) on a synth.MoEInputs with n_shared = 1.  Returns
+    dict(d_x, d_router, d_gate, d_up, d_down); gradients start from `grads` (a dict
+    of the same keys, copied) or zeros, and are accumulated into."""
+    T, d, f, E, k, S = inp.T, inp.d, inp.f, inp.E, inp.k, inp.n_shared
+    if S != 1:
+        raise ValueError("the reference backward has one shared expert")
+    x = _c(inp.x)
+    dout = _c(d_out)
+    gates, ups, downs = ([_c(a) for a in inp.gate], [_c(a) for a in inp.up],
+                         [_c(a) for a in inp.down])
+    G = S + E
+    if grads is None:
+        grads = dict(d_router=np.zeros((d, E), np.float32),
+                     d_gate=[np.zeros((d, f), np.float32) for _ in range(G)],
+                     d_up=[np.zeros((d, f), np.float32) for _ in range(G)],
+                     d_down=[np.zeros((f, d), np.float32) for _ in range(G)])
+    out = dict(d_x=np.empty((T, d), np.float32), d_router=_c(grads["d_router"]).copy(),
+               d_gate=[_c(a).copy() for a in grads["d_gate"]],
+               d_up=[_c(a).copy() for a in grads["d_up"]],
+               d_down=[_c(a).copy() for a in grads["d_down"]])
+    arr = C.c_void_p * G
+    ptrs = lambda lst: C.cast(arr(*[a.ctypes.data for a in lst]), C.c_void_p)  # noqa: E731
+    cb = None if concept_bias is None else _c(concept_bias)
+    rc = lib().orc_moe_backward(x, dout, T, d, f, E, k, _c(inp.w_router), _c(inp.router_bias),
+                                None if cb is None else cb.ctypes.data,
+                                0 if cb is None else cb.size, ptrs(gates), ptrs(ups), ptrs(downs),
+                                dx_weighting, out["d_x"], out["d_router"], ptrs(out["d_gate"]),
+                                ptrs(out["d_up"]), ptrs(out["d_down"]))
+    if rc != 0:
+        raise RuntimeError("oracle moe_backward failed")
+    return out
 
 
 def precompute_rope_cache(max_seq_len, head_dim, theta):

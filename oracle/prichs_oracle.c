@@ -39,6 +39,11 @@
  *                            row 0 attends only to itself.
  *   orc_block_forward        float64 re-assembly of the block from the pinned
  *                            pieces (RMSNorm, attention, MoE, residuals).
+ *   orc_moe_backward         central finite differences of the pinned
+ *                            forward (<d_out, out>) on small shapes for d_x
+ *                            and every weight gradient (dx_weighting = 1);
+ *                            dx_weighting = 2 differs only in the routed d_x
+ *                            term, by exactly the extra gate-weight factor.
  *   orc_update_aux_free_bias float64 closed form; the update sums to ~0 over
  *                            the experts (sum of counts = k * T); balanced
  *                            routing leaves the bias unchanged; T = 0 no-op.
@@ -370,6 +375,246 @@ ORC_API int orc_moe_forward(const float *x, size_t T, size_t d, size_t f,
   if (!offsets) free(off);
   if (!row_token) free(rt);
   if (!row_weight) free(rw);
+  return rc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MoE backward: the reference's training step (model.rs:1474-1561) through   */
+/* GpuModelEngine::gpu_moe_backward_expert / _shared / _router                */
+/* (engine.rs:2242-2789), its kernels (kernels.cu:459-480, 926-991) and the   */
+/* router VJP moe_router_unbiased_backward (backward.rs:269-287), in f32 with */
+/* one fixed order of additions.                                              */
+/*                                                                            */
+/* Forward (recomputed here): routing and binning as orc_moe_forward; per     */
+/* expert G = X Wg, U = X Wu, A = silu(G) U, Y = A Wd (Y before the gate      */
+/* weight, the reference's stashed expert output).                            */
+/* Per routed expert e ascending, rows r of its bin (token t, weight w):      */
+/*   dY[r] = w * d_out[t]                          (gather_weighted)          */
+/*   s[r]  = sum_c Y[r][c] * d_out[t][c]           (router_dot)               */
+/*   dWd  += A^T dY;  dA = dY Wd^T                                            */
+/*   sig = 1/(1+exp(-g)); dU = dA*silu(g); dG = (dA*u)*(sig*(1+g*(1-sig)))    */
+/*   dWg  += X^T dG;  dWu += X^T dU                                           */
+/*   d_x[t] += w * (dG Wg^T + dU Wu^T)[r]          (scatter_add_grad)         */
+/* The reference's gather already scaled dY by w, so its scatter applies the  */
+/* gate weight to the routed input gradient a second time; dx_weighting = 2   */
+/* restates that, dx_weighting = 1 drops the second factor (the chain rule).  */
+/* Weight gradients do not depend on it.                                      */
+/* Shared expert (weight 1, all T rows): the same with dY = d_out; its two    */
+/* input-gradient GEMMs accumulate into d_x one after the other.              */
+/* Router, per token: d_w[j] = s of its j-th selected expert;                 */
+/*   ws = sum_j g_j d_w[j];  d_logits[t][e_j] = g_j * (d_w[j] - ws), else 0;  */
+/*   dW_router += x^T d_logits;  d_x += d_logits W_router^T.                  */
+/* d_x is overwritten (the reference clears it first); every dW is added to   */
+/* (cuBLAS beta = 1): dW += (sum over rows ascending of the products).        */
+/* Order of the d_x additions: routed experts ascending (rows ascending),     */
+/* shared gate then up products, router.                                      */
+/* ------------------------------------------------------------------------ */
+
+/* dw[i][j] += sum_r a[r][i] * b[r][j] (r ascending), a [m, p], b [m, q]. */
+static void orc_accum_at_b(const float *a, const float *b, float *dw, size_t m, size_t p,
+                           size_t q) {
+  long long i;
+#pragma omp parallel for schedule(static)
+  for (i = 0; i < (long long)p; ++i) {
+    float *acc = (float *)calloc(q, sizeof(float));
+    if (!acc) continue;
+    for (size_t r = 0; r < m; ++r) {
+      const float av = a[r * p + (size_t)i];
+      const float *brow = b + r * q;
+      for (size_t j = 0; j < q; ++j) {
+        float prod = av * brow[j];
+        acc[j] = acc[j] + prod;
+      }
+    }
+    float *drow = dw + (size_t)i * q;
+    for (size_t j = 0; j < q; ++j) drow[j] = drow[j] + acc[j];
+    free(acc);
+  }
+}
+
+/* out[r][i] = sum_j a[r][j] * w[i][j] (j ascending): a [m, q], w [p, q]. */
+static void orc_matmul_bt(const float *a, const float *w, float *out, size_t m, size_t q,
+                          size_t p) {
+  long long r;
+#pragma omp parallel for schedule(static)
+  for (r = 0; r < (long long)m; ++r) {
+    const float *arow = a + (size_t)r * q;
+    for (size_t i = 0; i < p; ++i) {
+      const float *wrow = w + i * q;
+      float acc = 0.0f;
+      for (size_t j = 0; j < q; ++j) {
+        float prod = arow[j] * wrow[j];
+        acc = acc + prod;
+      }
+      out[(size_t)r * p + i] = acc;
+    }
+  }
+}
+
+/* SwiGLU backward, kernels.cu:459-480 in f32 with expf. */
+static void orc_swiglu_backward(const float *da, const float *g, const float *u, float *dg,
+                                float *du, size_t n) {
+  long long i;
+#pragma omp parallel for schedule(static)
+  for (i = 0; i < (long long)n; ++i) {
+    const float gv = g[i], uv = u[i], dy = da[i];
+    const float sig = 1.0f / (1.0f + expf(-gv));
+    const float silu = gv * sig;
+    const float dsilu = sig * (1.0f + gv * (1.0f - sig));
+    du[i] = dy * silu;
+    const float dyu = dy * uv;
+    dg[i] = dyu * dsilu;
+  }
+}
+
+/* One expert's backward on m rows of xin (rows of d_out given by dy, already
+ * weighted).  Accumulates dWg, dWu, dWd; writes dX [m, d] = dG Wg^T + dU Wu^T
+ * as two products (dxg, dxu) and Y [m, d] when y != NULL. */
+static int orc_expert_backward(const float *xin, const float *dy, size_t m, size_t d, size_t f,
+                               const float *wg, const float *wu, const float *wd, float *dwg,
+                               float *dwu, float *dwd, float *dxg, float *dxu, float *y) {
+  float *g = (float *)malloc(sizeof(float) * m * f);
+  float *u = (float *)malloc(sizeof(float) * m * f);
+  float *a = (float *)malloc(sizeof(float) * m * f);
+  float *da = (float *)malloc(sizeof(float) * m * f);
+  int rc = (g && u && a && da) ? 0 : -1;
+  if (rc == 0) {
+    orc_matmul_2d(xin, wg, g, m, d, f);
+    orc_matmul_2d(xin, wu, u, m, d, f);
+    orc_swiglu(g, u, a, m * f);
+    if (y) orc_matmul_2d(a, wd, y, m, f, d);
+    orc_accum_at_b(a, dy, dwd, m, f, d);    /* dWd [f, d] += A^T dY */
+    orc_matmul_bt(dy, wd, da, m, d, f);     /* dA = dY Wd^T          */
+    orc_swiglu_backward(da, g, u, g, u, m * f); /* g <- dG, u <- dU   */
+    orc_accum_at_b(xin, g, dwg, m, d, f);   /* dWg [d, f] += X^T dG  */
+    orc_accum_at_b(xin, u, dwu, m, d, f);   /* dWu [d, f] += X^T dU  */
+    orc_matmul_bt(g, wg, dxg, m, f, d);     /* dG Wg^T               */
+    orc_matmul_bt(u, wu, dxu, m, f, d);     /* dU Wu^T               */
+  }
+  free(g);
+  free(u);
+  free(a);
+  free(da);
+  return rc;
+}
+
+ORC_API int orc_moe_backward(const float *x, const float *d_out, size_t T, size_t d, size_t f,
+                             size_t E, size_t k, const float *w_router,
+                             const float *router_bias, const float *concept_bias,
+                             size_t n_concept, const float *const *w_gate,
+                             const float *const *w_up, const float *const *w_down,
+                             int dx_weighting, float *d_x, float *dw_router,
+                             float *const *dw_gate, float *const *dw_up,
+                             float *const *dw_down) {
+  if (E == 0 || E > ORC_MAX_E || k == 0 || k > E || (dx_weighting != 1 && dx_weighting != 2))
+    return -1;
+  int rc = 0;
+  float *lg = (float *)malloc(sizeof(float) * (T * E + 1));
+  int32_t *sl = (int32_t *)malloc(sizeof(int32_t) * (T * k + 1));
+  float *gw = (float *)malloc(sizeof(float) * (T * k + 1));
+  int32_t *off = (int32_t *)malloc(sizeof(int32_t) * (E + 1));
+  int32_t *rt = (int32_t *)malloc(sizeof(int32_t) * (T * k + 1));
+  float *rw = (float *)malloc(sizeof(float) * (T * k + 1));
+  int32_t *tr = (int32_t *)malloc(sizeof(int32_t) * (T * k + 1));
+  float *scal = (float *)calloc(T * E + 1, sizeof(float)); /* s per (token, expert) */
+  float *dlog = (float *)calloc(T * E + 1, sizeof(float));
+  if (!lg || !sl || !gw || !off || !rt || !rw || !tr || !scal || !dlog) rc = -1;
+  if (rc == 0)
+    rc = orc_route(x, w_router, router_bias, concept_bias, n_concept, T, d, E, k, lg, sl, gw);
+  if (rc == 0) orc_bin_tokens(sl, gw, T, E, k, off, rt, rw, tr);
+  if (rc == 0) memset(d_x, 0, sizeof(float) * T * d);
+
+  /* Routed experts, ascending. */
+  for (size_t e = 0; rc == 0 && e < E; ++e) {
+    const size_t m = (size_t)(off[e + 1] - off[e]);
+    if (m == 0) continue;
+    float *xb = (float *)malloc(sizeof(float) * m * d);
+    float *dy = (float *)malloc(sizeof(float) * m * d);
+    float *y = (float *)malloc(sizeof(float) * m * d);
+    float *dxg = (float *)malloc(sizeof(float) * m * d);
+    float *dxu = (float *)malloc(sizeof(float) * m * d);
+    if (!xb || !dy || !y || !dxg || !dxu) rc = -1;
+    for (size_t i = 0; rc == 0 && i < m; ++i) {
+      const size_t r = (size_t)off[e] + i, t = (size_t)rt[r];
+      memcpy(xb + i * d, x + t * d, sizeof(float) * d);
+      for (size_t c = 0; c < d; ++c) dy[i * d + c] = rw[r] * d_out[t * d + c];
+    }
+    if (rc == 0)
+      rc = orc_expert_backward(xb, dy, m, d, f, w_gate[1 + e], w_up[1 + e], w_down[1 + e],
+                               dw_gate[1 + e], dw_up[1 + e], dw_down[1 + e], dxg, dxu, y);
+    for (size_t i = 0; rc == 0 && i < m; ++i) {
+      const size_t r = (size_t)off[e] + i, t = (size_t)rt[r];
+      float s = 0.0f;
+      for (size_t c = 0; c < d; ++c) {
+        float prod = y[i * d + c] * d_out[t * d + c];
+        s = s + prod;
+      }
+      scal[t * E + e] = s;
+      const float wx = dx_weighting == 2 ? rw[r] : 1.0f;
+      for (size_t c = 0; c < d; ++c) {
+        const float sum = dxg[i * d + c] + dxu[i * d + c];
+        const float val = wx * sum;
+        d_x[t * d + c] = d_x[t * d + c] + val;
+      }
+    }
+    free(xb);
+    free(dy);
+    free(y);
+    free(dxg);
+    free(dxu);
+  }
+
+  /* Shared expert on all rows, weight 1. */
+  if (rc == 0) {
+    float *dxg = (float *)malloc(sizeof(float) * T * d);
+    float *dxu = (float *)malloc(sizeof(float) * T * d);
+    if (!dxg || !dxu) rc = -1;
+    if (rc == 0)
+      rc = orc_expert_backward(x, d_out, T, d, f, w_gate[0], w_up[0], w_down[0], dw_gate[0],
+                               dw_up[0], dw_down[0], dxg, dxu, NULL);
+    if (rc == 0) {
+      for (size_t i = 0; i < T * d; ++i) d_x[i] = d_x[i] + dxg[i];
+      for (size_t i = 0; i < T * d; ++i) d_x[i] = d_x[i] + dxu[i];
+    }
+    free(dxg);
+    free(dxu);
+  }
+
+  /* Router VJP per token, then its two products. */
+  if (rc == 0) {
+    for (size_t t = 0; t < T; ++t) {
+      const int32_t *idx = sl + t * k;
+      const float *g = gw + t * k;
+      float ws = 0.0f;
+      for (size_t j = 0; j < k; ++j) {
+        float prod = g[j] * scal[t * E + (size_t)idx[j]];
+        ws = ws + prod;
+      }
+      for (size_t j = 0; j < k; ++j) {
+        const float diff = scal[t * E + (size_t)idx[j]] - ws;
+        dlog[t * E + (size_t)idx[j]] = g[j] * diff;
+      }
+    }
+    orc_accum_at_b(x, dlog, dw_router, T, d, E); /* dW_router [d, E] += x^T d_logits */
+    float *dxr = (float *)malloc(sizeof(float) * T * d);
+    if (!dxr) {
+      rc = -1;
+    } else {
+      /* d_logits W_router^T: W_router is [d, E], so row c of it is w_router[c][:]. */
+      orc_matmul_bt(dlog, w_router, dxr, T, E, d);
+      for (size_t i = 0; i < T * d; ++i) d_x[i] = d_x[i] + dxr[i];
+      free(dxr);
+    }
+  }
+  free(lg);
+  free(sl);
+  free(gw);
+  free(off);
+  free(rt);
+  free(rw);
+  free(tr);
+  free(scal);
+  free(dlog);
   return rc;
 }
 
