@@ -377,6 +377,51 @@ int prichs_moe_engine_set_timing(prichs_moe_engine *eng, int max_forwards);
 int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
                                int *n_forwards);
 
+/* ---- Backward: the training step's MoE gradients ------------------------
+ * Replaces GpuModelEngine::gpu_moe_init_backward, gpu_moe_backward_expert
+ * (per routed expert), gpu_moe_backward_shared and gpu_moe_backward_router
+ * (crates/prichs-cuda/src/engine.rs:2242-2789) as Model::train_step drives
+ * them (crates/prichs-model/src/model.rs:1474-1561), with the router VJP
+ * moe_router_unbiased_backward (crates/prichs-core/src/backward.rs:269-287)
+ * on device.  One call covers every expert; nothing is summed with atomics,
+ * so the result is deterministic. */
+
+/* Allocates the backward's workspace (about (T*(k+1)) * (2f + 2d) elements
+ * of the engine dtype for max_tokens T) and makes the next uploads also pack
+ * the transposed weights the input-gradient products need.  Call after
+ * create and before upload / upload_checkpoint.  Needs n_shared = 1 (the
+ * reference's layer, moe.rs:61).  Synchronous. */
+int prichs_moe_engine_enable_backward(prichs_moe_engine *eng);
+
+/* Caller-owned f32 gradient buffers (device) in the reference's layouts,
+ * added to like dev_grads (cuBLAS beta = 1): d_router [d, E]; per expert
+ * slot s (0 = shared expert, 1 + e = routed expert e) d_gate + s*slot_stride
+ * and d_up + s*slot_stride [d, f], d_down + s*slot_stride [f, d].  With the
+ * reference's parameter order (model.rs:312-338) d_up = d_gate + d*f,
+ * d_down = d_gate + 2*d*f and slot_stride = 3*d*f.  16-byte aligned. */
+typedef struct prichs_moe_grads {
+  float *d_router;
+  float *d_gate;
+  float *d_up;
+  float *d_down;
+  size_t slot_stride;
+} prichs_moe_grads;
+
+/* Gradients of the layer output's loss given d_out = dL/d(moe output)
+ * [T, d] (engine dtype, device), for the batch of the forward that ran just
+ * before on this engine (same x [T, d], device): writes d_x [T, d] (d_x_dtype,
+ * device; the reference's d_normed2) and adds the weight gradients to
+ * *grads.  dx_weighting = 2 reproduces the reference, whose routed input
+ * gradient carries the gate weight twice (its gather scales dY by w,
+ * kernels.cu:926-944, and its scatter scales dX again, kernels.cu:971-991);
+ * dx_weighting = 1 is the chain rule.  The weight gradients do not depend on
+ * it.  The forward's stash is consumed (act is overwritten): one backward
+ * per forward.  x, d_out and d_x are 16-byte aligned. */
+int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
+                               const void *d_out, size_t T, void *d_x,
+                               int d_x_dtype, const prichs_moe_grads *grads,
+                               int dx_weighting, void *stream);
+
 /* ---------------------------------------------------------------------- */
 /* 4. PrichsBlock engine (crates/prichs-model/src/block.rs:50-68): RMSNorm,  */
 /*    GQA attention with RoPE, residual, RMSNorm, the MoE engine, residual. */

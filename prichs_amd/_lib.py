@@ -36,6 +36,18 @@ class PrichsError(RuntimeError):
         self.message = message
 
 
+class MoEGrads(C.Structure):
+    """prichs_moe_grads: device f32 gradient buffers (reference layouts)."""
+
+    _fields_ = [
+        ("d_router", C.c_void_p),
+        ("d_gate", C.c_void_p),
+        ("d_up", C.c_void_p),
+        ("d_down", C.c_void_p),
+        ("slot_stride", C.c_size_t),
+    ]
+
+
 class MoEStash(C.Structure):
     _fields_ = [
         ("T", C.c_size_t),
@@ -125,6 +137,8 @@ SIGNATURES = {
     "prichs_moe_engine_stash": (_i, [_vp, C.POINTER(MoEStash)]),
     "prichs_moe_engine_set_timing": (_i, [_vp, _i]),
     "prichs_moe_engine_stage_ms": (_i, [_vp, C.POINTER(_f), C.POINTER(_i)]),
+    "prichs_moe_engine_enable_backward": (_i, [_vp]),
+    "prichs_moe_engine_backward": (_i, [_vp, _vp, _vp, _sz, _vp, _i, C.POINTER(MoEGrads), _i, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,785 @@
+// backward.hip -- kernels of the MoE layer backward (the engine drives them).
+//
+// Replaces the reference's training-step MoE backward: GpuModelEngine::
+// gpu_moe_init_backward / gpu_moe_backward_expert / gpu_moe_backward_shared /
+// gpu_moe_backward_router (crates/prichs-cuda/src/engine.rs:2242-2789), their
+// kernels (crates/prichs-cuda/src/kernels.cu:455-480 SwiGLU backward, 926-991
+// gather / router dot / scatter) and the host router VJP
+// moe_router_unbiased_backward (crates/prichs-core/src/backward.rs:269-287),
+// as driven by Model::train_step (crates/prichs-model/src/model.rs:1474-1561).
+// The reference runs one expert at a time with host round trips; here every
+// stage covers all groups (routed experts and the shared expert) in one launch
+// over the engine's row space, and nothing is summed with atomics, so the
+// result is deterministic.
+//
+// Kernels here:
+//   rows_kernel       dY[r] = w_r * d_out[t_r], xg[r] = x[t_r], and the router
+//                     scalar s_r = <y[r], d_out[t_r]> (routed rows);
+//   swiglu_bwd_kernel dG, dU from dA and the gate/up pre-activations, in place
+//                     in the packed [gate 32 | up 32] column order;
+//   wgrad kernels     dW[group] += A_g^T B_g over each group's rows (MFMA);
+//   combine_kernel    the router VJP and the input gradient of each token;
+//   router wgrad      dW_router += x^T d_logits (two deterministic passes).
+#include "common.hpp"
+
+namespace prichs {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kIl = 32;  // packed gate/up interleave of both dtypes: [32 gate | 32 up] blocks
+
+// ------------------------------------------------------ 8-element vectors --
+template <typename T> struct V8;
+template <> struct V8<float> {
+  __device__ static void load(const float *p, float v[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p);
+    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  __device__ static void store(float *p, const float v[8]) {
+    *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4 *>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  __device__ static void copy(const float *src, float *dst) {
+    *reinterpret_cast<float4 *>(dst) = *reinterpret_cast<const float4 *>(src);
+    *reinterpret_cast<float4 *>(dst + 4) = *reinterpret_cast<const float4 *>(src + 4);
+  }
+};
+template <> struct V8<bf16_t> {
+  __device__ static void load(const bf16_t *p, float v[8]) {
+    const u32x4 u = *reinterpret_cast<const u32x4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __builtin_bit_cast(float, u[i] << 16);
+      v[2 * i + 1] = __builtin_bit_cast(float, u[i] & 0xffff0000u);
+    }
+  }
+  __device__ static void store(bf16_t *p, const float v[8]) {
+    u32x4 u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4 *>(p) = u;
+  }
+  __device__ static void copy(const bf16_t *src, bf16_t *dst) {
+    *reinterpret_cast<u32x4 *>(dst) = *reinterpret_cast<const u32x4 *>(src);
+  }
+};
+
+// Sum over the 64 lanes of a wave in a fixed butterfly order (every lane
+// ends with the same bits).
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+  return v;
+}
+
+// ------------------------------------------------------------- rows pass --
+// One wave per row r of the row space (routed rows, then the shared rows):
+// dY[r] = w_r * d_out[t] (kernels.cu:926-944; w = 1 on shared rows, whose
+// gradient the reference feeds straight to the shared expert, engine.rs:
+// 2513-2703), xg[r] = x[t] (the gathered expert input of the weight
+// gradients), and for routed rows s_r = sum_c y[r][c] * d_out[t][c]
+// (kernels.cu:946-969: the dot of the unweighted expert output with the
+// layer's output gradient).
+template <typename T>
+__global__ __launch_bounds__(256) void rows_kernel(const T *__restrict__ x,
+                                                   const T *__restrict__ d_out,
+                                                   const T *__restrict__ y,
+                                                   const int32_t *__restrict__ row_token,
+                                                   const float *__restrict__ row_weight, int rows,
+                                                   int routed_rows, int d, T *__restrict__ dy,
+                                                   T *__restrict__ xg, float *__restrict__ scal) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int t = row_token[r];
+  const bool routed = r < routed_rows;
+  const float w = routed ? row_weight[r] : 1.0f;
+  const T *go = d_out + (size_t)t * d;
+  float s = 0.f;
+  for (int c = lane * 8; c < d; c += 64 * 8) {
+    float g[8], o[8];
+    V8<T>::load(go + c, g);
+    V8<T>::copy(x + (size_t)t * d + c, xg + (size_t)r * d + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = w * g[j];
+    V8<T>::store(dy + (size_t)r * d + c, o);
+    if (routed) {
+      float yv[8];
+      V8<T>::load(y + (size_t)r * d + c, yv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = yv[j] * g[j];
+        s = s + p;
+      }
+    }
+  }
+  if (routed) {
+    s = wave_sum(s);
+    if (lane == 0) scal[r] = s;
+  }
+}
+
+// ------------------------------------------------------ SwiGLU backward --
+// kernels.cu:459-480 per element: sig = 1 / (1 + exp(-g)), silu = g sig,
+// dsilu = sig (1 + g (1 - sig)), dU = dA silu, dG = (dA u) dsilu.  gu holds
+// the packed pre-activations [rows, np] (block q: gate columns 32q.. at
+// 64q.., up at 64q + 32..) and receives dG, dU in the same places; padding
+// blocks (columns >= f) are cleared so the dX product sees zeros there.
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(T *__restrict__ gu,
+                                                         const T *__restrict__ da, int rows,
+                                                         int f, int np) {
+#pragma clang fp contract(off)
+  const int per_row = np / (2 * kIl) * (kIl / 8);  // 8-column chunks of gate per row
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (long long)rows * per_row) return;
+  const int r = (int)(gid / per_row);
+  const int rem = (int)(gid - (long long)r * per_row);
+  const int q = rem / (kIl / 8), h = rem - q * (kIl / 8);
+  const int col = q * kIl + h * 8;
+  T *gp = gu + (size_t)r * np + (size_t)q * 2 * kIl + h * 8;
+  T *up = gp + kIl;
+  float g[8], u[8], a[8], dg[8], du[8];
+  if (col >= f) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dg[j] = 0.f;
+    V8<T>::store(gp, dg);
+    V8<T>::store(up, dg);
+    return;
+  }
+  V8<T>::load(gp, g);
+  V8<T>::load(up, u);
+  V8<T>::load(da + (size_t)r * f + col, a);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sig = 1.0f / (1.0f + expf(-g[j]));
+    const float silu = g[j] * sig;
+    const float dsilu = sig * (1.0f + g[j] * (1.0f - sig));
+    du[j] = a[j] * silu;
+    const float au = a[j] * u[j];
+    dg[j] = au * dsilu;
+  }
+  V8<T>::store(gp, dg);
+  V8<T>::store(up, du);
+}
+
+// ------------------------------------------------------ weight gradients --
+// dW[group g] += A_g^T B_g, A_g = rows [offsets[g], offsets[g+1]) of A [*, lda]
+// (columns 0..P), B_g the same rows of B [*, ldb] (columns 0..Q): the
+// reference's cuBLAS sgemm calls with beta = 1 (engine.rs:2345-2362 for
+// dW_down, 2417-2451 for dW_gate / dW_up; 2619-2654 for the shared expert).  Groups are the engine's: routed
+// experts 0..E-1 then the shared expert (group E); group g's matrices sit at
+// slot g + 1 (routed) or 0 (shared) of the caller's gradients, slot s at
+// out + s * slot_stride.
+//   plain:  out0[i][j] (ldo) for i < P, j < Q.
+//   gateup: B's columns are packed gate/up (block q = [32 gate | 32 up]); column
+//           p goes to out0 (gate) or out1 (up) at column 32 (p / 64) + p % 32
+//           when that is < f.
+// Workgroups: one per (group, 128 x 128 output tile), the shared group's
+// tiles first (it has the most rows).
+namespace wg {
+constexpr int BP = 128, BQ = 128;
+constexpr int kThreads = 256;
+}  // namespace wg
+
+__device__ __forceinline__ int slot_of(int g, int E) { return g < E ? g + 1 : 0; }
+
+// Output element pointer of (i, j) or nullptr when outside the gradient.
+template <bool GATEUP>
+__device__ __forceinline__ float *wgrad_dst(float *out0, float *out1, int ldo, long long base,
+                                            int i, int j, int P, int Q, int f) {
+  if (i >= P || j >= Q) return nullptr;
+  if (!GATEUP) return out0 + base + (long long)i * ldo + j;
+  const int q = j / (2 * kIl), w = j - q * 2 * kIl;
+  const int col = q * kIl + (w & (kIl - 1));
+  if (col >= f) return nullptr;
+  return (w < kIl ? out0 : out1) + base + (long long)i * ldo + col;
+}
+
+// --- bf16: v_mfma_f32_16x16x32_bf16, both operands read transposed from LDS.
+// A K-step is 32 rows.  Both 32 x 128 operand tiles go from global memory to
+// LDS with buffer_load ... lds (16 bytes per lane, no VGPR round trip) into a
+// ring of 4 stages, 3 ahead of the MFMAs; rows past the group's end load as
+// zeros (their offsets are past the buffer's range).  Tile rows are 256
+// bytes of 16 chunks, chunk c of row R stored at c ^ ((2R) & 15).
+// ds_read_b64_tr_b16 hands lane i of a 16-lane group column i of the 4 rows x
+// 16 columns the group addresses, so lane 16g + m, reading row 4g + m/4
+// (and 16 rows on) at columns 4(m % 4).., receives the 8 K values {4g..4g+3,
+// 16+4g..16+4g+3} of one column: the same K slots for both operands.
+namespace wgb {
+constexpr int BK = 32;
+constexpr uint32_t kTileBytes = BK * 128 * 2;        // 8 KiB: one operand tile
+constexpr uint32_t kStageBytes = 2 * kTileBytes;     // A tile then B tile
+constexpr int kStages = 4;
+constexpr size_t kLdsBytes = (size_t)kStages * kStageBytes;  // 64 KiB
+constexpr uint32_t kHiOff = 16 * 256;                // rows 16.. of a tile
+constexpr uint32_t kOutOfRange = 0x80000000u;        // buffer offset that loads zeros
+}  // namespace wgb
+
+__device__ __forceinline__ int wg_key(int row) { return (2 * row) & 15; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wg_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ void wg_dma(__amdgpu_buffer_rsrc_t r, uint32_t voff, bf16_t *lds_dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void *)lds_dst, 16, voff, 0, 0, 0);
+}
+// ds_read_b64_tr_b16 with an immediate byte offset, as inline asm (the
+// builtin makes the compiler wait for every LDS DMA in flight); the result is
+// pending until wg_wait_tied() takes it.
+template <int OFF>
+__device__ __forceinline__ u32x2 wg_read_tr(uint32_t lds_byte_addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(lds_byte_addr), "n"(OFF));
+  return r;
+}
+__device__ __forceinline__ void wg_wait_tied(u32x2 (&a)[4], u32x2 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]),
+                 "+v"(b[2]), "+v"(b[3])
+               :
+               : "memory");
+}
+// s_waitcnt with only vmcnt constrained (gfx9 encoding, vmcnt < 16 here).
+#define PRICHS_WG_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8))
+
+template <bool GATEUP>
+__global__ __launch_bounds__(wg::kThreads) void wgrad_bf16_kernel(
+    const bf16_t *__restrict__ A, int lda, uint32_t a_bytes, const bf16_t *__restrict__ B,
+    int ldb, uint32_t b_bytes, const int32_t *__restrict__ offsets, int G, int E, int P, int Q,
+    int tiles_q, int tiles, float *out0, float *out1, int ldo, long long slot_stride, int f) {
+  using namespace wgb;
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  const int gi = blockIdx.x / tiles;
+  const int tile = blockIdx.x - gi * tiles;
+  const int g = (gi + G - 1) % G;  // the last group (shared) first
+  const int row_lo = offsets[g];
+  const int mg = offsets[g + 1] - row_lo;
+  if (mg <= 0) return;
+  const int tp = tile / tiles_q;
+  const int i0 = tp * wg::BP, j0 = (tile - tp * tiles_q) * wg::BQ;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int wp = wave >> 1, wq = wave & 1;
+  const __amdgpu_buffer_rsrc_t ra = wg_rsrc(A, a_bytes), rb = wg_rsrc(B, b_bytes);
+
+  // DMA: wave w's instruction i fills tile rows 8w + 4i .. + 3; lane l lands
+  // in row 8w + 4i + l/16, physical chunk l % 16, holding logical chunk
+  // (l % 16) ^ key(row).
+  uint32_t a_col[2], b_col[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int R = 8 * wave + 4 * i + (lane >> 4);
+    const int lc = (lane & 15) ^ wg_key(R);
+    a_col[i] = 2u * (uint32_t)(i0 + lc * 8);
+    b_col[i] = 2u * (uint32_t)(j0 + lc * 8);
+  }
+  auto issue = [&](int kt) {
+    bf16_t *sa = lds + (size_t)(kt & (kStages - 1)) * (kStageBytes / 2);
+    bf16_t *sb = sa + kTileBytes / 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rr = kt * BK + 8 * wave + 4 * i + (lane >> 4);
+      const bool ok = rr < mg;
+      const uint32_t row = (uint32_t)(row_lo + rr);
+      wg_dma(ra, ok ? row * (uint32_t)lda * 2u + a_col[i] : kOutOfRange,
+             sa + (8 * wave + 4 * i) * 128);
+      wg_dma(rb, ok ? row * (uint32_t)ldb * 2u + b_col[i] : kOutOfRange,
+             sb + (8 * wave + 4 * i) * 128);
+    }
+  };
+
+  // Transposing reads: lane 16g + m reads row 4g + m/4 at column
+  // 16 blk + 4 (m % 4) of the wave's 64 columns.
+  const uint32_t lds_base = (uint32_t)(size_t)(const __attribute__((address_space(3))) bf16_t *)lds;
+  uint32_t a_rd[4], b_rd[4];
+  {
+    const int g4 = lane >> 4, m = lane & 15;
+    const int R = 4 * g4 + (m >> 2);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int ca = wp * 64 + blk * 16 + 4 * (m & 3);
+      const int cb = wq * 64 + blk * 16 + 4 * (m & 3);
+      a_rd[blk] = lds_base + (uint32_t)(R * 256 + (((ca >> 3) ^ wg_key(R)) << 4) + (ca & 7) * 2);
+      b_rd[blk] = lds_base + kTileBytes +
+                  (uint32_t)(R * 256 + (((cb >> 3) ^ wg_key(R)) << 4) + (cb & 7) * 2);
+    }
+  }
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = (mg + BK - 1) / BK;
+  issue(0);
+  if (KT > 1) issue(1);
+  if (KT > 2) issue(2);
+  for (int kt = 0; kt < KT; ++kt) {
+    // This wave's DMAs of stage kt have landed once at most the later
+    // stages' (4 instructions each) are outstanding.
+    const int ahead = min(2, KT - 1 - kt);
+    if (ahead == 2)
+      PRICHS_WG_VMCNT(8);
+    else if (ahead == 1)
+      PRICHS_WG_VMCNT(4);
+    else
+      PRICHS_WG_VMCNT(0);
+    // Every wave's DMAs of stage kt landed, and every wave is done reading
+    // stage kt - 1, whose slot the next issue refills.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + 3 < KT) issue(kt + 3);
+    const uint32_t st = (uint32_t)(kt & (kStages - 1)) * kStageBytes;
+    u32x2 alo[4], ahi[4], blo[4], bhi[4];
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      alo[blk] = wg_read_tr<0>(a_rd[blk] + st);
+      ahi[blk] = wg_read_tr<(int)kHiOff>(a_rd[blk] + st);
+      blo[blk] = wg_read_tr<0>(b_rd[blk] + st);
+      bhi[blk] = wg_read_tr<(int)kHiOff>(b_rd[blk] + st);
+    }
+    wg_wait_tied(alo, ahi);
+    wg_wait_tied(blo, bhi);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const bf16x8 bf = __builtin_bit_cast(bf16x8, u32x4{blo[jb][0], blo[jb][1], bhi[jb][0], bhi[jb][1]});
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const bf16x8 af =
+            __builtin_bit_cast(bf16x8, u32x4{alo[ib][0], alo[ib][1], ahi[ib][0], ahi[ib][1]});
+        acc[jb][ib] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, af, acc[jb][ib], 0, 0, 0);
+      }
+    }
+  }
+
+  // acc[jb][ib] lane l holds out[i = 16 ib + l % 16][j = 16 jb + 4 (l / 16) + r].
+  const long long base = (long long)slot_of(g, E) * slot_stride;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      const int i = i0 + wp * 64 + ib * 16 + (lane & 15);
+      const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
+      float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
+      if (dst) {
+        float4 v = *reinterpret_cast<float4 *>(dst);
+        v.x = v.x + acc[jb][ib][0];
+        v.y = v.y + acc[jb][ib][1];
+        v.z = v.z + acc[jb][ib][2];
+        v.w = v.w + acc[jb][ib][3];
+        *reinterpret_cast<float4 *>(dst) = v;
+      }
+    }
+}
+
+// --- f32 (the fp32-checked mode): v_mfma_f32_16x16x4_f32, K-steps of 16 rows
+// through padded LDS tiles, register double buffering.  Lane l's operand is
+// element (row l / 16, column l % 16) of a 4-row slice: a plain LDS read.
+namespace wgf {
+constexpr int BK = 16;
+constexpr int kLd = 128 + 4;  // padded LDS row (floats)
+constexpr int kTile = BK * kLd;
+constexpr size_t kLdsBytes = 2 * 2 * (size_t)kTile * sizeof(float);  // A and B, two buffers
+}  // namespace wgf
+
+template <bool GATEUP>
+__global__ __launch_bounds__(wg::kThreads) void wgrad_f32_kernel(
+    const float *__restrict__ A, int lda, const float *__restrict__ B, int ldb,
+    const int32_t *__restrict__ offsets, int G, int E, int P, int Q, int tiles_q, int tiles,
+    float *out0, float *out1, int ldo, long long slot_stride, int f) {
+  using namespace wgf;
+  extern __shared__ __attribute__((aligned(16))) float ldsw[];
+  const int gi = blockIdx.x / tiles;
+  const int tile = blockIdx.x - gi * tiles;
+  const int g = (gi + G - 1) % G;
+  const int row_lo = offsets[g];
+  const int mg = offsets[g + 1] - row_lo;
+  if (mg <= 0) return;
+  const int tp = tile / tiles_q;
+  const int i0 = tp * wg::BP, j0 = (tile - tp * tiles_q) * wg::BQ;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wp = wave >> 1, wq = wave & 1;
+  // Loads: thread t moves rows t / 32 and t / 32 + 8, columns 4 (t % 32)...
+  const int lrow = tid >> 5, lc4 = (tid & 31) * 4;
+  // Columns past P / Q read column 0 instead (their outputs are dropped).
+  const int ca = i0 + lc4 < P ? i0 + lc4 : 0;
+  const int cb = j0 + lc4 < Q ? j0 + lc4 : 0;
+  // Rows past the group's end read its last row and are replaced by zeros
+  // (a select of values: a select of pointers would read zeros from memory).
+  float4 ra0, ra1, rb0, rb1;
+#define PRICHS_WGF_SEL(v, ok) \
+  v = make_float4((ok) ? v.x : 0.f, (ok) ? v.y : 0.f, (ok) ? v.z : 0.f, (ok) ? v.w : 0.f)
+#define PRICHS_WGF_LOAD(k0)                                                         \
+  do {                                                                              \
+    const int r0_ = (k0) + lrow, r1_ = (k0) + lrow + 8;                             \
+    const size_t s0_ = (size_t)(row_lo + min(r0_, mg - 1));                         \
+    const size_t s1_ = (size_t)(row_lo + min(r1_, mg - 1));                         \
+    ra0 = *reinterpret_cast<const float4 *>(A + s0_ * lda + ca);                    \
+    rb0 = *reinterpret_cast<const float4 *>(B + s0_ * ldb + cb);                    \
+    ra1 = *reinterpret_cast<const float4 *>(A + s1_ * lda + ca);                    \
+    rb1 = *reinterpret_cast<const float4 *>(B + s1_ * ldb + cb);                    \
+    PRICHS_WGF_SEL(ra0, r0_ < mg);                                                  \
+    PRICHS_WGF_SEL(rb0, r0_ < mg);                                                  \
+    PRICHS_WGF_SEL(ra1, r1_ < mg);                                                  \
+    PRICHS_WGF_SEL(rb1, r1_ < mg);                                                  \
+  } while (0)
+#define PRICHS_WGF_STORE(buf)                                             \
+  do {                                                                    \
+    float *as_ = ldsw + (buf) * 2 * kTile;                                \
+    float *bs_ = as_ + kTile;                                             \
+    *reinterpret_cast<float4 *>(as_ + lrow * kLd + lc4) = ra0;            \
+    *reinterpret_cast<float4 *>(bs_ + lrow * kLd + lc4) = rb0;            \
+    *reinterpret_cast<float4 *>(as_ + (lrow + 8) * kLd + lc4) = ra1;      \
+    *reinterpret_cast<float4 *>(bs_ + (lrow + 8) * kLd + lc4) = rb1;      \
+  } while (0)
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int KT = (mg + BK - 1) / BK;
+  PRICHS_WGF_LOAD(0);
+  PRICHS_WGF_STORE(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const bool more = kt + 1 < KT;
+    if (more) PRICHS_WGF_LOAD((kt + 1) * BK);
+    const float *as = ldsw + (kt & 1) * 2 * kTile;
+    const float *bs = as + kTile;
+#pragma unroll
+    for (int ks = 0; ks < BK / 4; ++ks) {
+      const int row = ks * 4 + (lane >> 4);
+      float av[4], bv[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        av[b] = as[row * kLd + wp * 64 + b * 16 + (lane & 15)];
+        bv[b] = bs[row * kLd + wq * 64 + b * 16 + (lane & 15)];
+      }
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib)
+          acc[jb][ib] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[jb], av[ib], acc[jb][ib], 0, 0, 0);
+    }
+    if (more) PRICHS_WGF_STORE((kt + 1) & 1);
+    __syncthreads();
+  }
+#undef PRICHS_WGF_LOAD
+#undef PRICHS_WGF_SEL
+#undef PRICHS_WGF_STORE
+  const long long base = (long long)slot_of(g, E) * slot_stride;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      const int i = i0 + wp * 64 + ib * 16 + (lane & 15);
+      const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
+      float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
+      if (dst) {
+        float4 v = *reinterpret_cast<float4 *>(dst);
+        v.x = v.x + acc[jb][ib][0];
+        v.y = v.y + acc[jb][ib][1];
+        v.z = v.z + acc[jb][ib][2];
+        v.w = v.w + acc[jb][ib][3];
+        *reinterpret_cast<float4 *>(dst) = v;
+      }
+    }
+}
+
+// ------------------------------------------------------------- combine --
+// Per token t (8 columns per thread): the router VJP of
+// moe_router_unbiased_backward (backward.rs:269-287) over its k selections
+// in selection order, ws = sum_j g_j s_j, d_logit_j = g_j (s_j - ws); then
+//   d_x[t] = sum over the routed rows in ascending expert order of
+//            (w_j if weighting == 2 else 1) * dX[row_j]
+//          + dX[shared row of t]
+//          + sum over the selections in ascending expert order of
+//            d_logit_j * W_router[:, e_j]
+// (the reference's scatter_add_grad, kernels.cu:971-991, applies w_j to dX,
+// whose dY already carried w_j; weighting = 1 is the chain rule).  The
+// thread of column 0 also writes the token's row of d_logits [T, E] (zeros
+// outside the selections) for the router's weight gradient.
+template <typename T, typename OT>
+__global__ __launch_bounds__(256) void combine_kernel(
+    const T *__restrict__ dX, const float *__restrict__ scal, const int32_t *__restrict__ topk_idx,
+    const float *__restrict__ topk_w, const int32_t *__restrict__ token_row,
+    const float *__restrict__ w_router, int T_, int d, int k, int E, int weighting,
+    float *__restrict__ d_logits, OT *__restrict__ d_x) {
+#pragma clang fp contract(off)
+  const int per_tok = d / 8;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (long long)T_ * per_tok) return;
+  const int t = (int)(gid / per_tok);
+  const int c = (int)(gid - (long long)t * per_tok) * 8;
+
+  int ex[PRICHS_MAX_TOPK], rows[PRICHS_MAX_TOPK];
+  float wt[PRICHS_MAX_TOPK], dl[PRICHS_MAX_TOPK];
+  float ws = 0.f;
+#pragma unroll
+  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+    if (s < k) {
+      ex[s] = topk_idx[(size_t)t * k + s];
+      rows[s] = token_row[(size_t)t * k + s];
+      wt[s] = topk_w[(size_t)t * k + s];
+      dl[s] = scal[rows[s]];
+      const float p = wt[s] * dl[s];
+      ws = ws + p;
+    } else {
+      ex[s] = 0x7fffffff;
+      rows[s] = 0;
+      wt[s] = 0.f;
+      dl[s] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+    const float diff = dl[s] - ws;
+    dl[s] = s < k ? wt[s] * diff : 0.f;
+  }
+  // Ascending expert id (bubble passes over registers, as in the forward combine).
+#pragma unroll
+  for (int a = 0; a < PRICHS_MAX_TOPK - 1; ++a)
+#pragma unroll
+    for (int b = 0; b < PRICHS_MAX_TOPK - 1 - a; ++b)
+      if (ex[b] > ex[b + 1]) {
+        int te = ex[b]; ex[b] = ex[b + 1]; ex[b + 1] = te;
+        int tr = rows[b]; rows[b] = rows[b + 1]; rows[b + 1] = tr;
+        float tw = wt[b]; wt[b] = wt[b + 1]; wt[b + 1] = tw;
+        float td = dl[b]; dl[b] = dl[b + 1]; dl[b + 1] = td;
+      }
+  if (c == 0) {
+    float *row = d_logits + (size_t)t * E;
+    for (int e = 0; e < E; ++e) row[e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < PRICHS_MAX_TOPK; ++s)
+      if (s < k) row[ex[s]] = dl[s];
+  }
+  float acc[8], v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+#pragma unroll
+  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+    if (s < k) {
+      V8<T>::load(dX + (size_t)rows[s] * d + c, v);
+      const float wx = weighting == 2 ? wt[s] : 1.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = wx * v[j];
+        acc[j] = acc[j] + p;
+      }
+    }
+  }
+  V8<T>::load(dX + ((size_t)T_ * k + t) * d + c, v);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = acc[j] + v[j];
+  float rs[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rs[j] = 0.f;
+#pragma unroll
+  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+    if (s < k) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = dl[s] * w_router[(size_t)(c + j) * E + ex[s]];
+        rs[j] = rs[j] + p;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = acc[j] + rs[j];
+  V8<OT>::store(d_x + (size_t)t * d + c, acc);
+}
+
+// ------------------------------------------------------- router weights --
+// dW_router [d, E] += x^T d_logits (the reference's router sgemm, beta = 1,
+// engine.rs:2705-2789).  Pass 1: chunk n of kRouterChunk tokens writes
+// part[n][c][e] = sum over its tokens (ascending) of x[t][c] d_logits[t][e];
+// pass 2 adds the chunks in ascending order to dW.
+constexpr int kRouterChunk = 128;  // tokens per pass-1 workgroup (32 KiB of d_logits in LDS)
+
+template <typename T>
+__global__ __launch_bounds__(256) void router_wgrad_part_kernel(const T *__restrict__ x,
+                                                                const float *__restrict__ d_logits,
+                                                                int T_, int d, int E,
+                                                                float *__restrict__ part) {
+#pragma clang fp contract(off)
+  __shared__ float dl[kRouterChunk * PRICHS_MAX_EXPERTS];
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int t0 = blockIdx.y * kRouterChunk;
+  const int nt = min(kRouterChunk, T_ - t0);
+  for (int i = threadIdx.x; i < nt * E; i += 256) dl[i] = d_logits[(size_t)t0 * E + i];
+  __syncthreads();
+  if (c >= d) return;
+  float acc[PRICHS_MAX_EXPERTS];
+#pragma unroll
+  for (int e = 0; e < PRICHS_MAX_EXPERTS; ++e) acc[e] = 0.f;
+  for (int t = 0; t < nt; ++t) {
+    const float xv = Elem<T>::load(x + (size_t)(t0 + t) * d + c);
+#pragma unroll
+    for (int e = 0; e < PRICHS_MAX_EXPERTS; ++e) {
+      if (e < E) {
+        const float p = xv * dl[t * E + e];
+        acc[e] = acc[e] + p;
+      }
+    }
+  }
+  float *dst = part + ((size_t)blockIdx.y * d + c) * E;
+#pragma unroll
+  for (int e = 0; e < PRICHS_MAX_EXPERTS; ++e)
+    if (e < E) dst[e] = acc[e];
+}
+
+__global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(const float *__restrict__ part,
+                                                                  int n_chunks, int n,
+                                                                  float *__restrict__ dw) {
+#pragma clang fp contract(off)
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int ch = 0; ch < n_chunks; ++ch) s = s + part[(size_t)ch * n + i];
+  dw[i] = dw[i] + s;
+}
+
+unsigned blocks_for(long long n, int per = 256) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers --
+int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *row_token,
+             const float *row_weight, size_t rows, size_t routed_rows, size_t d, int dtype,
+             void *dy, void *xg, float *scal, hipStream_t s) {
+  if (rows == 0) return PRICHS_OK;
+  const unsigned grid = (unsigned)cdiv(rows, 4);
+  if (dtype == PRICHS_DTYPE_BF16)
+    hipLaunchKernelGGL(rows_kernel<bf16_t>, dim3(grid), dim3(256), 0, s,
+                       static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(d_out),
+                       static_cast<const bf16_t *>(y), row_token, row_weight, (int)rows,
+                       (int)routed_rows, (int)d, static_cast<bf16_t *>(dy),
+                       static_cast<bf16_t *>(xg), scal);
+  else
+    hipLaunchKernelGGL(rows_kernel<float>, dim3(grid), dim3(256), 0, s,
+                       static_cast<const float *>(x), static_cast<const float *>(d_out),
+                       static_cast<const float *>(y), row_token, row_weight, (int)rows,
+                       (int)routed_rows, (int)d, static_cast<float *>(dy),
+                       static_cast<float *>(xg), scal);
+  PRICHS_LAUNCH_CHECK("moe backward: rows");
+  return PRICHS_OK;
+}
+
+int bwd_swiglu(void *gu, const void *da, size_t rows, size_t f, size_t np, int dtype,
+               hipStream_t s) {
+  if (rows == 0) return PRICHS_OK;
+  const long long n = (long long)rows * (long long)(np / (2 * kIl) * (kIl / 8));
+  if (dtype == PRICHS_DTYPE_BF16)
+    hipLaunchKernelGGL(swiglu_bwd_kernel<bf16_t>, dim3(blocks_for(n)), dim3(256), 0, s,
+                       static_cast<bf16_t *>(gu), static_cast<const bf16_t *>(da), (int)rows,
+                       (int)f, (int)np);
+  else
+    hipLaunchKernelGGL(swiglu_bwd_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, s,
+                       static_cast<float *>(gu), static_cast<const float *>(da), (int)rows,
+                       (int)f, (int)np);
+  PRICHS_LAUNCH_CHECK("moe backward: swiglu");
+  return PRICHS_OK;
+}
+
+int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb, size_t total_rows,
+              const int32_t *offsets, size_t G, size_t E, size_t P, size_t Q, float *out0,
+              float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, hipStream_t s) {
+  const int tiles_q = (int)cdiv(Q, wg::BQ);
+  const int tiles = (int)cdiv(P, wg::BP) * tiles_q;
+  const unsigned grid = (unsigned)(G * (size_t)tiles);
+  if (grid == 0) return PRICHS_OK;
+  if (dtype == PRICHS_DTYPE_BF16) {
+    const size_t ab = total_rows * lda * 2, bb = total_rows * ldb * 2;
+    if (ab >= wgb::kOutOfRange || bb >= wgb::kOutOfRange)
+      return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: operands of %zu and %zu bytes exceed 2 GiB",
+                  ab, bb);
+    auto kern = gateup ? wgrad_bf16_kernel<true> : wgrad_bf16_kernel<false>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[gateup]) {
+      PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)wgb::kLdsBytes),
+                     "moe backward: set LDS size");
+      attr_set[gateup] = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(wg::kThreads), wgb::kLdsBytes, s,
+                       static_cast<const bf16_t *>(A), (int)lda, (uint32_t)ab,
+                       static_cast<const bf16_t *>(B), (int)ldb, (uint32_t)bb, offsets, (int)G,
+                       (int)E, (int)P, (int)Q, tiles_q, tiles, out0, out1, (int)ldo,
+                       (long long)slot_stride, (int)f);
+  } else {
+    auto kern = gateup ? wgrad_f32_kernel<true> : wgrad_f32_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(wg::kThreads), wgf::kLdsBytes, s,
+                       static_cast<const float *>(A), (int)lda, static_cast<const float *>(B),
+                       (int)ldb, offsets, (int)G, (int)E, (int)P, (int)Q, tiles_q, tiles, out0,
+                       out1, (int)ldo, (long long)slot_stride, (int)f);
+  }
+  PRICHS_LAUNCH_CHECK("moe backward: weight gradient");
+  return PRICHS_OK;
+}
+
+int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, const float *topk_w,
+                const int32_t *token_row, const float *w_router, size_t T, size_t d, size_t k,
+                size_t E, int weighting, int dtype, float *d_logits, void *d_x, int dx_dtype,
+                hipStream_t s) {
+  if (T == 0) return PRICHS_OK;
+  const unsigned grid = blocks_for((long long)T * (long long)(d / 8));
+#define PRICHS_BWD_COMBINE(TT, OT)                                                              \
+  hipLaunchKernelGGL((combine_kernel<TT, OT>), dim3(grid), dim3(256), 0, s,                    \
+                     static_cast<const TT *>(dX), scal, topk_idx, topk_w, token_row, w_router, \
+                     (int)T, (int)d, (int)k, (int)E, weighting, d_logits, static_cast<OT *>(d_x))
+  if (dtype == PRICHS_DTYPE_BF16) {
+    if (dx_dtype == PRICHS_DTYPE_BF16)
+      PRICHS_BWD_COMBINE(bf16_t, bf16_t);
+    else
+      PRICHS_BWD_COMBINE(bf16_t, float);
+  } else {
+    if (dx_dtype == PRICHS_DTYPE_BF16)
+      PRICHS_BWD_COMBINE(float, bf16_t);
+    else
+      PRICHS_BWD_COMBINE(float, float);
+  }
+#undef PRICHS_BWD_COMBINE
+  PRICHS_LAUNCH_CHECK("moe backward: combine");
+  return PRICHS_OK;
+}
+
+size_t bwd_router_part_elems(size_t max_tokens, size_t d, size_t E) {
+  return cdiv(max_tokens, kRouterChunk) * d * E;
+}
+
+int bwd_router_wgrad(const void *x, const float *d_logits, size_t T, size_t d, size_t E, int dtype,
+                     float *part, float *dw, hipStream_t s) {
+  if (T == 0) return PRICHS_OK;
+  const unsigned n_chunks = (unsigned)cdiv(T, kRouterChunk);
+  const dim3 grid((unsigned)cdiv(d, 256), n_chunks);
+  if (dtype == PRICHS_DTYPE_BF16)
+    hipLaunchKernelGGL(router_wgrad_part_kernel<bf16_t>, grid, dim3(256), 0, s,
+                       static_cast<const bf16_t *>(x), d_logits, (int)T, (int)d, (int)E, part);
+  else
+    hipLaunchKernelGGL(router_wgrad_part_kernel<float>, grid, dim3(256), 0, s,
+                       static_cast<const float *>(x), d_logits, (int)T, (int)d, (int)E, part);
+  PRICHS_LAUNCH_CHECK("moe backward: router weight gradient");
+  const int n = (int)(d * E);
+  hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3(blocks_for(n)), dim3(256), 0, s, part,
+                     (int)n_chunks, n, dw);
+  PRICHS_LAUNCH_CHECK("moe backward: router weight gradient reduce");
+  return PRICHS_OK;
+}
+
+}  // namespace prichs

@@ -121,6 +121,32 @@ int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t 
                       size_t max_group_rows, const void *w_packed, size_t d, size_t f, int dtype,
                       void *y, void *stream);
 
+// Plain grouped GEMM over the engine's row space (no SwiGLU):
+// C[r][n] = sum_k A[a_rows ? a_rows[r] : r][k] * B_g[n][k] for the rows r of
+// each group g, B_g the g-th packed [Np, K] weight (prichs_pack_weight layout,
+// b_group_stride elements apart); columns n < n_store are written.
+int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const void *B,
+                      size_t b_group_stride, size_t Np, size_t K, void *C, size_t ldc,
+                      size_t n_store, const int32_t *offsets, size_t G, size_t max_rows,
+                      size_t max_group_rows, int dtype, void *stream);
+
+// MoE backward stages (backward.hip); the engine sequences them.
+int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *row_token,
+             const float *row_weight, size_t rows, size_t routed_rows, size_t d, int dtype,
+             void *dy, void *xg, float *scal, hipStream_t s);
+int bwd_swiglu(void *gu, const void *da, size_t rows, size_t f, size_t np, int dtype,
+               hipStream_t s);
+int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb, size_t total_rows,
+              const int32_t *offsets, size_t G, size_t E, size_t P, size_t Q, float *out0,
+              float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, hipStream_t s);
+int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, const float *topk_w,
+                const int32_t *token_row, const float *w_router, size_t T, size_t d, size_t k,
+                size_t E, int weighting, int dtype, float *d_logits, void *d_x, int dx_dtype,
+                hipStream_t s);
+size_t bwd_router_part_elems(size_t max_tokens, size_t d, size_t E);
+int bwd_router_wgrad(const void *x, const float *d_logits, size_t T, size_t d, size_t E, int dtype,
+                     float *part, float *dw, hipStream_t s);
+
 // Checkpoint reading shared by the engines' upload-from-checkpoint entry
 // points: parameter `index` must hold exactly `want` floats (`what` and
 // `layer` name it in the error message).

@@ -10,6 +10,14 @@
 //
 // Row space of act / y: routed rows (expert ascending, token ascending), then
 // the shared expert's T rows (group E).
+//
+// Backward (after enable_backward): nine launches on the forward's stash,
+//   gate/up pre-activations (plain grouped GEMM) -> rows pass (dY, gathered
+//   x, router scalars) -> dW_down -> dA = dY Wd^T -> SwiGLU backward ->
+//   dW_gate / dW_up -> dX = [dG dU] [Wg Wu]^T -> combine (router VJP, d_x)
+//   -> dW_router
+// with the transposed weights packed at upload.
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -39,6 +47,20 @@ struct prichs_moe_engine {
   void *y = nullptr;
   size_t gu_elems = 0, dn_elems = 0;  // packed elements per expert
   size_t last_T = 0;
+  bool stash_valid = false;  // a forward's intermediates await a backward
+
+  // Backward: a second allocation made by enable_backward.
+  bool bwd = false;
+  void *bwd_arena = nullptr;
+  void *w_down_t = nullptr;  // per group packed [roundup(f, 256)][d]: B of dA = dY Wd^T
+  void *w_cat = nullptr;     // per group packed [roundup(d, 256)][np_gu]: B of dX
+  size_t np_gu = 0, dt_elems = 0, cat_elems = 0;
+  void *gu = nullptr;        // [rows, np_gu] gate/up pre-activations, then dG / dU
+  void *dy = nullptr;        // [rows, d] dY, then dX
+  void *xg = nullptr;        // [rows, d] x gathered by row
+  float *scal = nullptr;     // [rows] router scalars of the routed rows
+  float *dlogits = nullptr;  // [max_tokens, E]
+  float *rpart = nullptr;    // router weight-gradient partial sums
 
   // Stage timing: `slots` sets of PRICHS_NUM_STAGES events, filled in turn
   // by timed forwards (created by set_timing, never inside forward).
@@ -181,6 +203,8 @@ extern "C" int prichs_moe_engine_destroy(prichs_moe_engine *eng) {
       if (e) (void)hipEventDestroy(e);
     if (eng->arena && hipFree(eng->arena) != hipSuccess)
       rc = fail(PRICHS_ERR_HIP, "engine_destroy: hipFree failed");
+    if (eng->bwd_arena && hipFree(eng->bwd_arena) != hipSuccess)
+      rc = fail(PRICHS_ERR_HIP, "engine_destroy: hipFree failed");
   }
   delete eng;
   return rc;
@@ -208,6 +232,32 @@ extern "C" int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_r
                           dn.data() + es * eng->dn_elems * grp);
     if (rc) return rc;
   }
+  // Backward operands: B[n][k] = Wd[n][k] (n < f, k < d) for dA = dY Wd^T,
+  // and B[n][p] = Wg[n][c] / Wu[n][c] for packed gate / up column p of
+  // column c (zero on padding) for dX = [dG dU] [Wg Wu]^T.
+  std::vector<char> dt, cat;
+  if (eng->bwd) {
+    const size_t d = eng->d, f = eng->f, np = eng->np_gu;
+    dt.resize(es * eng->dt_elems * G);
+    cat.resize(es * eng->cat_elems * G);
+    std::vector<float> wt(d * f), wc(np * d);
+    for (size_t slot = 0; slot < G; ++slot) {
+      const size_t grp = slot < eng->S ? eng->E : slot - eng->S;
+      for (size_t n = 0; n < f; ++n)
+        for (size_t kk = 0; kk < d; ++kk) wt[kk * f + n] = down[slot][n * d + kk];
+      int rc = prichs_pack_weight(wt.data(), d, f, eng->dtype, dt.data() + es * eng->dt_elems * grp);
+      if (rc) return rc;
+      const size_t il = prichs_gate_up_interleave(eng->dtype);
+      for (size_t p = 0; p < np; ++p) {
+        const size_t blk = p / (2 * il), w = p % (2 * il);
+        const size_t c = blk * il + (w < il ? w : w - il);
+        const float *src = w < il ? gate[slot] : up[slot];
+        for (size_t n = 0; n < d; ++n) wc[p * d + n] = c < f ? src[n * f + c] : 0.0f;
+      }
+      rc = prichs_pack_weight(wc.data(), np, d, eng->dtype, cat.data() + es * eng->cat_elems * grp);
+      if (rc) return rc;
+    }
+  }
   std::vector<float> bias(eng->E, 0.0f);
   if (router_bias) std::memcpy(bias.data(), router_bias, sizeof(float) * eng->E);
   DeviceGuard g(eng->device);
@@ -222,6 +272,13 @@ extern "C" int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_r
                  "engine_upload: gate/up");
   PRICHS_HIP_TRY(hipMemcpy(eng->w_down, dn.data(), dn.size(), hipMemcpyHostToDevice),
                  "engine_upload: down");
+  if (eng->bwd) {
+    PRICHS_HIP_TRY(hipMemcpy(eng->w_down_t, dt.data(), dt.size(), hipMemcpyHostToDevice),
+                   "engine_upload: transposed down");
+    PRICHS_HIP_TRY(hipMemcpy(eng->w_cat, cat.data(), cat.size(), hipMemcpyHostToDevice),
+                   "engine_upload: transposed gate/up");
+  }
+  eng->stash_valid = false;
   PRICHS_HIP_TRY(hipDeviceSynchronize(), "engine_upload: synchronize");
   eng->uploaded = true;
   return PRICHS_OK;
@@ -309,8 +366,10 @@ extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, 
   if (T > eng->max_tokens)
     return fail(PRICHS_ERR_CAPACITY, "engine_forward: T=%zu exceeds max_tokens=%zu", T,
                 eng->max_tokens);
+  eng->stash_valid = false;
   if (T == 0) {
     eng->last_T = 0;
+    eng->stash_valid = true;
     return PRICHS_OK;
   }
   PRICHS_REQUIRE(x && out, "engine_forward: null pointer argument");
@@ -349,7 +408,131 @@ extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, 
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[5], s), "engine_forward: event");
   if (tm) ++eng->recorded;
   eng->last_T = T;
+  eng->stash_valid = true;
   return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_enable_backward(prichs_moe_engine *eng) {
+  PRICHS_REQUIRE(eng != nullptr, "engine_enable_backward: null engine");
+  if (eng->bwd) return PRICHS_OK;
+  if (eng->uploaded)
+    return fail(PRICHS_ERR_STATE,
+                "engine_enable_backward: call before upload (the upload packs the transposed "
+                "weights)");
+  if (eng->S != 1)
+    return fail(PRICHS_ERR_UNSUPPORTED,
+                "engine_enable_backward: the backward has one shared expert (moe.rs:61), the "
+                "engine has n_shared=%zu",
+                eng->S);
+  const size_t d = eng->d, f = eng->f, E = eng->E, G = E + 1, Tm = eng->max_tokens;
+  const size_t es = dtype_size(eng->dtype);
+  const size_t rows = Tm * (eng->k + 1);
+  const size_t np = prichs_packed_gate_up_elems(1, f, eng->dtype);  // packed rows of one K column
+  // The bf16 weight-gradient kernel addresses its operands with 32-bit offsets.
+  if (eng->dtype == PRICHS_DTYPE_BF16 && rows * std::max(np, d) * es >= (size_t)1 << 31)
+    return fail(PRICHS_ERR_UNSUPPORTED,
+                "engine_enable_backward: max_tokens=%zu makes operands of 2 GiB or more", Tm);
+  eng->np_gu = np;
+  eng->dt_elems = prichs_packed_weight_elems(d, f, eng->dtype);
+  eng->cat_elems = prichs_packed_weight_elems(np, d, eng->dtype);
+  Carve c;
+  const size_t o_dt = c.take(es * eng->dt_elems * G);
+  const size_t o_cat = c.take(es * eng->cat_elems * G);
+  const size_t o_gu = c.take(es * rows * np);
+  const size_t o_dy = c.take(es * rows * d);
+  const size_t o_xg = c.take(es * rows * d);
+  const size_t o_scal = c.take(sizeof(float) * rows);
+  const size_t o_dl = c.take(sizeof(float) * Tm * E);
+  const size_t o_rp = c.take(sizeof(float) * bwd_router_part_elems(Tm, d, E));
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_enable_backward: cannot select device");
+  hipError_t e = hipMalloc(&eng->bwd_arena, c.off);
+  if (e != hipSuccess) {
+    eng->bwd_arena = nullptr;
+    return fail(PRICHS_ERR_CAPACITY, "engine_enable_backward: hipMalloc(%zu bytes): %s", c.off,
+                hipGetErrorString(e));
+  }
+  char *base = static_cast<char *>(eng->bwd_arena);
+  eng->w_down_t = base + o_dt;
+  eng->w_cat = base + o_cat;
+  eng->gu = base + o_gu;
+  eng->dy = base + o_dy;
+  eng->xg = base + o_xg;
+  eng->scal = reinterpret_cast<float *>(base + o_scal);
+  eng->dlogits = reinterpret_cast<float *>(base + o_dl);
+  eng->rpart = reinterpret_cast<float *>(base + o_rp);
+  eng->bwd = true;
+  return PRICHS_OK;
+}
+
+namespace {
+bool aligned16(const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+}  // namespace
+
+extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
+                                          const void *d_out, size_t T, void *d_x, int d_x_dtype,
+                                          const prichs_moe_grads *grads, int dx_weighting,
+                                          void *stream) {
+  PRICHS_REQUIRE(eng != nullptr && grads != nullptr, "engine_backward: null pointer argument");
+  PRICHS_REQUIRE(dtype_ok(d_x_dtype), "engine_backward: bad d_x dtype %d", d_x_dtype);
+  PRICHS_REQUIRE(dx_weighting == 1 || dx_weighting == 2,
+                 "engine_backward: dx_weighting=%d (1 = chain rule, 2 = the reference's)",
+                 dx_weighting);
+  if (!eng->bwd)
+    return fail(PRICHS_ERR_STATE, "engine_backward: enable_backward was not called before upload");
+  if (!eng->uploaded) return fail(PRICHS_ERR_STATE, "engine_backward: weights not uploaded");
+  if (!eng->stash_valid || eng->last_T != T)
+    return fail(PRICHS_ERR_STATE,
+                "engine_backward: needs the forward of this batch (T=%zu) right before it", T);
+  const size_t d = eng->d, f = eng->f, E = eng->E, k = eng->k, G = E + 1;
+  PRICHS_REQUIRE(grads->d_router && grads->d_gate && grads->d_up && grads->d_down,
+                 "engine_backward: null gradient buffer");
+  PRICHS_REQUIRE(grads->slot_stride >= d * f && grads->slot_stride % 4 == 0,
+                 "engine_backward: slot_stride=%zu (a multiple of 4, at least d*f=%zu)",
+                 grads->slot_stride, d * f);
+  PRICHS_REQUIRE(aligned16(grads->d_router) && aligned16(grads->d_gate) &&
+                     aligned16(grads->d_up) && aligned16(grads->d_down),
+                 "engine_backward: gradient buffers must be 16-byte aligned");
+  if (T == 0) {
+    eng->stash_valid = false;
+    return PRICHS_OK;
+  }
+  PRICHS_REQUIRE(x && d_out && d_x, "engine_backward: null pointer argument");
+  PRICHS_REQUIRE(aligned16(x) && aligned16(d_out) && aligned16(d_x),
+                 "engine_backward: x, d_out and d_x must be 16-byte aligned");
+  DeviceGuard g(eng->device);
+  if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_backward: cannot select device");
+  eng->stash_valid = false;
+  hipStream_t s = as_stream(stream);
+  const int dt = eng->dtype;
+  const size_t rows = T * (k + 1), routed = T * k, np = eng->np_gu;
+  const size_t np_f = roundup(f, 256), np_d = roundup(d, 256);
+  int rc;
+  // Gate/up pre-activations of every row (the forward keeps only SwiGLU's output).
+  rc = grouped_gemm_rows(x, eng->row_token, d, eng->w_gate_up, eng->gu_elems, np, d, eng->gu, np,
+                         np, eng->offsets, G, rows, T, dt, stream);
+  if (rc) return rc;
+  rc = bwd_rows(x, d_out, eng->y, eng->row_token, eng->row_weight, rows, routed, d, dt, eng->dy,
+                eng->xg, eng->scal, s);
+  if (rc) return rc;
+  rc = bwd_wgrad(false, eng->act, f, eng->dy, d, rows, eng->offsets, G, E, f, d, grads->d_down,
+                 nullptr, d, grads->slot_stride, f, dt, s);
+  if (rc) return rc;
+  rc = grouped_gemm_rows(eng->dy, nullptr, d, eng->w_down_t, eng->dt_elems, np_f, d, eng->act, f,
+                         f, eng->offsets, G, rows, T, dt, stream);
+  if (rc) return rc;
+  rc = bwd_swiglu(eng->gu, eng->act, rows, f, np, dt, s);
+  if (rc) return rc;
+  rc = bwd_wgrad(true, eng->xg, d, eng->gu, np, rows, eng->offsets, G, E, d, np, grads->d_gate,
+                 grads->d_up, f, grads->slot_stride, f, dt, s);
+  if (rc) return rc;
+  rc = grouped_gemm_rows(eng->gu, nullptr, np, eng->w_cat, eng->cat_elems, np_d, np, eng->dy, d, d,
+                         eng->offsets, G, rows, T, dt, stream);
+  if (rc) return rc;
+  rc = bwd_combine(eng->dy, eng->scal, eng->topk_idx, eng->topk_w, eng->token_row, eng->w_router, T,
+                   d, k, E, dx_weighting, dt, eng->dlogits, d_x, d_x_dtype, s);
+  if (rc) return rc;
+  return bwd_router_wgrad(x, eng->dlogits, T, d, E, dt, eng->rpart, grads->d_router, s);
 }
 
 extern "C" int prichs_moe_engine_stash(const prichs_moe_engine *eng, prichs_moe_stash *out) {

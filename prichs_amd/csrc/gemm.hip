@@ -1073,6 +1073,27 @@ int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t 
                         (int)f, y, (int)d, (int)d, offsets, (int)G, 0, max_rows, dtype,
                         as_stream(stream), std::min(max_rows, max_group_rows));
 }
+int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const void *B,
+                      size_t b_group_stride, size_t Np, size_t K, void *C, size_t ldc,
+                      size_t n_store, const int32_t *offsets, size_t G, size_t max_rows,
+                      size_t max_group_rows, int dtype, void *stream) {
+  if (int rc = check_gemm_shape(Np, K, dtype, "grouped gemm")) return rc;
+  PRICHS_REQUIRE(Np % bn_of(dtype) == 0,
+                 "grouped gemm: Np=%zu is not a whole number of weight tiles", Np);
+  PRICHS_REQUIRE(G >= 1 && G <= (size_t)kMaxGroups, "grouped gemm: G=%zu outside [1, %d]", G,
+                 kMaxGroups);
+  PRICHS_REQUIRE(A && offsets && B && C, "grouped gemm: null pointer argument");
+  PRICHS_REQUIRE(lda >= K && ldc >= n_store && n_store <= Np && lda % 8 == 0 && ldc % 4 == 0,
+                 "grouped gemm: lda=%zu, ldc=%zu, n_store=%zu invalid for K=%zu, Np=%zu", lda,
+                 ldc, n_store, K, Np);
+  PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX && max_rows * lda <= (size_t)UINT32_MAX &&
+                     max_rows * ldc <= (size_t)UINT32_MAX &&
+                     b_group_stride * G <= (size_t)INT64_MAX,
+                 "grouped gemm: operands too large");
+  return launch_grouped(false, A, a_rows, (int)lda, B, (long long)b_group_stride, (int)Np,
+                        (int)K, C, (int)ldc, (int)n_store, offsets, (int)G, 0, max_rows, dtype,
+                        as_stream(stream), std::min(max_rows, max_group_rows));
+}
 }  // namespace prichs
 
 // A group can hold all max_rows rows, so the public entry points take that as

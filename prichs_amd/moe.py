@@ -120,6 +120,46 @@ class MoEEngine:
             ops.dtype_code(out), ops._stream(stream)))
         return out
 
+    def enable_backward(self):
+        """prichs_moe_engine_enable_backward: before upload."""
+        L.check(self.lib.prichs_moe_engine_enable_backward(self.handle))
+
+    def backward(self, x: torch.Tensor, d_out: torch.Tensor, grads: dict,
+                 dx_weighting: int = 2, d_x: torch.Tensor | None = None, d_x_dtype=None,
+                 stream=None) -> torch.Tensor:
+        """prichs_moe_engine_backward after the forward of the same x.
+
+        grads: device f32 tensors added to in place -- "d_router" [d, E] and
+        "d_gate", "d_up" [G, d, f], "d_down" [G, f, d] (G = 1 + E, the shared
+        expert first), or a "flat" [G, 3, d*f] buffer in the reference's
+        parameter order (gate, up, down of each slot).  Returns d_x [T, d]."""
+        for t in (x, d_out):
+            if ops.dtype_code(t) != self.dtype:
+                raise TypeError("x and d_out must have the engine dtype")
+        T = x.shape[0]
+        if d_x is None:
+            od = d_x_dtype if d_x_dtype is not None else x.dtype
+            d_x = torch.empty((T, self.d), dtype=od, device=x.device)
+        def ptr(t):
+            if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
+                raise ValueError("gradients are contiguous f32 device tensors")
+            return t.data_ptr()
+
+        g = L.MoEGrads()
+        g.d_router = ptr(grads["d_router"])
+        df = self.d * self.f
+        if "flat" in grads:
+            base = ptr(grads["flat"])
+            g.d_gate, g.d_up, g.d_down = base, base + 4 * df, base + 8 * df
+            g.slot_stride = 3 * df
+        else:
+            g.d_gate, g.d_up, g.d_down = (ptr(grads[k]) for k in ("d_gate", "d_up", "d_down"))
+            g.slot_stride = df
+        L.check(self.lib.prichs_moe_engine_backward(
+            self.handle, ops._p(ops._dev(x)), ops._p(ops._dev(d_out)), T, ops._p(d_x),
+            ops.dtype_code(d_x), C.byref(g), int(dx_weighting), ops._stream(stream)))
+        return d_x
+
     def set_timing(self, max_forwards: int):
         """Record stage events for the next ``max_forwards`` forwards (0 = off)."""
         L.check(self.lib.prichs_moe_engine_set_timing(self.handle, int(max_forwards)))

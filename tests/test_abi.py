@@ -120,6 +120,11 @@ def test_engine_argument_errors(lib):
     _expect(lib.prichs_moe_engine_forward(None, None, 4, None, 0, None, 0, None),
             L.PRICHS_ERR_INVALID_ARGUMENT, "null engine")
     assert lib.prichs_moe_engine_destroy(None) == L.PRICHS_OK
+    _expect(lib.prichs_moe_engine_enable_backward(None), L.PRICHS_ERR_INVALID_ARGUMENT,
+            "null engine")
+    g = L.MoEGrads()
+    _expect(lib.prichs_moe_engine_backward(None, None, None, 4, None, L.DTYPE_F32, C.byref(g), 2,
+                                           None), L.PRICHS_ERR_INVALID_ARGUMENT, "null pointer")
 
 
 # ----------------------------------------------------------------- packing --

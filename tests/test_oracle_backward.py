@@ -5,8 +5,8 @@ L = <d_out, moe(x)> with respect to x, the router and every expert matrix,
 with routing held where it is (each perturbed point is checked to select the
 same experts).  The float64 forward itself is pinned against the oracle's
 forward first.  The reference's routed input gradient carries the gate weight
-twice (its gather scales dY by w, kernels.cu:926-948, and its scatter scales
-again, kernels.cu:966-987); that mode is pinned by differencing a forward in
+twice (its gather scales dY by w, kernels.cu:926-944, and its scatter scales
+again, kernels.cu:971-991); that mode is pinned by differencing a forward in
 which each routed expert's output is weighted by w^2 held constant, plus the
 router path differenced on its own.
 """
@@ -175,7 +175,7 @@ def test_top1_modes_agree(orc):
 
 def test_gradients_accumulate(orc):
     # Weight gradients add onto what the caller passes (cuBLAS beta = 1 in the
-    # reference, engine.rs:2416-2440); d_x is overwritten.
+    # reference, engine.rs:2345-2362); d_x is overwritten.
     inp, d_out, _, _ = _setup()
     fresh = orc.moe_backward(inp, d_out)
     rng = np.random.default_rng(9)
