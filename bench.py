@@ -79,6 +79,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--backward", action="store_true",
+                    help="time a training step instead (the forward plus the MoE backward, "
+                         "prichs_moe_engine_backward) on configuration 2 or 3")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (known bytes) so that "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE can be scaled")
@@ -98,6 +101,8 @@ def main():
         copy_calibration()
     if args.config == 5:
         return bench_block(args)
+    if args.backward:
+        return bench_backward(args)
     log(f"bench: generating config {args.config} inputs")
     inp = synth.config_inputs(args.config)
     T, d, f, E, k, S = inp.T, inp.d, inp.f, inp.E, inp.k, inp.n_shared
@@ -196,6 +201,157 @@ def main():
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
         res["cpu_baseline"] = cpu_baseline(inp, args.cpu_seconds)
+    else:
+        res["cpu_baseline"] = None
+    eng.close()
+    print(json.dumps(res), flush=True)
+
+
+TRAIN_METRIC = ("MoE-layer training step (forward + backward) tokens/s + backward GEMM TFLOP/s "
+                "at d=1536 top-2, 1 GPU")
+
+
+def cpu_baseline_train(inp, d_out, target_s: float):
+    """Times the CPU oracle's forward + backward on a token sample of about target_s."""
+    from oracle import oracle
+    from prichs_amd import synth
+
+    oracle.build()
+    cores = oracle.num_threads()
+
+    def run(n):
+        sub = synth.MoEInputs(**{**inp.__dict__, "x": inp.x[:n], "T": n})
+        t0 = time.perf_counter()
+        oracle.moe_forward(sub)
+        oracle.moe_backward(sub, d_out[:n], dx_weighting=2)
+        return time.perf_counter() - t0
+
+    n0 = min(inp.T, 32)
+    t = run(n0)
+    n = int(min(inp.T, max(n0, n0 * target_s / max(t, 1e-3))))
+    n = max(n0, n - n % 32)
+    t = run(n)
+    return {
+        "value": n / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+        "sample": f"first {n} of {inp.T} tokens of the same synthetic inputs; C oracle forward "
+                  f"+ backward (reference CPU algorithm, f32, naive GEMMs), OpenMP over rows on "
+                  f"{cores} threads, {t:.1f} s",
+        "seconds": t,
+    }
+
+
+def bench_backward(args):
+    """One step = MoELayer forward + the MoE backward (d_x and every weight
+    gradient, accumulated into f32 buffers in the reference's parameter
+    layout) on configuration 2 (or 3)."""
+    import numpy as np
+    import torch
+
+    from prichs_amd import moe, synth
+
+    cfg = args.config if args.config in (2, 3) else 2
+    log(f"bench: generating config {cfg} inputs (training step)")
+    inp = synth.config_inputs(cfg)
+    T, d, f, E, k = inp.T, inp.d, inp.f, inp.E, inp.k
+    G = 1 + E
+    eng = moe.MoEEngine(d, f, E, k, 1, inp.dtype, max_tokens=T)
+    eng.enable_backward()
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    bf = torch.bfloat16
+    x = torch.from_numpy(inp.x).to("cuda").to(bf)
+    d_out_np = synth.round_bf16(np.random.default_rng(1).standard_normal((T, d)).astype(np.float32))
+    d_out = torch.from_numpy(d_out_np).to("cuda").to(bf)
+    out = torch.empty((T, d), dtype=bf, device="cuda")
+    d_x = torch.empty((T, d), dtype=bf, device="cuda")
+    grads = {"d_router": torch.zeros((d, E), dtype=torch.float32, device="cuda"),
+             "flat": torch.zeros((G, 3, d * f), dtype=torch.float32, device="cuda")}
+
+    def step():
+        eng.forward(x, out=out)
+        eng.backward(x, d_out, grads, dx_weighting=2, d_x=d_x)
+
+    log("bench: warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    eng.set_timing(args.steps)
+    log(f"bench: timing {args.steps} training steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    fms = eng.stage_ms()
+    bms = eng.backward_stage_ms()
+    log("bench: forward stage ms", json.dumps({kk: round(v, 4) for kk, v in fms.items()}))
+    log("bench: backward stage ms", json.dumps({kk: round(v, 4) for kk, v in bms.items()}))
+
+    rows = T * (k + 1)
+    np_gu = 2 * ((f + 31) // 32 * 32)
+    np_gu = (np_gu + 255) // 256 * 256
+    gemm_flops = {  # algorithmic flops per launch (padding excluded)
+        "gate_up": 4.0 * rows * d * f, "dw_down": 2.0 * rows * f * d, "d_act": 2.0 * rows * d * f,
+        "dw_gate_up": 4.0 * rows * d * f, "d_x_gemm": 4.0 * rows * f * d,
+    }
+    kernels = {
+        "gate_up": "grouped GEMM, gate/up pre-activations (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, false>)",
+        "dw_down": "grouped weight gradient dW_down += act^T dY (wgrad_bf16_kernel<false>)",
+        "d_act": "grouped GEMM dA = dY Wd^T (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, false>)",
+        "dw_gate_up": "grouped weight gradient dW_gate/up += x^T [dG dU] (wgrad_bf16_kernel<true>)",
+        "d_x_gemm": "grouped GEMM dX = [dG dU] [Wg Wu]^T (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, false>)",
+    }
+    per = {kk: {"ms": bms[kk], "tflops": fl / (bms[kk] / 1e3) / 1e12}
+           for kk, fl in gemm_flops.items()}
+    dom = max(per, key=lambda kk: per[kk]["ms"])
+    bwd_gemm_ms = sum(bms[kk] for kk in gemm_flops)
+    bwd_gemm_tflops = sum(gemm_flops.values()) / (bwd_gemm_ms / 1e3) / 1e12
+    es = 2
+    rows_bytes = rows * d * es * 4 + T * k * d * es + rows * 4 + T * k * 8
+    swiglu_bytes = rows * np_gu * es * 2 + rows * f * es
+    combine_bytes = rows * d * es + T * k * 16 + T * d * es + T * E * 4 + d * E * 4
+
+    def gbps(b, stage):
+        return b / (bms[stage] / 1e3) / 1e9 if bms[stage] > 0 else None
+
+    res = {
+        "metric": TRAIN_METRIC,
+        "value": T * args.steps / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": inp.dtype,
+        "data": "synthetic (seeded SplitMix64 + Box-Muller, seed 0; d_out numpy seed 1)",
+        "config": {"workload": WORKLOADS[cfg].replace("forward", "forward + backward"),
+                   "tokens": T, "d_model": d, "d_ffn": f, "routed_experts": E,
+                   "shared_experts": 1, "top_k": k, "dx_weighting": 2},
+        "roofline": {"kernel": kernels[dom], "bound": "mfma", "achieved": per[dom]["tflops"],
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": per[dom]["tflops"] / PEAK_BF16_TFLOPS, "traffic": None,
+                     "algorithmic_flops_per_launch": gemm_flops[dom],
+                     "avg_launch_ms": per[dom]["ms"]},
+        "backward_gemms": {"tflops": bwd_gemm_tflops, "frac_of_peak": bwd_gemm_tflops / PEAK_BF16_TFLOPS,
+                           "per_stage": per},
+        "memory_bound_stages": {
+            "rows": {"ms": bms["rows"], "GB/s": gbps(rows_bytes, "rows"), "bytes": rows_bytes},
+            "swiglu_bwd": {"ms": bms["swiglu_bwd"], "GB/s": gbps(swiglu_bytes, "swiglu_bwd"),
+                           "bytes": swiglu_bytes},
+            "combine": {"ms": bms["combine"], "GB/s": gbps(combine_bytes, "combine"),
+                        "bytes": combine_bytes},
+            "peak_GB/s": PEAK_HBM_GBPS,
+        },
+        "forward_ms": fms["total"],
+        "backward_ms": bms["total"],
+        "backward_stage_ms": {kk: v for kk, v in bms.items() if kk != "n"},
+        "device": torch.cuda.get_device_name(0),
+    }
+    if not args.no_cpu_baseline:
+        log("bench: CPU baseline (oracle forward + backward)")
+        res["cpu_baseline"] = cpu_baseline_train(inp, d_out_np, args.cpu_seconds)
     else:
         res["cpu_baseline"] = None
     eng.close()

@@ -388,9 +388,10 @@ int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
 
 /* Allocates the backward's workspace (about (T*(k+1)) * (2f + 2d) elements
  * of the engine dtype for max_tokens T) and makes the next uploads also pack
- * the transposed weights the input-gradient products need.  Call after
- * create and before upload / upload_checkpoint.  Needs n_shared = 1 (the
- * reference's layer, moe.rs:61).  Synchronous. */
+ * the transposed weights the input-gradient products need; from then on each
+ * forward's gate/up GEMM also stores its pre-activations for the backward.
+ * Call after create and before upload / upload_checkpoint.  Needs
+ * n_shared = 1 (the reference's layer, moe.rs:61).  Synchronous. */
 int prichs_moe_engine_enable_backward(prichs_moe_engine *eng);
 
 /* Caller-owned f32 gradient buffers (device) in the reference's layouts,
@@ -421,6 +422,17 @@ int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
                                const void *d_out, size_t T, void *d_x,
                                int d_x_dtype, const prichs_moe_grads *grads,
                                int dx_weighting, void *stream);
+
+/* Backward stage timing: with backward enabled, set_timing(eng, n) also
+ * records events in each of the next n backwards, and backward_stage_ms
+ * writes their AVERAGE milliseconds: [0] gate/up pre-activations (empty:
+ * the forward's gate/up GEMM writes them once the backward is enabled), [1] rows
+ * pass (dY, gathered x, router scalars), [2] dW_down, [3] dA = dY Wd^T,
+ * [4] SwiGLU backward, [5] dW_gate / dW_up, [6] dX = [dG dU] [Wg Wu]^T,
+ * [7] combine (router VJP, d_x), [8] dW_router, [9] whole backward. */
+#define PRICHS_NUM_BWD_STAGES 10
+int prichs_moe_engine_backward_stage_ms(prichs_moe_engine *eng, float *ms_out,
+                                        int *n_backwards);
 
 /* ---------------------------------------------------------------------- */
 /* 4. PrichsBlock engine (crates/prichs-model/src/block.rs:50-68): RMSNorm,  */

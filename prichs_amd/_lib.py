@@ -26,6 +26,9 @@ DTYPE_BF16 = 1
 MAX_EXPERTS = 64
 MAX_TOPK = 8
 NUM_STAGES = 6
+NUM_BWD_STAGES = 10
+BWD_STAGE_NAMES = ["gate_up", "rows", "dw_down", "d_act", "swiglu_bwd", "dw_gate_up", "d_x_gemm",
+                   "combine", "dw_router", "total"]
 STAGE_NAMES = ("router", "permute", "gate_up", "down", "combine", "total")
 
 
@@ -138,6 +141,7 @@ SIGNATURES = {
     "prichs_moe_engine_set_timing": (_i, [_vp, _i]),
     "prichs_moe_engine_stage_ms": (_i, [_vp, C.POINTER(_f), C.POINTER(_i)]),
     "prichs_moe_engine_enable_backward": (_i, [_vp]),
+    "prichs_moe_engine_backward_stage_ms": (_i, [_vp, C.POINTER(_f), C.POINTER(_i)]),
     "prichs_moe_engine_backward": (_i, [_vp, _vp, _vp, _sz, _vp, _i, C.POINTER(MoEGrads), _i, _vp]),
 }
 

@@ -19,7 +19,8 @@
 //                     in the packed [gate 32 | up 32] column order;
 //   wgrad kernels     dW[group] += A_g^T B_g over each group's rows (MFMA);
 //   combine_kernel    the router VJP and the input gradient of each token;
-//   router wgrad      dW_router += x^T d_logits (two deterministic passes).
+//   router wgrad      dW_router += x^T d_logits as per-expert weighted sums of
+//                     the gathered rows (two deterministic passes).
 #include "common.hpp"
 
 namespace prichs {
@@ -510,15 +511,16 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_f32_kernel(
 //          + sum over the selections in ascending expert order of
 //            d_logit_j * W_router[:, e_j]
 // (the reference's scatter_add_grad, kernels.cu:971-991, applies w_j to dX,
-// whose dY already carried w_j; weighting = 1 is the chain rule).  The
-// thread of column 0 also writes the token's row of d_logits [T, E] (zeros
-// outside the selections) for the router's weight gradient.
+// whose dY already carried w_j; weighting = 1 is the chain rule).  W_router
+// comes transposed, wrt [E, d], so a selection's 8 columns are one vector
+// load.  The thread of column 0 also writes d_logit_j at the row of each
+// selection (dlr [T*k], in row-space order) for the router's weight gradient.
 template <typename T, typename OT>
 __global__ __launch_bounds__(256) void combine_kernel(
     const T *__restrict__ dX, const float *__restrict__ scal, const int32_t *__restrict__ topk_idx,
     const float *__restrict__ topk_w, const int32_t *__restrict__ token_row,
-    const float *__restrict__ w_router, int T_, int d, int k, int E, int weighting,
-    float *__restrict__ d_logits, OT *__restrict__ d_x) {
+    const float *__restrict__ wrt, int T_, int d, int k, int weighting,
+    float *__restrict__ dlr, OT *__restrict__ d_x) {
 #pragma clang fp contract(off)
   const int per_tok = d / 8;
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -562,11 +564,9 @@ __global__ __launch_bounds__(256) void combine_kernel(
         float td = dl[b]; dl[b] = dl[b + 1]; dl[b + 1] = td;
       }
   if (c == 0) {
-    float *row = d_logits + (size_t)t * E;
-    for (int e = 0; e < E; ++e) row[e] = 0.f;
 #pragma unroll
     for (int s = 0; s < PRICHS_MAX_TOPK; ++s)
-      if (s < k) row[ex[s]] = dl[s];
+      if (s < k) dlr[rows[s]] = dl[s];
   }
   float acc[8], v[8];
 #pragma unroll
@@ -592,9 +592,10 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
   for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
     if (s < k) {
+      V8<float>::load(wrt + (size_t)ex[s] * d + c, v);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float p = dl[s] * w_router[(size_t)(c + j) * E + ex[s]];
+        const float p = dl[s] * v[j];
         rs[j] = rs[j] + p;
       }
     }
@@ -606,51 +607,85 @@ __global__ __launch_bounds__(256) void combine_kernel(
 
 // ------------------------------------------------------- router weights --
 // dW_router [d, E] += x^T d_logits (the reference's router sgemm, beta = 1,
-// engine.rs:2705-2789).  Pass 1: chunk n of kRouterChunk tokens writes
-// part[n][c][e] = sum over its tokens (ascending) of x[t][c] d_logits[t][e];
-// pass 2 adds the chunks in ascending order to dW.
-constexpr int kRouterChunk = 128;  // tokens per pass-1 workgroup (32 KiB of d_logits in LDS)
+// engine.rs:2705-2789).  d_logits[t][e] is zero unless t selected e, so
+// column e is a weighted sum over expert e's rows of the row space:
+// dW[:, e] += sum over rows r of group e of dlr[r] * xg[r] (xg = x gathered
+// by row, written by the rows pass).  Pass 1: one workgroup per chunk of
+// kRouterChunk rows of one group (chunks numbered group by group) writes
+// part[chunk][c]; pass 2 adds each group's chunks in ascending order.
+constexpr int kRouterChunk = 64;
+constexpr int kRouterUnroll = 8;  // rows whose loads are in flight together
+
+// Group and row range of chunk `ch` (-1 past the last chunk).
+__device__ inline int router_chunk(const int32_t *offsets, int E, int ch, int &r0, int &r1) {
+  int first = 0;
+  for (int e = 0; e < E; ++e) {
+    const int lo = offsets[e], hi = offsets[e + 1];
+    const int n = (hi - lo + kRouterChunk - 1) / kRouterChunk;
+    if (ch < first + n) {
+      r0 = lo + (ch - first) * kRouterChunk;
+      r1 = min(r0 + kRouterChunk, hi);
+      return e;
+    }
+    first += n;
+  }
+  return -1;
+}
 
 template <typename T>
-__global__ __launch_bounds__(256) void router_wgrad_part_kernel(const T *__restrict__ x,
-                                                                const float *__restrict__ d_logits,
-                                                                int T_, int d, int E,
+__global__ __launch_bounds__(256) void router_wgrad_part_kernel(const T *__restrict__ xg,
+                                                                const float *__restrict__ dlr,
+                                                                const int32_t *__restrict__ offsets,
+                                                                int E, int d,
                                                                 float *__restrict__ part) {
 #pragma clang fp contract(off)
-  __shared__ float dl[kRouterChunk * PRICHS_MAX_EXPERTS];
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  const int t0 = blockIdx.y * kRouterChunk;
-  const int nt = min(kRouterChunk, T_ - t0);
-  for (int i = threadIdx.x; i < nt * E; i += 256) dl[i] = d_logits[(size_t)t0 * E + i];
-  __syncthreads();
-  if (c >= d) return;
-  float acc[PRICHS_MAX_EXPERTS];
+  int r0 = 0, r1 = 0;
+  if (router_chunk(offsets, E, blockIdx.x, r0, r1) < 0) return;
+  for (int c = threadIdx.x * 8; c < d; c += 256 * 8) {
+    float acc[8];
 #pragma unroll
-  for (int e = 0; e < PRICHS_MAX_EXPERTS; ++e) acc[e] = 0.f;
-  for (int t = 0; t < nt; ++t) {
-    const float xv = Elem<T>::load(x + (size_t)(t0 + t) * d + c);
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int r = r0; r < r1; r += kRouterUnroll) {
+      float xv[kRouterUnroll][8], w[kRouterUnroll];
 #pragma unroll
-    for (int e = 0; e < PRICHS_MAX_EXPERTS; ++e) {
-      if (e < E) {
-        const float p = xv * dl[t * E + e];
-        acc[e] = acc[e] + p;
+      for (int u = 0; u < kRouterUnroll; ++u) {
+        const int rr = min(r + u, r1 - 1);  // rows past r1 get weight 0 below
+        V8<T>::load(xg + (size_t)rr * d + c, xv[u]);
+        w[u] = r + u < r1 ? dlr[rr] : 0.f;
       }
-    }
-  }
-  float *dst = part + ((size_t)blockIdx.y * d + c) * E;
 #pragma unroll
-  for (int e = 0; e < PRICHS_MAX_EXPERTS; ++e)
-    if (e < E) dst[e] = acc[e];
+      for (int u = 0; u < kRouterUnroll; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = xv[u][j] * w[u];
+          acc[j] = acc[j] + p;
+        }
+    }
+    V8<float>::store(part + (size_t)blockIdx.x * d + c, acc);
+  }
 }
 
 __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(const float *__restrict__ part,
-                                                                  int n_chunks, int n,
+                                                                  const int32_t *__restrict__ offsets,
+                                                                  int E, int d,
                                                                   float *__restrict__ dw) {
 #pragma clang fp contract(off)
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
+  if (i >= d * E) return;
+  const int c = i / E, e = i - c * E;
+  int first = 0;
+  for (int g = 0; g < e; ++g)
+    first += (offsets[g + 1] - offsets[g] + kRouterChunk - 1) / kRouterChunk;
+  const int n = (offsets[e + 1] - offsets[e] + kRouterChunk - 1) / kRouterChunk;
   float s = 0.f;
-  for (int ch = 0; ch < n_chunks; ++ch) s = s + part[(size_t)ch * n + i];
+  for (int ch = 0; ch < n; ch += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = ch + u < n ? part[(size_t)(first + ch + u) * d + c] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s = s + v[u];
+  }
   dw[i] = dw[i] + s;
 }
 
@@ -734,15 +769,14 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
 }
 
 int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, const float *topk_w,
-                const int32_t *token_row, const float *w_router, size_t T, size_t d, size_t k,
-                size_t E, int weighting, int dtype, float *d_logits, void *d_x, int dx_dtype,
-                hipStream_t s) {
+                const int32_t *token_row, const float *wrt, size_t T, size_t d, size_t k,
+                int weighting, int dtype, float *dlr, void *d_x, int dx_dtype, hipStream_t s) {
   if (T == 0) return PRICHS_OK;
   const unsigned grid = blocks_for((long long)T * (long long)(d / 8));
 #define PRICHS_BWD_COMBINE(TT, OT)                                                              \
   hipLaunchKernelGGL((combine_kernel<TT, OT>), dim3(grid), dim3(256), 0, s,                    \
-                     static_cast<const TT *>(dX), scal, topk_idx, topk_w, token_row, w_router, \
-                     (int)T, (int)d, (int)k, (int)E, weighting, d_logits, static_cast<OT *>(d_x))
+                     static_cast<const TT *>(dX), scal, topk_idx, topk_w, token_row, wrt,      \
+                     (int)T, (int)d, (int)k, weighting, dlr, static_cast<OT *>(d_x))
   if (dtype == PRICHS_DTYPE_BF16) {
     if (dx_dtype == PRICHS_DTYPE_BF16)
       PRICHS_BWD_COMBINE(bf16_t, bf16_t);
@@ -759,25 +793,24 @@ int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, cons
   return PRICHS_OK;
 }
 
-size_t bwd_router_part_elems(size_t max_tokens, size_t d, size_t E) {
-  return cdiv(max_tokens, kRouterChunk) * d * E;
+size_t bwd_router_part_elems(size_t max_tokens, size_t k, size_t d, size_t E) {
+  return (cdiv(max_tokens * k, kRouterChunk) + E) * d;
 }
 
-int bwd_router_wgrad(const void *x, const float *d_logits, size_t T, size_t d, size_t E, int dtype,
-                     float *part, float *dw, hipStream_t s) {
+int bwd_router_wgrad(const void *xg, const float *dlr, const int32_t *offsets, size_t T, size_t k,
+                     size_t d, size_t E, int dtype, float *part, float *dw, hipStream_t s) {
   if (T == 0) return PRICHS_OK;
-  const unsigned n_chunks = (unsigned)cdiv(T, kRouterChunk);
-  const dim3 grid((unsigned)cdiv(d, 256), n_chunks);
+  // Every group's chunks fit in cdiv(T*k, chunk) + E workgroups; the rest exit.
+  const unsigned grid = (unsigned)(cdiv(T * k, kRouterChunk) + E);
   if (dtype == PRICHS_DTYPE_BF16)
-    hipLaunchKernelGGL(router_wgrad_part_kernel<bf16_t>, grid, dim3(256), 0, s,
-                       static_cast<const bf16_t *>(x), d_logits, (int)T, (int)d, (int)E, part);
+    hipLaunchKernelGGL(router_wgrad_part_kernel<bf16_t>, dim3(grid), dim3(256), 0, s,
+                       static_cast<const bf16_t *>(xg), dlr, offsets, (int)E, (int)d, part);
   else
-    hipLaunchKernelGGL(router_wgrad_part_kernel<float>, grid, dim3(256), 0, s,
-                       static_cast<const float *>(x), d_logits, (int)T, (int)d, (int)E, part);
+    hipLaunchKernelGGL(router_wgrad_part_kernel<float>, dim3(grid), dim3(256), 0, s,
+                       static_cast<const float *>(xg), dlr, offsets, (int)E, (int)d, part);
   PRICHS_LAUNCH_CHECK("moe backward: router weight gradient");
-  const int n = (int)(d * E);
-  hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3(blocks_for(n)), dim3(256), 0, s, part,
-                     (int)n_chunks, n, dw);
+  hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3(blocks_for((long long)(d * E))), dim3(256),
+                     0, s, part, offsets, (int)E, (int)d, dw);
   PRICHS_LAUNCH_CHECK("moe backward: router weight gradient reduce");
   return PRICHS_OK;
 }

@@ -112,11 +112,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 // prichs_grouped_gate_up_swiglu / prichs_grouped_down with a tighter bound on
 // every group's row count (a caller that knows T passes T): decode-sized
-// groups then take the skinny weight-streaming kernel.
+// groups then take the skinny weight-streaming kernel.  pre (may be null)
+// also receives the gate/up pre-activations [rows][Np] in the packed column
+// order (Np = prichs_packed_gate_up_elems(1, f, dtype)), for a backward.
 int grouped_gate_up_swiglu_rows(const void *x, const int32_t *row_token, const int32_t *offsets,
                                 size_t G, size_t max_rows, size_t max_group_rows,
                                 const void *w_packed, size_t d, size_t f, int dtype, void *act,
-                                void *stream);
+                                void *stream, void *pre = nullptr);
 int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t max_rows,
                       size_t max_group_rows, const void *w_packed, size_t d, size_t f, int dtype,
                       void *y, void *stream);
@@ -140,12 +142,11 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
               const int32_t *offsets, size_t G, size_t E, size_t P, size_t Q, float *out0,
               float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, hipStream_t s);
 int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, const float *topk_w,
-                const int32_t *token_row, const float *w_router, size_t T, size_t d, size_t k,
-                size_t E, int weighting, int dtype, float *d_logits, void *d_x, int dx_dtype,
-                hipStream_t s);
-size_t bwd_router_part_elems(size_t max_tokens, size_t d, size_t E);
-int bwd_router_wgrad(const void *x, const float *d_logits, size_t T, size_t d, size_t E, int dtype,
-                     float *part, float *dw, hipStream_t s);
+                const int32_t *token_row, const float *wrt, size_t T, size_t d, size_t k,
+                int weighting, int dtype, float *dlr, void *d_x, int dx_dtype, hipStream_t s);
+size_t bwd_router_part_elems(size_t max_tokens, size_t k, size_t d, size_t E);
+int bwd_router_wgrad(const void *xg, const float *dlr, const int32_t *offsets, size_t T, size_t k,
+                     size_t d, size_t E, int dtype, float *part, float *dw, hipStream_t s);
 
 // Checkpoint reading shared by the engines' upload-from-checkpoint entry
 // points: parameter `index` must hold exactly `want` floats (`what` and

@@ -11,11 +11,11 @@
 // Row space of act / y: routed rows (expert ascending, token ascending), then
 // the shared expert's T rows (group E).
 //
-// Backward (after enable_backward): nine launches on the forward's stash,
-//   gate/up pre-activations (plain grouped GEMM) -> rows pass (dY, gathered
-//   x, router scalars) -> dW_down -> dA = dY Wd^T -> SwiGLU backward ->
-//   dW_gate / dW_up -> dX = [dG dU] [Wg Wu]^T -> combine (router VJP, d_x)
-//   -> dW_router
+// Backward (after enable_backward): on the forward's stash, whose gate/up
+// GEMM then also keeps the pre-activations,
+//   rows pass (dY, gathered x, router scalars) -> dW_down -> dA = dY Wd^T ->
+//   SwiGLU backward -> dW_gate / dW_up -> dX = [dG dU] [Wg Wu]^T ->
+//   combine (router VJP, d_x) -> dW_router (two passes)
 // with the transposed weights packed at upload.
 #include <algorithm>
 #include <cstring>
@@ -59,7 +59,8 @@ struct prichs_moe_engine {
   void *dy = nullptr;        // [rows, d] dY, then dX
   void *xg = nullptr;        // [rows, d] x gathered by row
   float *scal = nullptr;     // [rows] router scalars of the routed rows
-  float *dlogits = nullptr;  // [max_tokens, E]
+  float *dlr = nullptr;      // [max_tokens * k] d_logit of each routed row
+  float *wrt = nullptr;      // [E, d] router weights transposed
   float *rpart = nullptr;    // router weight-gradient partial sums
 
   // Stage timing: `slots` sets of PRICHS_NUM_STAGES events, filled in turn
@@ -67,6 +68,9 @@ struct prichs_moe_engine {
   int slots = 0;
   int recorded = 0;
   std::vector<hipEvent_t> ev;
+  // The same for backwards: PRICHS_NUM_BWD_STAGES events per backward.
+  int brecorded = 0;
+  std::vector<hipEvent_t> bev;
 };
 
 namespace prichs {
@@ -201,6 +205,8 @@ extern "C" int prichs_moe_engine_destroy(prichs_moe_engine *eng) {
     DeviceGuard g(eng->device);
     for (hipEvent_t e : eng->ev)
       if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : eng->bev)
+      if (e) (void)hipEventDestroy(e);
     if (eng->arena && hipFree(eng->arena) != hipSuccess)
       rc = fail(PRICHS_ERR_HIP, "engine_destroy: hipFree failed");
     if (eng->bwd_arena && hipFree(eng->bwd_arena) != hipSuccess)
@@ -273,6 +279,12 @@ extern "C" int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_r
   PRICHS_HIP_TRY(hipMemcpy(eng->w_down, dn.data(), dn.size(), hipMemcpyHostToDevice),
                  "engine_upload: down");
   if (eng->bwd) {
+    std::vector<float> wrt(eng->E * eng->d);
+    for (size_t e = 0; e < eng->E; ++e)
+      for (size_t c = 0; c < eng->d; ++c) wrt[e * eng->d + c] = w_router[c * eng->E + e];
+    PRICHS_HIP_TRY(hipMemcpy(eng->wrt, wrt.data(), sizeof(float) * wrt.size(),
+                             hipMemcpyHostToDevice),
+                   "engine_upload: transposed router");
     PRICHS_HIP_TRY(hipMemcpy(eng->w_down_t, dt.data(), dt.size(), hipMemcpyHostToDevice),
                    "engine_upload: transposed down");
     PRICHS_HIP_TRY(hipMemcpy(eng->w_cat, cat.data(), cat.size(), hipMemcpyHostToDevice),
@@ -394,8 +406,10 @@ extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, 
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[2], s), "engine_forward: event");
   // No group holds more than T rows (a token picks an expert at most once).
+  // With the backward enabled the GEMM also keeps the gate/up pre-activations.
   rc = grouped_gate_up_swiglu_rows(x, eng->row_token, eng->offsets, G, rows, T, eng->w_gate_up,
-                                   eng->d, eng->f, eng->dtype, eng->act, stream);
+                                   eng->d, eng->f, eng->dtype, eng->act, stream,
+                                   eng->bwd ? eng->gu : nullptr);
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[3], s), "engine_forward: event");
   rc = grouped_down_rows(eng->act, eng->offsets, G, rows, T, eng->w_down, eng->d, eng->f,
@@ -442,8 +456,9 @@ extern "C" int prichs_moe_engine_enable_backward(prichs_moe_engine *eng) {
   const size_t o_dy = c.take(es * rows * d);
   const size_t o_xg = c.take(es * rows * d);
   const size_t o_scal = c.take(sizeof(float) * rows);
-  const size_t o_dl = c.take(sizeof(float) * Tm * E);
-  const size_t o_rp = c.take(sizeof(float) * bwd_router_part_elems(Tm, d, E));
+  const size_t o_dl = c.take(sizeof(float) * Tm * eng->k);
+  const size_t o_wrt = c.take(sizeof(float) * E * d);
+  const size_t o_rp = c.take(sizeof(float) * bwd_router_part_elems(Tm, eng->k, d, E));
   DeviceGuard g(eng->device);
   if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_enable_backward: cannot select device");
   hipError_t e = hipMalloc(&eng->bwd_arena, c.off);
@@ -459,7 +474,8 @@ extern "C" int prichs_moe_engine_enable_backward(prichs_moe_engine *eng) {
   eng->dy = base + o_dy;
   eng->xg = base + o_xg;
   eng->scal = reinterpret_cast<float *>(base + o_scal);
-  eng->dlogits = reinterpret_cast<float *>(base + o_dl);
+  eng->dlr = reinterpret_cast<float *>(base + o_dl);
+  eng->wrt = reinterpret_cast<float *>(base + o_wrt);
   eng->rpart = reinterpret_cast<float *>(base + o_rp);
   eng->bwd = true;
   return PRICHS_OK;
@@ -507,32 +523,49 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   const int dt = eng->dtype;
   const size_t rows = T * (k + 1), routed = T * k, np = eng->np_gu;
   const size_t np_f = roundup(f, 256), np_d = roundup(d, 256);
+  const bool tm = eng->slots > 0 && eng->brecorded < eng->slots;
+  hipEvent_t *ev = tm ? &eng->bev[(size_t)eng->brecorded * PRICHS_NUM_BWD_STAGES] : nullptr;
   int rc;
-  // Gate/up pre-activations of every row (the forward keeps only SwiGLU's output).
-  rc = grouped_gemm_rows(x, eng->row_token, d, eng->w_gate_up, eng->gu_elems, np, d, eng->gu, np,
-                         np, eng->offsets, G, rows, T, dt, stream);
-  if (rc) return rc;
+#define PRICHS_BWD_MARK(i) \
+  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[i], s), "engine_backward: event")
+  PRICHS_BWD_MARK(0);
+  // (Stage 0, the gate/up pre-activations, is written by the forward's
+  // gate/up GEMM when the backward is enabled; its interval stays empty.)
+  PRICHS_BWD_MARK(1);
   rc = bwd_rows(x, d_out, eng->y, eng->row_token, eng->row_weight, rows, routed, d, dt, eng->dy,
                 eng->xg, eng->scal, s);
   if (rc) return rc;
+  PRICHS_BWD_MARK(2);
   rc = bwd_wgrad(false, eng->act, f, eng->dy, d, rows, eng->offsets, G, E, f, d, grads->d_down,
                  nullptr, d, grads->slot_stride, f, dt, s);
   if (rc) return rc;
+  PRICHS_BWD_MARK(3);
   rc = grouped_gemm_rows(eng->dy, nullptr, d, eng->w_down_t, eng->dt_elems, np_f, d, eng->act, f,
                          f, eng->offsets, G, rows, T, dt, stream);
   if (rc) return rc;
+  PRICHS_BWD_MARK(4);
   rc = bwd_swiglu(eng->gu, eng->act, rows, f, np, dt, s);
   if (rc) return rc;
+  PRICHS_BWD_MARK(5);
   rc = bwd_wgrad(true, eng->xg, d, eng->gu, np, rows, eng->offsets, G, E, d, np, grads->d_gate,
                  grads->d_up, f, grads->slot_stride, f, dt, s);
   if (rc) return rc;
+  PRICHS_BWD_MARK(6);
   rc = grouped_gemm_rows(eng->gu, nullptr, np, eng->w_cat, eng->cat_elems, np_d, np, eng->dy, d, d,
                          eng->offsets, G, rows, T, dt, stream);
   if (rc) return rc;
-  rc = bwd_combine(eng->dy, eng->scal, eng->topk_idx, eng->topk_w, eng->token_row, eng->w_router, T,
-                   d, k, E, dx_weighting, dt, eng->dlogits, d_x, d_x_dtype, s);
+  PRICHS_BWD_MARK(7);
+  rc = bwd_combine(eng->dy, eng->scal, eng->topk_idx, eng->topk_w, eng->token_row, eng->wrt, T, d,
+                   k, dx_weighting, dt, eng->dlr, d_x, d_x_dtype, s);
   if (rc) return rc;
-  return bwd_router_wgrad(x, eng->dlogits, T, d, E, dt, eng->rpart, grads->d_router, s);
+  PRICHS_BWD_MARK(8);
+  rc = bwd_router_wgrad(eng->xg, eng->dlr, eng->offsets, T, k, d, E, dt, eng->rpart,
+                        grads->d_router, s);
+  if (rc) return rc;
+  PRICHS_BWD_MARK(9);
+#undef PRICHS_BWD_MARK
+  if (tm) ++eng->brecorded;
+  return PRICHS_OK;
 }
 
 extern "C" int prichs_moe_engine_stash(const prichs_moe_engine *eng, prichs_moe_stash *out) {
@@ -562,8 +595,15 @@ extern "C" int prichs_moe_engine_set_timing(prichs_moe_engine *eng, int max_forw
     PRICHS_HIP_TRY(hipEventCreate(&e), "engine_set_timing: hipEventCreate");
     eng->ev.push_back(e);
   }
+  const size_t bneed = eng->bwd ? (size_t)max_forwards * PRICHS_NUM_BWD_STAGES : 0;
+  while (eng->bev.size() < bneed) {
+    hipEvent_t e = nullptr;
+    PRICHS_HIP_TRY(hipEventCreate(&e), "engine_set_timing: hipEventCreate");
+    eng->bev.push_back(e);
+  }
   eng->slots = max_forwards;
   eng->recorded = 0;
+  eng->brecorded = 0;
   return PRICHS_OK;
 }
 
@@ -589,5 +629,30 @@ extern "C" int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
   for (int i = 0; i < PRICHS_NUM_STAGES; ++i) ms_out[i] = (float)(acc[i] / eng->recorded);
   if (n_forwards) *n_forwards = eng->recorded;
   eng->recorded = 0;
+  return PRICHS_OK;
+}
+
+extern "C" int prichs_moe_engine_backward_stage_ms(prichs_moe_engine *eng, float *ms_out,
+                                                   int *n_backwards) {
+  PRICHS_REQUIRE(eng && ms_out, "engine_backward_stage_ms: null pointer argument");
+  if (eng->brecorded == 0)
+    return fail(PRICHS_ERR_STATE, "engine_backward_stage_ms: no timed backward since set_timing");
+  DeviceGuard g(eng->device);
+  constexpr int N = PRICHS_NUM_BWD_STAGES;
+  double acc[N] = {0};
+  for (int b = 0; b < eng->brecorded; ++b) {
+    hipEvent_t *ev = &eng->bev[(size_t)b * N];
+    PRICHS_HIP_TRY(hipEventSynchronize(ev[N - 1]), "engine_backward_stage_ms: sync");
+    float ms = 0.f;
+    for (int i = 0; i + 1 < N; ++i) {
+      PRICHS_HIP_TRY(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "engine_backward_stage_ms: elapsed");
+      acc[i] += ms;
+    }
+    PRICHS_HIP_TRY(hipEventElapsedTime(&ms, ev[0], ev[N - 1]), "engine_backward_stage_ms: elapsed");
+    acc[N - 1] += ms;
+  }
+  for (int i = 0; i < N; ++i) ms_out[i] = (float)(acc[i] / eng->brecorded);
+  if (n_backwards) *n_backwards = eng->brecorded;
+  eng->brecorded = 0;
   return PRICHS_OK;
 }

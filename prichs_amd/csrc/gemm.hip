@@ -231,7 +231,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
     bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
-    int G, int dense_m, int stage_c) {
+    int G, int dense_m, int stage_c, bf16_t *__restrict__ P) {
   constexpr int BM = Cf::BM, BN = Cf::BN, BK = Cf::BK, kStages = Cf::kStages;
   constexpr int WGN = Cf::WGN, WM = Cf::WM, WN = Cf::WN, MI = Cf::MI, NJ = Cf::NJ;
   constexpr int kRowsPerInst = Cf::kRowsPerInst, kInstA = Cf::kInstA, kInstB = Cf::kInstB;
@@ -461,6 +461,23 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
       // blocks: in block q, gate column c (16-column piece jj) pairs with up
       // column c, kIl / 16 pieces on.
       constexpr int kPieces = Cf::kIl / 16;  // 16-column pieces per gate (or up) half
+      if (P != nullptr) {
+        // Training forward: the gate/up pre-activations too, [rows][Np] in
+        // packed column order (the backward's SwiGLU derivative needs them).
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int m = lr + 16 * i;
+          if (m < mg) {
+            bf16_t *prow = P + (long long)(row0 + m) * Np + n0 + wn * WN + cq;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const f32x4 a = acc[i][j];
+              *reinterpret_cast<u32x2 *>(prow + 16 * j) =
+                  u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+            }
+          }
+        }
+      }
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = lr + 16 * i;
@@ -525,7 +542,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     const float *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const float *__restrict__ B, long long b_group_stride, int Np, int K,
     float *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets, int G,
-    int dense_m) {
+    int dense_m, float *__restrict__ P) {
   extern __shared__ float ldsf[];
   __shared__ TileMap tm;
   build_tile_map(tm, offsets, G, BM, dense_m);
@@ -616,6 +633,21 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(
     }
 
     const int rbase = m0 + wm * WM + 4 * (lane >> 4);
+    if (GATEUP && P != nullptr) {
+      // Training forward: the pre-activations, [rows][Np] in packed order.
+      const int pbase = n0 + wn * WN + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int lr = rbase + i * 16 + r;
+          if (lr < mg) {
+            float *prow = P + (long long)(row0 + lr) * Np + pbase;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) prow[j * 16] = acc[i][j][r];
+          }
+        }
+    }
     if (GATEUP) {
       const int cbase = (n0 / (2 * kIl) + wn) * kIl + (lane & 15);
 #pragma unroll
@@ -694,7 +726,7 @@ template <bool GATEUP, int U, int SK>
 __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_stride, int K, bf16_t *__restrict__ C, int ldc,
-    int n_store, const int32_t *__restrict__ offsets) {
+    int n_store, const int32_t *__restrict__ offsets, bf16_t *__restrict__ P, int ldp) {
   constexpr int kRow = 32 * U + 8;                 // LDS row (16-byte pad: conflict-free reads)
   constexpr int kSegs = BM * 4 * U;                // 16-byte segments of one chunk tile
   constexpr int kSegPerThread = kSegs / kThreads;  // U / 2
@@ -798,6 +830,19 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
   const int cq = 4 * (lane >> 4);
   const int mr = m0 + (lane & 15);
   if (GATEUP) {
+    if (P != nullptr && ks == 0) {
+      // Training forward: this wave's pre-activations (packed rows 16 wn..).
+      const int pcol = blockIdx.x * BN + wn * 16 + cq;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int m = mr + 16 * t;
+        if (m < r1) {
+          const f32x4 v = t == 0 ? acc0 : acc1;
+          *reinterpret_cast<u32x2 *>(P + (long long)m * ldp + pcol) =
+              u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        }
+      }
+    }
     if (ks == 0 && wn < 2) {
       gate_s[wn][0][lane] = acc0;
       gate_s[wn][1][lane] = acc1;
@@ -894,7 +939,7 @@ template <typename T> void pack_down_impl(const float *down, size_t d, size_t f,
 template <class Cf, bool GATEUP>
 int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                 int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
-                int dense_m, size_t max_rows, int cus, hipStream_t s) {
+                int dense_m, size_t max_rows, int cus, hipStream_t s, void *pre) {
   // Persistent grid: one workgroup per CU (the LDS ring allows one), fewer
   // when the launch has fewer tiles.
   const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN);
@@ -915,7 +960,7 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
   hipLaunchKernelGGL((bf16_gemm_kernel<Cf, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
                      b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G, dense_m,
-                     stage_c);
+                     stage_c, static_cast<bf16_t *>(pre));
   PRICHS_LAUNCH_CHECK("grouped gemm launch");
   return PRICHS_OK;
 }
@@ -923,12 +968,13 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
 template <bool GATEUP, int U, int SK>
 int launch_skinny_u(const void *A, const int32_t *a_rows, int lda, const void *B,
                     long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
-                    const int32_t *offsets, int G, int mtiles, hipStream_t s) {
+                    const int32_t *offsets, int G, int mtiles, hipStream_t s, void *pre) {
   static_assert(Bf16::kIl == skinny::BN / 2, "a skinny slab is one [gate | up] block");
   hipLaunchKernelGGL((skinny::skinny_gemm_kernel<GATEUP, U, SK>),
                      dim3(Np / skinny::BN, G, mtiles), dim3(skinny::kThreads * SK), 0, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
-                     b_stride, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets);
+                     b_stride, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets,
+                     static_cast<bf16_t *>(pre), Np);
   PRICHS_LAUNCH_CHECK("skinny grouped gemm launch");
   return PRICHS_OK;
 }
@@ -948,7 +994,7 @@ int launch_skinny_u(const void *A, const int32_t *a_rows, int lda, const void *B
 template <bool GATEUP>
 int launch_skinny(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                   int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
-                  size_t max_group_rows, hipStream_t s) {
+                  size_t max_group_rows, hipStream_t s, void *pre) {
   const int mtiles = (int)std::max<size_t>(1, (max_group_rows + skinny::BM - 1) / skinny::BM);
   int sk = PRICHS_SKINNY_SK;
   while (sk > 1 && K % (sk * 64) != 0) sk /= 2;
@@ -958,7 +1004,7 @@ int launch_skinny(const void *A, const int32_t *a_rows, int lda, const void *B, 
 #define PRICHS_SKINNY(U_, SK_)                                                                   \
   if (u == U_ && sk == SK_)                                                                     \
   return launch_skinny_u<GATEUP, U_, SK_>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store, \
-                                          offsets, G, mtiles, s)
+                                          offsets, G, mtiles, s, pre)
   PRICHS_SKINNY(2, 1);
   PRICHS_SKINNY(4, 1);
   PRICHS_SKINNY(8, 1);
@@ -973,25 +1019,26 @@ int launch_skinny(const void *A, const int32_t *a_rows, int lda, const void *B, 
 
 // max_group_rows bounds every group's row count (offsets[g+1] - offsets[g]);
 // bf16 launches whose groups all fit the skinny kernel's reach take it.
+// pre (gate/up only, may be null): the pre-activations [rows][Np], packed order.
 int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, const void *B,
                    long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
                    const int32_t *offsets, int G, int dense_m, size_t max_rows, int dtype,
-                   hipStream_t s, size_t max_group_rows) {
+                   hipStream_t s, size_t max_group_rows, void *pre = nullptr) {
   if (dtype == PRICHS_DTYPE_BF16 && dense_m == 0 && max_group_rows <= (size_t)skinny::kSkinnyRows &&
       K % kBf16KMultiple == 0 && Np % skinny::BN == 0) {
     return gateup ? launch_skinny<true>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
-                                        offsets, G, max_group_rows, s)
+                                        offsets, G, max_group_rows, s, pre)
                   : launch_skinny<false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
-                                         offsets, G, max_group_rows, s);
+                                         offsets, G, max_group_rows, s, nullptr);
   }
   const int cus = device_cu_count();
   if (cus <= 0) return fail(PRICHS_ERR_HIP, "grouped gemm: cannot query the device");
   if (dtype == PRICHS_DTYPE_BF16) {
     if (gateup)
       return launch_bf16<Bf16, true>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
-                                     offsets, G, dense_m, max_rows, cus, s);
+                                     offsets, G, dense_m, max_rows, cus, s, pre);
     return launch_bf16<Bf16Down, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
-                                        offsets, G, dense_m, max_rows, cus, s);
+                                        offsets, G, dense_m, max_rows, cus, s, nullptr);
   } else {
     const size_t ub = (max_rows / fp::BM + G) * (size_t)(Np / fp::BN);
     const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus * 4));
@@ -999,7 +1046,8 @@ int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, c
     hipLaunchKernelGGL(kern, dim3(grid), dim3(fp::kThreads), fp::kLdsBytes, s,
                        static_cast<const float *>(A), a_rows, lda,
                        static_cast<const float *>(B), b_stride, Np, K,
-                       static_cast<float *>(Cp), ldc, n_store, offsets, G, dense_m);
+                       static_cast<float *>(Cp), ldc, n_store, offsets, G, dense_m,
+                       gateup ? static_cast<float *>(pre) : nullptr);
   }
   PRICHS_LAUNCH_CHECK("grouped gemm launch");
   return PRICHS_OK;
@@ -1048,16 +1096,18 @@ namespace prichs {
 int grouped_gate_up_swiglu_rows(const void *x, const int32_t *row_token, const int32_t *offsets,
                                 size_t G, size_t max_rows, size_t max_group_rows,
                                 const void *w_packed, size_t d, size_t f, int dtype, void *act,
-                                void *stream) {
+                                void *stream, void *pre) {
   if (int rc = check_gemm_shape(d, f, dtype, "gate_up")) return rc;
   PRICHS_REQUIRE(G >= 1 && G <= (size_t)kMaxGroups, "gate_up: G=%zu outside [1, %d]", G,
                  kMaxGroups);
   PRICHS_REQUIRE(x && row_token && offsets && w_packed && act, "gate_up: null pointer argument");
   PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX, "gate_up: max_rows too large");
   const size_t np = gate_up_np(f, dtype);
+  PRICHS_REQUIRE(pre == nullptr || max_rows * np <= (size_t)INT64_MAX / 4,
+                 "gate_up: pre-activation buffer too large");
   return launch_grouped(true, x, row_token, (int)d, w_packed, (long long)(np * d), (int)np,
                         (int)d, act, (int)f, (int)f, offsets, (int)G, 0, max_rows, dtype,
-                        as_stream(stream), std::min(max_rows, max_group_rows));
+                        as_stream(stream), std::min(max_rows, max_group_rows), pre);
 }
 
 int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t max_rows,
@@ -1103,7 +1153,7 @@ extern "C" int prichs_grouped_gate_up_swiglu(const void *x, const int32_t *row_t
                                              const void *w_packed, size_t d, size_t f, int dtype,
                                              void *act, void *stream) {
   return grouped_gate_up_swiglu_rows(x, row_token, offsets, G, max_rows, max_rows, w_packed, d,
-                                     f, dtype, act, stream);
+                                     f, dtype, act, stream, nullptr);
 }
 
 extern "C" int prichs_grouped_down(const void *act, const int32_t *offsets, size_t G,

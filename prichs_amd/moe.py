@@ -160,6 +160,15 @@ class MoEEngine:
             ops.dtype_code(d_x), C.byref(g), int(dx_weighting), ops._stream(stream)))
         return d_x
 
+    def backward_stage_ms(self) -> dict:
+        """Average backward stage milliseconds over the recorded backwards (plus "n")."""
+        buf = (C.c_float * L.NUM_BWD_STAGES)()
+        n = C.c_int(0)
+        L.check(self.lib.prichs_moe_engine_backward_stage_ms(self.handle, buf, C.byref(n)))
+        out = dict(zip(L.BWD_STAGE_NAMES, list(buf)))
+        out["n"] = n.value
+        return out
+
     def set_timing(self, max_forwards: int):
         """Record stage events for the next ``max_forwards`` forwards (0 = off)."""
         L.check(self.lib.prichs_moe_engine_set_timing(self.handle, int(max_forwards)))

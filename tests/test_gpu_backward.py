@@ -231,3 +231,36 @@ def test_backward_config2_against_autograd(cuda):
     say("  errors", {k: f"{v:.2e}" for k, v in errs.items()})
     for k, v in errs.items():
         assert v <= TOL["bf16"], (k, v)
+
+
+@pytest.mark.parametrize("T,dtype", [(512, "bf16"), (32, "bf16"), (200, "f32")])
+def test_forward_unchanged_by_enable_backward(cuda, T, dtype):
+    # With the backward enabled the gate/up GEMM also stores its
+    # pre-activations; the layer output stays bit-identical (tiled, skinny and
+    # fp32 kernels).
+    say("forward with/without backward", T, dtype)
+    inp, _ = inputs(T, 256, 128, 8, 2, dtype, seed=T)
+    x = dev(inp.x, dtype)
+    outs = []
+    for enable in (False, True):
+        eng = make_engine(inp, enable=enable)
+        outs.append(eng.forward(x))
+        torch.cuda.synchronize()
+        eng.close()
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_backward_stage_timing(cuda):
+    inp, d_out = inputs(512, 256, 128, 8, 2, "bf16", seed=8)
+    eng = make_engine(inp)
+    eng.set_timing(2)
+    for _ in range(2):
+        run(eng, inp, d_out, 2)
+    ms = eng.backward_stage_ms()
+    say("  backward stage ms", ms)
+    assert ms["n"] == 2
+    assert ms["total"] > 0 and ms["gate_up"] >= 0
+    parts = sum(v for kk, v in ms.items() if kk not in ("total", "n"))
+    assert abs(parts - ms["total"]) <= 0.05 * ms["total"] + 1e-3
+    with pytest.raises(L.PrichsError, match="no timed backward"):
+        eng.backward_stage_ms()
