@@ -289,12 +289,13 @@ def bench_backward(args):
     rows = T * (k + 1)
     np_gu = 2 * ((f + 31) // 32 * 32)
     np_gu = (np_gu + 255) // 256 * 256
-    gemm_flops = {  # algorithmic flops per launch (padding excluded)
-        "gate_up": 4.0 * rows * d * f, "dw_down": 2.0 * rows * f * d, "d_act": 2.0 * rows * d * f,
+    # Algorithmic flops per launch (padding excluded).  The gate/up
+    # pre-activations come from the forward's GEMM, so the backward has four.
+    gemm_flops = {
+        "dw_down": 2.0 * rows * f * d, "d_act": 2.0 * rows * d * f,
         "dw_gate_up": 4.0 * rows * d * f, "d_x_gemm": 4.0 * rows * f * d,
     }
     kernels = {
-        "gate_up": "grouped GEMM, gate/up pre-activations (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, false>)",
         "dw_down": "grouped weight gradient dW_down += act^T dY (wgrad_bf16_kernel<false>)",
         "d_act": "grouped GEMM dA = dY Wd^T (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, false>)",
         "dw_gate_up": "grouped weight gradient dW_gate/up += x^T [dG dU] (wgrad_bf16_kernel<true>)",

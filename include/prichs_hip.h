@@ -20,7 +20,8 @@
  *  3. An engine handle that owns packed weights and workspace and runs the
  *     whole MoELayer forward (crates/prichs-model/src/moe.rs:93-225) on one
  *     stream with no host round trip and no allocation per call (and a
- *     PrichsBlock engine around it).
+ *     PrichsBlock engine around it); the same engine runs the layer's
+ *     training-step backward (crates/prichs-cuda/src/engine.rs:2242-2789).
  *
  *  4. A reader of the reference's checkpoint files that uploads a block's
  *     weights into those engines.

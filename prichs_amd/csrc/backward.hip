@@ -184,13 +184,27 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(T *__restrict__ gu,
 //           p goes to out0 (gate) or out1 (up) at column 32 (p / 64) + p % 32
 //           when that is < f.
 // Workgroups: one per (group, 128 x 128 output tile), the shared group's
-// tiles first (it has the most rows).
+// tiles first (it has the most rows).  Workgroups are dealt round-robin to
+// the 8 XCDs, so block b runs on XCD b % 8; each XCD takes a contiguous band
+// of every group's tiles (tiles in a band share A and B panels in that XCD's
+// L2), and every group's tiles spread over all XCDs.
 namespace wg {
 constexpr int BP = 128, BQ = 128;
 constexpr int kThreads = 256;
 }  // namespace wg
 
 __device__ __forceinline__ int slot_of(int g, int E) { return g < E ? g + 1 : 0; }
+
+// Block -> (group, tile), or false past the last tile (the grid is
+// 8 * band * G with band = ceil(tiles / 8)).
+__device__ __forceinline__ bool wgrad_item(int G, int tiles, int &g, int &tile) {
+  const int band = (tiles + 7) / 8;
+  const int xcd = (int)(blockIdx.x & 7), s = (int)(blockIdx.x >> 3);
+  const int gi = s / band;
+  tile = xcd * band + (s - gi * band);
+  g = (gi + G - 1) % G;  // the last group (shared) first
+  return gi < G && tile < tiles;
+}
 
 // Output element pointer of (i, j) or nullptr when outside the gradient.
 template <bool GATEUP>
@@ -261,9 +275,8 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_bf16_kernel(
     int tiles_q, int tiles, float *out0, float *out1, int ldo, long long slot_stride, int f) {
   using namespace wgb;
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  const int gi = blockIdx.x / tiles;
-  const int tile = blockIdx.x - gi * tiles;
-  const int g = (gi + G - 1) % G;  // the last group (shared) first
+  int g, tile;
+  if (!wgrad_item(G, tiles, g, tile)) return;
   const int row_lo = offsets[g];
   const int mg = offsets[g + 1] - row_lo;
   if (mg <= 0) return;
@@ -404,9 +417,8 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_f32_kernel(
     float *out0, float *out1, int ldo, long long slot_stride, int f) {
   using namespace wgf;
   extern __shared__ __attribute__((aligned(16))) float ldsw[];
-  const int gi = blockIdx.x / tiles;
-  const int tile = blockIdx.x - gi * tiles;
-  const int g = (gi + G - 1) % G;
+  int g, tile;
+  if (!wgrad_item(G, tiles, g, tile)) return;
   const int row_lo = offsets[g];
   const int mg = offsets[g + 1] - row_lo;
   if (mg <= 0) return;
@@ -736,7 +748,7 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
               float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, hipStream_t s) {
   const int tiles_q = (int)cdiv(Q, wg::BQ);
   const int tiles = (int)cdiv(P, wg::BP) * tiles_q;
-  const unsigned grid = (unsigned)(G * (size_t)tiles);
+  const unsigned grid = (unsigned)(8 * cdiv((size_t)tiles, 8) * G);
   if (grid == 0) return PRICHS_OK;
   if (dtype == PRICHS_DTYPE_BF16) {
     const size_t ab = total_rows * lda * 2, bb = total_rows * ldb * 2;
