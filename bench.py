@@ -476,10 +476,48 @@ def bench_block(args):
             "peak_GB/s": PEAK_HBM_GBPS,
         },
         "device": torch.cuda.get_device_name(0),
-        "cpu_baseline": None,
     }
     eng.close()
+    if not args.no_cpu_baseline:
+        log("bench: CPU baseline (oracle block forward)")
+        res["cpu_baseline"] = cpu_baseline_block(inp, args.cpu_seconds)
+    else:
+        res["cpu_baseline"] = None
     print(json.dumps(res), flush=True)
+
+
+def cpu_baseline_block(inp, target_s: float):
+    """Times the CPU oracle's block forward on a prefix of the first sequence:
+    with causal attention a prefix's rows need no later rows, so the prefix is
+    an exact sample of the workload.  The prefix doubles (from 64 rows) until a
+    run takes a third of target_s or the whole sequence is covered."""
+    import dataclasses
+
+    from oracle import oracle
+
+    oracle.build()
+    cores = oracle.num_threads()
+
+    def run(n):
+        sub = dataclasses.replace(inp, batch=1, seq_len=n, x=inp.x[:n])
+        t0 = time.perf_counter()
+        oracle.block_forward(sub)
+        return time.perf_counter() - t0
+
+    n = 64
+    t = run(n)
+    while t < target_s / 3 and n < inp.seq_len:
+        n = min(inp.seq_len, 2 * n)
+        t = run(n)
+    note = ("" if n == inp.seq_len else
+            "; a prefix's tokens attend to fewer keys than the average token of a full sequence")
+    return {
+        "value": n / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+        "sample": f"first {n} rows of sequence 0 (of {inp.batch} x {inp.seq_len}); C oracle block "
+                  f"forward (RMSNorm, f32 projections, causal GQA attention with RoPE, MoE, "
+                  f"residuals), OpenMP over rows on {cores} threads, {t:.1f} s{note}",
+        "seconds": t,
+    }
 
 
 if __name__ == "__main__":
