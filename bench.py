@@ -266,9 +266,11 @@ def bench_backward(args):
     grads = {"d_router": torch.zeros((d, E), dtype=torch.float32, device="cuda"),
              "flat": torch.zeros((G, 3, d * f), dtype=torch.float32, device="cuda")}
 
+    # beta = 0: the gradients are overwritten, as zero_grads() followed by the
+    # backward (forward_backward_vram, model.rs:1198-1207) leaves them.
     def step():
         eng.forward(x, out=out)
-        eng.backward(x, d_out, grads, dx_weighting=2, d_x=d_x)
+        eng.backward(x, d_out, grads, dx_weighting=2, d_x=d_x, beta=0)
 
     log("bench: warmup")
     for _ in range(args.warmup):
@@ -329,7 +331,9 @@ def bench_backward(args):
         "data": "synthetic (seeded SplitMix64 + Box-Muller, seed 0; d_out numpy seed 1)",
         "config": {"workload": WORKLOADS[cfg].replace("forward", "forward + backward"),
                    "tokens": T, "d_model": d, "d_ffn": f, "routed_experts": E,
-                   "shared_experts": 1, "top_k": k, "dx_weighting": 2},
+                   "shared_experts": 1, "top_k": k, "dx_weighting": 2,
+                   "grads": "f32, reference parameter layout, overwritten (beta = 0: zero_grads "
+                            "then the backward)"},
         "roofline": {"kernel": kernels[dom], "bound": "mfma", "achieved": per[dom]["tflops"],
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": per[dom]["tflops"] / PEAK_BF16_TFLOPS, "traffic": None,

@@ -395,25 +395,31 @@ int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
  * n_shared = 1 (the reference's layer, moe.rs:61).  Synchronous. */
 int prichs_moe_engine_enable_backward(prichs_moe_engine *eng);
 
-/* Caller-owned f32 gradient buffers (device) in the reference's layouts,
- * added to like dev_grads (cuBLAS beta = 1): d_router [d, E]; per expert
- * slot s (0 = shared expert, 1 + e = routed expert e) d_gate + s*slot_stride
- * and d_up + s*slot_stride [d, f], d_down + s*slot_stride [f, d].  With the
- * reference's parameter order (model.rs:312-338) d_up = d_gate + d*f,
- * d_down = d_gate + 2*d*f and slot_stride = 3*d*f.  16-byte aligned. */
+/* Caller-owned f32 gradient buffers (device) in the reference's layouts:
+ * d_router [d, E]; per expert slot s (0 = shared expert, 1 + e = routed
+ * expert e) d_gate + s*slot_stride and d_up + s*slot_stride [d, f],
+ * d_down + s*slot_stride [f, d].  With the reference's parameter order
+ * (model.rs:312-338) d_up = d_gate + d*f, d_down = d_gate + 2*d*f and
+ * slot_stride = 3*d*f.  16-byte aligned.  Every buffer becomes
+ * beta * buffer + gradient: beta = 1 adds to it like the reference's dev_grads
+ * (cuBLAS beta = 1; gradient accumulation over micro-batches,
+ * model.rs:1209-1215); beta = 0 overwrites it, the same as zero_grads
+ * (engine.rs:710-720) before the call (model.rs:1198-1207), and needs no read
+ * of the old values. */
 typedef struct prichs_moe_grads {
   float *d_router;
   float *d_gate;
   float *d_up;
   float *d_down;
   size_t slot_stride;
+  int beta;
 } prichs_moe_grads;
 
 /* Gradients of the layer output's loss given d_out = dL/d(moe output)
  * [T, d] (engine dtype, device), for the batch of the forward that ran just
  * before on this engine (same x [T, d], device): writes d_x [T, d] (d_x_dtype,
- * device; the reference's d_normed2) and adds the weight gradients to
- * *grads.  dx_weighting = 2 reproduces the reference, whose routed input
+ * device; the reference's d_normed2) and the weight gradients into *grads
+ * (beta above).  dx_weighting = 2 reproduces the reference, whose routed input
  * gradient carries the gate weight twice (its gather scales dY by w,
  * kernels.cu:926-944, and its scatter scales dX again, kernels.cu:971-991);
  * dx_weighting = 1 is the chain rule.  The weight gradients do not depend on

@@ -48,6 +48,7 @@ class MoEGrads(C.Structure):
         ("d_up", C.c_void_p),
         ("d_down", C.c_void_p),
         ("slot_stride", C.c_size_t),
+        ("beta", C.c_int),
     ]
 
 

@@ -21,6 +21,8 @@
 //   combine_kernel    the router VJP and the input gradient of each token;
 //   router wgrad      dW_router += x^T d_logits as per-expert weighted sums of
 //                     the gathered rows (two deterministic passes).
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace prichs {
@@ -172,10 +174,12 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(T *__restrict__ gu,
 }
 
 // ------------------------------------------------------ weight gradients --
-// dW[group g] += A_g^T B_g, A_g = rows [offsets[g], offsets[g+1]) of A [*, lda]
-// (columns 0..P), B_g the same rows of B [*, ldb] (columns 0..Q): the
-// reference's cuBLAS sgemm calls with beta = 1 (engine.rs:2345-2362 for
-// dW_down, 2417-2451 for dW_gate / dW_up; 2619-2654 for the shared expert).  Groups are the engine's: routed
+// dW[group g] = beta dW + A_g^T B_g, A_g = rows [offsets[g], offsets[g+1]) of
+// A [*, lda] (columns 0..P), B_g the same rows of B [*, ldb] (columns 0..Q):
+// the reference's cuBLAS sgemm calls, beta = 1 (engine.rs:2345-2362 for
+// dW_down, 2417-2451 for dW_gate / dW_up; 2619-2654 for the shared expert);
+// beta = 0 is the same after zero_grads (engine.rs:710-720), whose gradients
+// of experts without rows are zero.  Groups are the engine's: routed
 // experts 0..E-1 then the shared expert (group E); group g's matrices sit at
 // slot g + 1 (routed) or 0 (shared) of the caller's gradients, slot s at
 // out + s * slot_stride.
@@ -219,24 +223,45 @@ __device__ __forceinline__ float *wgrad_dst(float *out0, float *out1, int ldo, l
 }
 
 // --- bf16: v_mfma_f32_16x16x32_bf16, both operands read transposed from LDS.
-// A K-step is 32 rows.  Both 32 x 128 operand tiles go from global memory to
-// LDS with buffer_load ... lds (16 bytes per lane, no VGPR round trip) into a
-// ring of 4 stages, 3 ahead of the MFMAs; rows past the group's end load as
-// zeros (their offsets are past the buffer's range).  Tile rows are 256
-// bytes of 16 chunks, chunk c of row R stored at c ^ ((2R) & 15).
-// ds_read_b64_tr_b16 hands lane i of a 16-lane group column i of the 4 rows x
-// 16 columns the group addresses, so lane 16g + m, reading row 4g + m/4
-// (and 16 rows on) at columns 4(m % 4).., receives the 8 K values {4g..4g+3,
-// 16+4g..16+4g+3} of one column: the same K slots for both operands.
+// 256 x 256 output tiles, 8 waves as 2 (P) x 4 (Q) of 128 x 64 each; a K-step
+// is 32 rows.  Both 32 x 256 operand tiles go from global memory to LDS with
+// buffer_load ... lds (16 bytes per lane, no VGPR round trip) into a ring of 4
+// stages, 3 ahead of the MFMAs; rows past the chunk's end load as zeros (their
+// offsets are past the buffer's range).  Tile rows are 512 bytes of 32 chunks,
+// chunk c of row R stored at c ^ ((2R) & 15).  ds_read_b64_tr_b16 hands lane i
+// of a 16-lane group column i of the 4 rows x 16 columns the group addresses,
+// so lane 16g + m, reading row 4g + m/4 (and 16 rows on) at columns
+// 4(m % 4).., receives the 8 K values {4g..4g+3, 16+4g..16+4g+3} of one
+// column: the same K slots for both operands.
+//
+// Balance: a group of m > kSplitRows rows (the shared expert, a hot expert)
+// is split over K into n = ceil(m / kSplitRows) chunks of equal length
+// (a multiple of 32), so work items are of similar size.  Chunk c of a split
+// group stores its tile to partial slot (the group's first slot) + c, and
+// wgrad_reduce_kernel then adds the chunk sum, in chunk order, to the
+// gradient: dW + (((p0 + p1) + p2) + ...), one addition to dW like an
+// unsplit group's.  Deterministic, no atomics and no waiting between
+// workgroups.
 namespace wgb {
-constexpr int BK = 32;
-constexpr uint32_t kTileBytes = BK * 128 * 2;        // 8 KiB: one operand tile
-constexpr uint32_t kStageBytes = 2 * kTileBytes;     // A tile then B tile
+constexpr int BP = 256, BQ = 256, BK = 32;
+constexpr int kThreads = 512;
+constexpr int kRowBytes = 2 * BP;                     // one tile row: 256 bf16
+constexpr uint32_t kTileBytes = BK * kRowBytes;       // 16 KiB: one operand tile
+constexpr uint32_t kStageBytes = 2 * kTileBytes;      // A tile then B tile
 constexpr int kStages = 4;
-constexpr size_t kLdsBytes = (size_t)kStages * kStageBytes;  // 64 KiB
-constexpr uint32_t kHiOff = 16 * 256;                // rows 16.. of a tile
-constexpr uint32_t kOutOfRange = 0x80000000u;        // buffer offset that loads zeros
+constexpr size_t kLdsBytes = (size_t)kStages * kStageBytes;  // 128 KiB
+constexpr uint32_t kHiOff = 16 * kRowBytes;           // rows 16.. of a tile
+constexpr uint32_t kOutOfRange = 0x80000000u;         // buffer offset that loads zeros
+constexpr int kSplitRows = 2560;
+static_assert(BQ == 4 * 64 && BP == 2 * 128, "wave grid 2 x 4 of 128 x 64");
 }  // namespace wgb
+
+// Chunking of a group of m > 0 rows: nc chunks of L rows (the last shorter).
+__device__ __forceinline__ void wg_split(int m, int &L, int &nc) {
+  const int s = (m + wgb::kSplitRows - 1) / wgb::kSplitRows;
+  L = ((m + s - 1) / s + 31) / 32 * 32;
+  nc = (m + L - 1) / L;
+}
 
 __device__ __forceinline__ int wg_key(int row) { return (2 * row) & 15; }
 
@@ -258,10 +283,10 @@ __device__ __forceinline__ u32x2 wg_read_tr(uint32_t lds_byte_addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(lds_byte_addr), "n"(OFF));
   return r;
 }
-__device__ __forceinline__ void wg_wait_tied(u32x2 (&a)[4], u32x2 (&b)[4]) {
+__device__ __forceinline__ void wg_wait_tied(u32x2 (&a)[8]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]),
-                 "+v"(b[2]), "+v"(b[3])
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]),
+                 "+v"(a[6]), "+v"(a[7])
                :
                : "memory");
 }
@@ -269,33 +294,64 @@ __device__ __forceinline__ void wg_wait_tied(u32x2 (&a)[4], u32x2 (&b)[4]) {
 #define PRICHS_WG_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8))
 
 template <bool GATEUP>
-__global__ __launch_bounds__(wg::kThreads) void wgrad_bf16_kernel(
+__global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
     const bf16_t *__restrict__ A, int lda, uint32_t a_bytes, const bf16_t *__restrict__ B,
     int ldb, uint32_t b_bytes, const int32_t *__restrict__ offsets, int G, int E, int P, int Q,
-    int tiles_q, int tiles, float *out0, float *out1, int ldo, long long slot_stride, int f) {
+    int tiles_q, int tiles, float *out0, float *out1, int ldo, long long slot_stride, int f,
+    float *__restrict__ part, int beta) {
   using namespace wgb;
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  int g, tile;
-  if (!wgrad_item(G, tiles, g, tile)) return;
-  const int row_lo = offsets[g];
-  const int mg = offsets[g + 1] - row_lo;
-  if (mg <= 0) return;
+  // Work item of this block: groups in launch order (shared first), each as
+  // its chunks x tiles.  The offsets come to LDS in one parallel load.
+  __shared__ int item[5];  // group (-1: none), first row, end row, partial slot (-1: none), tile
+  __shared__ int offs_s[PRICHS_MAX_EXPERTS + 2];
+  if ((int)threadIdx.x <= G) offs_s[threadIdx.x] = offsets[threadIdx.x];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int rest = (int)blockIdx.x, pslot = 0;
+    item[0] = -1;
+    for (int gi = 0; gi < G; ++gi) {
+      const int g = (gi + G - 1) % G;
+      const int lo = offs_s[g], m = offs_s[g + 1] - lo;
+      if (m <= 0) continue;
+      int L, nc;
+      wg_split(m, L, nc);
+      if (rest < nc * tiles) {
+        const int c = rest / tiles;
+        item[0] = g;
+        item[1] = lo + c * L;
+        item[2] = min(lo + (c + 1) * L, lo + m);
+        item[3] = nc == 1 ? -1 : pslot + c;
+        item[4] = rest - c * tiles;
+        break;
+      }
+      rest -= nc * tiles;
+      if (nc > 1) pslot += nc;
+    }
+  }
+  __syncthreads();
+  const int g = item[0];
+  if (g < 0) return;
+  const int row_lo = item[1];
+  const int mg = item[2] - row_lo;
+  const int pslot = item[3];
+  const int tile = item[4];
   const int tp = tile / tiles_q;
-  const int i0 = tp * wg::BP, j0 = (tile - tp * tiles_q) * wg::BQ;
+  const int i0 = tp * BP, j0 = (tile - tp * tiles_q) * BQ;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int wp = wave >> 1, wq = wave & 1;
+  const int wp = wave >> 2, wq = wave & 3;
   const __amdgpu_buffer_rsrc_t ra = wg_rsrc(A, a_bytes), rb = wg_rsrc(B, b_bytes);
 
-  // DMA: wave w's instruction i fills tile rows 8w + 4i .. + 3; lane l lands
-  // in row 8w + 4i + l/16, physical chunk l % 16, holding logical chunk
-  // (l % 16) ^ key(row).
+  // DMA: wave w's instruction i fills tile rows 4w + 2i, + 1; lane l lands in
+  // row 4w + 2i + l/32, physical chunk l % 32, holding logical chunk
+  // (l % 32) ^ key(row).
   uint32_t a_col[2], b_col[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int R = 8 * wave + 4 * i + (lane >> 4);
-    const int lc = (lane & 15) ^ wg_key(R);
+    const int R = 4 * wave + 2 * i + (lane >> 5);
+    const int lc = (lane & 31) ^ wg_key(R);
     a_col[i] = 2u * (uint32_t)(i0 + lc * 8);
     b_col[i] = 2u * (uint32_t)(j0 + lc * 8);
   }
@@ -304,38 +360,41 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_bf16_kernel(
     bf16_t *sb = sa + kTileBytes / 2;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int rr = kt * BK + 8 * wave + 4 * i + (lane >> 4);
+      const int rr = kt * BK + 4 * wave + 2 * i + (lane >> 5);
       const bool ok = rr < mg;
       const uint32_t row = (uint32_t)(row_lo + rr);
       wg_dma(ra, ok ? row * (uint32_t)lda * 2u + a_col[i] : kOutOfRange,
-             sa + (8 * wave + 4 * i) * 128);
+             sa + (4 * wave + 2 * i) * BP);
       wg_dma(rb, ok ? row * (uint32_t)ldb * 2u + b_col[i] : kOutOfRange,
-             sb + (8 * wave + 4 * i) * 128);
+             sb + (4 * wave + 2 * i) * BP);
     }
   };
 
   // Transposing reads: lane 16g + m reads row 4g + m/4 at column
-  // 16 blk + 4 (m % 4) of the wave's 64 columns.
+  // 16 blk + 4 (m % 4) of the wave's columns (128 of A, 64 of B).
   const uint32_t lds_base = (uint32_t)(size_t)(const __attribute__((address_space(3))) bf16_t *)lds;
-  uint32_t a_rd[4], b_rd[4];
+  uint32_t a_rd[8], b_rd[4];
   {
     const int g4 = lane >> 4, m = lane & 15;
     const int R = 4 * g4 + (m >> 2);
 #pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      const int ca = wp * 128 + blk * 16 + 4 * (m & 3);
+      a_rd[blk] = lds_base + (uint32_t)(R * kRowBytes + (((ca >> 3) ^ wg_key(R)) << 4) + (ca & 7) * 2);
+    }
+#pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
-      const int ca = wp * 64 + blk * 16 + 4 * (m & 3);
       const int cb = wq * 64 + blk * 16 + 4 * (m & 3);
-      a_rd[blk] = lds_base + (uint32_t)(R * 256 + (((ca >> 3) ^ wg_key(R)) << 4) + (ca & 7) * 2);
       b_rd[blk] = lds_base + kTileBytes +
-                  (uint32_t)(R * 256 + (((cb >> 3) ^ wg_key(R)) << 4) + (cb & 7) * 2);
+                  (uint32_t)(R * kRowBytes + (((cb >> 3) ^ wg_key(R)) << 4) + (cb & 7) * 2);
     }
   }
 
-  f32x4 acc[4][4];
+  f32x4 acc[4][8];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = (mg + BK - 1) / BK;
   issue(0);
@@ -358,21 +417,26 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_bf16_kernel(
     asm volatile("" ::: "memory");
     if (kt + 3 < KT) issue(kt + 3);
     const uint32_t st = (uint32_t)(kt & (kStages - 1)) * kStageBytes;
-    u32x2 alo[4], ahi[4], blo[4], bhi[4];
+    u32x2 alo[8], ahi[8], bt[8];  // bt: B lo (0..3) and hi (4..7)
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
+      bt[blk] = wg_read_tr<0>(b_rd[blk] + st);
+      bt[4 + blk] = wg_read_tr<(int)kHiOff>(b_rd[blk] + st);
+    }
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
       alo[blk] = wg_read_tr<0>(a_rd[blk] + st);
       ahi[blk] = wg_read_tr<(int)kHiOff>(a_rd[blk] + st);
-      blo[blk] = wg_read_tr<0>(b_rd[blk] + st);
-      bhi[blk] = wg_read_tr<(int)kHiOff>(b_rd[blk] + st);
     }
-    wg_wait_tied(alo, ahi);
-    wg_wait_tied(blo, bhi);
+    wg_wait_tied(bt);
+    wg_wait_tied(alo);
+    wg_wait_tied(ahi);
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
-      const bf16x8 bf = __builtin_bit_cast(bf16x8, u32x4{blo[jb][0], blo[jb][1], bhi[jb][0], bhi[jb][1]});
+      const bf16x8 bf =
+          __builtin_bit_cast(bf16x8, u32x4{bt[jb][0], bt[jb][1], bt[4 + jb][0], bt[4 + jb][1]});
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
+      for (int ib = 0; ib < 8; ++ib) {
         const bf16x8 af =
             __builtin_bit_cast(bf16x8, u32x4{alo[ib][0], alo[ib][1], ahi[ib][0], ahi[ib][1]});
         acc[jb][ib] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, af, acc[jb][ib], 0, 0, 0);
@@ -380,24 +444,128 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_bf16_kernel(
     }
   }
 
-  // acc[jb][ib] lane l holds out[i = 16 ib + l % 16][j = 16 jb + 4 (l / 16) + r].
+  // acc[jb][ib] lane l holds out[i = 16 ib + l % 16][j = 16 jb + 4 (l / 16) + r]
+  // of the wave's 128 x 64 block.
   const long long base = (long long)slot_of(g, E) * slot_stride;
+  if (pslot >= 0 || beta == 0) {
+    // Stores only: a chunk partial, or the gradient itself when beta = 0.
+    float *pbase = pslot >= 0 ? part + (long long)pslot * P * Q : nullptr;
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
+    for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      const int i = i0 + wp * 64 + ib * 16 + (lane & 15);
+      for (int ib = 0; ib < 8; ++ib) {
+        const int i = i0 + wp * 128 + ib * 16 + (lane & 15);
+        const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
+        const f32x4 a = acc[jb][ib];
+        float *dst = pbase != nullptr ? (i < P && j < Q ? pbase + (long long)i * Q + j : nullptr)
+                                      : wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
+        if (dst) *reinterpret_cast<float4 *>(dst) = make_float4(a[0], a[1], a[2], a[3]);
+      }
+    return;
+  }
+  // Read-modify-write in batches of 8: all loads of a batch are issued before
+  // its stores (a load cannot move past a store that may alias it).
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    float *dst[8];
+    float4 old[8];
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+      const int i = i0 + wp * 128 + ib * 16 + (lane & 15);
       const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
-      float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
-      if (dst) {
-        float4 v = *reinterpret_cast<float4 *>(dst);
-        v.x = v.x + acc[jb][ib][0];
-        v.y = v.y + acc[jb][ib][1];
-        v.z = v.z + acc[jb][ib][2];
-        v.w = v.w + acc[jb][ib][3];
-        *reinterpret_cast<float4 *>(dst) = v;
+      dst[ib] = wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
+      old[ib] = dst[ib] ? *reinterpret_cast<const float4 *>(dst[ib]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+      const f32x4 a = acc[jb][ib];
+      if (dst[ib]) {
+        float4 v = old[ib];
+        v.x = v.x + a[0];
+        v.y = v.y + a[1];
+        v.z = v.z + a[2];
+        v.w = v.w + a[3];
+        *reinterpret_cast<float4 *>(dst[ib]) = v;
       }
     }
+  }
+}
+
+// Finishes the groups the tile kernel does not write whole: a split group
+// gets its partials in chunk order, dW = beta dW + (((p0 + p1) + p2) + ...);
+// with beta = 0 a group without rows gets zeros.  (split = 0: the f32 kernel,
+// which splits nothing.)  Grid-stride over those groups' P x Q elements, 4 at
+// a time.
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restrict__ part,
+                                                           const int32_t *__restrict__ offsets,
+                                                           int G, int E, int P, int Q, float *out0,
+                                                           float *out1, int ldo,
+                                                           long long slot_stride, int f, int beta,
+                                                           int split) {
+  __shared__ int sg[PRICHS_MAX_EXPERTS + 1], snc[PRICHS_MAX_EXPERTS + 1],
+      sps[PRICHS_MAX_EXPERTS + 1];
+  __shared__ int n_split;
+  if (threadIdx.x == 0) {
+    int pslot = 0, n = 0;
+    for (int gi = 0; gi < G; ++gi) {
+      const int g = (gi + G - 1) % G;
+      const int m = offsets[g + 1] - offsets[g];
+      if (m <= 0) {
+        if (beta == 0) {  // nc = 0: written as zeros
+          sg[n] = g;
+          snc[n] = 0;
+          sps[n] = 0;
+          ++n;
+        }
+        continue;
+      }
+      if (!split) continue;
+      int L, nc;
+      wg_split(m, L, nc);
+      if (nc > 1) {
+        sg[n] = g;
+        snc[n] = nc;
+        sps[n] = pslot;
+        ++n;
+        pslot += nc;
+      }
+    }
+    n_split = n;
+  }
+  __syncthreads();
+  const long long per = (long long)P * Q / 4;
+  const long long total = per * n_split;
+  const long long PQ = (long long)P * Q;
+  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total;
+       e += (long long)gridDim.x * 256) {
+    const int s = (int)(e / per);
+    const long long q4 = (e - s * per) * 4;
+    const int i = (int)(q4 / Q), j = (int)(q4 - (long long)i * Q);
+    float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, (long long)slot_of(sg[s], E) * slot_stride,
+                                   i, j, P, Q, f);
+    if (dst == nullptr) continue;
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (snc[s] > 0) {
+      const float *p = part + (long long)sps[s] * PQ + q4;
+      sum = *reinterpret_cast<const float4 *>(p);
+      for (int c = 1; c < snc[s]; ++c) {
+        const float4 v = *reinterpret_cast<const float4 *>(p + (long long)c * PQ);
+        sum.x = sum.x + v.x;
+        sum.y = sum.y + v.y;
+        sum.z = sum.z + v.z;
+        sum.w = sum.w + v.w;
+      }
+    }
+    if (beta != 0) {
+      const float4 d = *reinterpret_cast<const float4 *>(dst);
+      sum.x = d.x + sum.x;
+      sum.y = d.y + sum.y;
+      sum.z = d.z + sum.z;
+      sum.w = d.w + sum.w;
+    }
+    *reinterpret_cast<float4 *>(dst) = sum;
+  }
 }
 
 // --- f32 (the fp32-checked mode): v_mfma_f32_16x16x4_f32, K-steps of 16 rows
@@ -414,7 +582,7 @@ template <bool GATEUP>
 __global__ __launch_bounds__(wg::kThreads) void wgrad_f32_kernel(
     const float *__restrict__ A, int lda, const float *__restrict__ B, int ldb,
     const int32_t *__restrict__ offsets, int G, int E, int P, int Q, int tiles_q, int tiles,
-    float *out0, float *out1, int ldo, long long slot_stride, int f) {
+    float *out0, float *out1, int ldo, long long slot_stride, int f, int beta) {
   using namespace wgf;
   extern __shared__ __attribute__((aligned(16))) float ldsw[];
   int g, tile;
@@ -503,11 +671,14 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_f32_kernel(
       const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
       float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
       if (dst) {
-        float4 v = *reinterpret_cast<float4 *>(dst);
-        v.x = v.x + acc[jb][ib][0];
-        v.y = v.y + acc[jb][ib][1];
-        v.z = v.z + acc[jb][ib][2];
-        v.w = v.w + acc[jb][ib][3];
+        float4 v = make_float4(acc[jb][ib][0], acc[jb][ib][1], acc[jb][ib][2], acc[jb][ib][3]);
+        if (beta != 0) {
+          const float4 o = *reinterpret_cast<const float4 *>(dst);
+          v.x = o.x + v.x;
+          v.y = o.y + v.y;
+          v.z = o.z + v.z;
+          v.w = o.w + v.w;
+        }
         *reinterpret_cast<float4 *>(dst) = v;
       }
     }
@@ -679,7 +850,7 @@ __global__ __launch_bounds__(256) void router_wgrad_part_kernel(const T *__restr
 
 __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(const float *__restrict__ part,
                                                                   const int32_t *__restrict__ offsets,
-                                                                  int E, int d,
+                                                                  int E, int d, int beta,
                                                                   float *__restrict__ dw) {
 #pragma clang fp contract(off)
   const int i = blockIdx.x * 256 + threadIdx.x;
@@ -698,10 +869,31 @@ __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(const float *_
 #pragma unroll
     for (int u = 0; u < 8; ++u) s = s + v[u];
   }
-  dw[i] = dw[i] + s;
+  dw[i] = beta != 0 ? dw[i] + s : s;
 }
 
 unsigned blocks_for(long long n, int per = 256) { return (unsigned)((n + per - 1) / per); }
+
+// Zeros of every gradient (beta = 0 with no rows): d_router [n_router], and
+// per slot s < G the three [n_mat] matrices at slot_stride * s.
+__global__ __launch_bounds__(256) void zero_grads_kernel(float *d_router, long long n_router,
+                                                         float *d_gate, float *d_up, float *d_down,
+                                                         long long slot_stride, int G,
+                                                         long long n_mat) {
+  const long long total = n_router + 3LL * G * n_mat;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (long long)gridDim.x * 256) {
+    if (i < n_router) {
+      d_router[i] = 0.f;
+      continue;
+    }
+    const long long r = i - n_router;
+    const long long which = r / (G * n_mat), q = r - which * G * n_mat;
+    const long long slot = q / n_mat, e = q - slot * n_mat;
+    float *m = which == 0 ? d_gate : which == 1 ? d_up : d_down;
+    m[slot * slot_stride + e] = 0.f;
+  }
+}
 
 }  // namespace
 
@@ -743,18 +935,30 @@ int bwd_swiglu(void *gu, const void *da, size_t rows, size_t f, size_t np, int d
   return PRICHS_OK;
 }
 
+// A split group has m > kSplitRows rows and at most ceil(m / kSplitRows) <=
+// 2 floor(m / kSplitRows) chunks, so all split groups together hold at most
+// 2 floor(rows / kSplitRows) chunk partials.
+size_t bwd_wgrad_part_elems(size_t max_rows, size_t P, size_t Q) {
+  return 2 * (max_rows / wgb::kSplitRows) * P * Q;
+}
+
 int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb, size_t total_rows,
               const int32_t *offsets, size_t G, size_t E, size_t P, size_t Q, float *out0,
-              float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, hipStream_t s) {
-  const int tiles_q = (int)cdiv(Q, wg::BQ);
-  const int tiles = (int)cdiv(P, wg::BP) * tiles_q;
-  const unsigned grid = (unsigned)(8 * cdiv((size_t)tiles, 8) * G);
-  if (grid == 0) return PRICHS_OK;
+              float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, float *part,
+              int beta, hipStream_t s) {
+  if (total_rows == 0) return PRICHS_OK;
+  const int cus = device_cu_count();
+  const unsigned rgrid = (unsigned)std::max(1, 4 * cus);
   if (dtype == PRICHS_DTYPE_BF16) {
+    const int tiles_q = (int)cdiv(Q, wgb::BQ);
+    const int tiles = (int)cdiv(P, wgb::BP) * tiles_q;
+    // Every group's chunks: at most G + total_rows / kSplitRows per tile.
+    const size_t items = (G + total_rows / wgb::kSplitRows) * (size_t)tiles;
     const size_t ab = total_rows * lda * 2, bb = total_rows * ldb * 2;
     if (ab >= wgb::kOutOfRange || bb >= wgb::kOutOfRange)
       return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: operands of %zu and %zu bytes exceed 2 GiB",
                   ab, bb);
+    if (items > (size_t)INT32_MAX) return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: too many tiles");
     auto kern = gateup ? wgrad_bf16_kernel<true> : wgrad_bf16_kernel<false>;
     static bool attr_set[2] = {false, false};
     if (!attr_set[gateup]) {
@@ -764,19 +968,36 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
                      "moe backward: set LDS size");
       attr_set[gateup] = true;
     }
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(wg::kThreads), wgb::kLdsBytes, s,
+    hipLaunchKernelGGL(kern, dim3((unsigned)items), dim3(wgb::kThreads), wgb::kLdsBytes, s,
                        static_cast<const bf16_t *>(A), (int)lda, (uint32_t)ab,
                        static_cast<const bf16_t *>(B), (int)ldb, (uint32_t)bb, offsets, (int)G,
                        (int)E, (int)P, (int)Q, tiles_q, tiles, out0, out1, (int)ldo,
-                       (long long)slot_stride, (int)f);
-  } else {
-    auto kern = gateup ? wgrad_f32_kernel<true> : wgrad_f32_kernel<false>;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(wg::kThreads), wgf::kLdsBytes, s,
-                       static_cast<const float *>(A), (int)lda, static_cast<const float *>(B),
-                       (int)ldb, offsets, (int)G, (int)E, (int)P, (int)Q, tiles_q, tiles, out0,
-                       out1, (int)ldo, (long long)slot_stride, (int)f);
+                       (long long)slot_stride, (int)f, part, beta);
+    PRICHS_LAUNCH_CHECK("moe backward: weight gradient");
+    // Some group may have been split, or (beta = 0) may have no rows.
+    if (total_rows > (size_t)wgb::kSplitRows || beta == 0) {
+      auto rk = gateup ? wgrad_reduce_kernel<true> : wgrad_reduce_kernel<false>;
+      hipLaunchKernelGGL(rk, dim3(rgrid), dim3(256), 0, s, part, offsets, (int)G, (int)E, (int)P,
+                         (int)Q, out0, out1, (int)ldo, (long long)slot_stride, (int)f, beta, 1);
+      PRICHS_LAUNCH_CHECK("moe backward: weight gradient partials");
+    }
+    return PRICHS_OK;
   }
+  const int tiles_q = (int)cdiv(Q, wg::BQ);
+  const int tiles = (int)cdiv(P, wg::BP) * tiles_q;
+  const unsigned grid = (unsigned)(8 * cdiv((size_t)tiles, 8) * G);
+  auto kern = gateup ? wgrad_f32_kernel<true> : wgrad_f32_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(wg::kThreads), wgf::kLdsBytes, s,
+                     static_cast<const float *>(A), (int)lda, static_cast<const float *>(B),
+                     (int)ldb, offsets, (int)G, (int)E, (int)P, (int)Q, tiles_q, tiles, out0,
+                     out1, (int)ldo, (long long)slot_stride, (int)f, beta);
   PRICHS_LAUNCH_CHECK("moe backward: weight gradient");
+  if (beta == 0) {  // zeros for groups without rows
+    auto rk = gateup ? wgrad_reduce_kernel<true> : wgrad_reduce_kernel<false>;
+    hipLaunchKernelGGL(rk, dim3(rgrid), dim3(256), 0, s, nullptr, offsets, (int)G, (int)E, (int)P,
+                       (int)Q, out0, out1, (int)ldo, (long long)slot_stride, (int)f, 0, 0);
+    PRICHS_LAUNCH_CHECK("moe backward: weight gradient zeros");
+  }
   return PRICHS_OK;
 }
 
@@ -805,12 +1026,23 @@ int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, cons
   return PRICHS_OK;
 }
 
+int bwd_zero_grads(float *d_router, size_t n_router, float *d_gate, float *d_up, float *d_down,
+                   size_t slot_stride, size_t G, size_t n_mat, hipStream_t s) {
+  const int cus = device_cu_count();
+  hipLaunchKernelGGL(zero_grads_kernel, dim3((unsigned)std::max(1, 4 * cus)), dim3(256), 0, s,
+                     d_router, (long long)n_router, d_gate, d_up, d_down, (long long)slot_stride,
+                     (int)G, (long long)n_mat);
+  PRICHS_LAUNCH_CHECK("moe backward: zero gradients");
+  return PRICHS_OK;
+}
+
 size_t bwd_router_part_elems(size_t max_tokens, size_t k, size_t d, size_t E) {
   return (cdiv(max_tokens * k, kRouterChunk) + E) * d;
 }
 
 int bwd_router_wgrad(const void *xg, const float *dlr, const int32_t *offsets, size_t T, size_t k,
-                     size_t d, size_t E, int dtype, float *part, float *dw, hipStream_t s) {
+                     size_t d, size_t E, int dtype, float *part, float *dw, int beta,
+                     hipStream_t s) {
   if (T == 0) return PRICHS_OK;
   // Every group's chunks fit in cdiv(T*k, chunk) + E workgroups; the rest exit.
   const unsigned grid = (unsigned)(cdiv(T * k, kRouterChunk) + E);
@@ -822,7 +1054,7 @@ int bwd_router_wgrad(const void *xg, const float *dlr, const int32_t *offsets, s
                        static_cast<const float *>(xg), dlr, offsets, (int)E, (int)d, part);
   PRICHS_LAUNCH_CHECK("moe backward: router weight gradient");
   hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3(blocks_for((long long)(d * E))), dim3(256),
-                     0, s, part, offsets, (int)E, (int)d, dw);
+                     0, s, part, offsets, (int)E, (int)d, beta, dw);
   PRICHS_LAUNCH_CHECK("moe backward: router weight gradient reduce");
   return PRICHS_OK;
 }

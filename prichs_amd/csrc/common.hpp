@@ -138,15 +138,21 @@ int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *row
              void *dy, void *xg, float *scal, hipStream_t s);
 int bwd_swiglu(void *gu, const void *da, size_t rows, size_t f, size_t np, int dtype,
                hipStream_t s);
+// part: bf16 split-K partials, bwd_wgrad_part_elems(rows, P, Q) floats.
+size_t bwd_wgrad_part_elems(size_t max_rows, size_t P, size_t Q);
 int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb, size_t total_rows,
               const int32_t *offsets, size_t G, size_t E, size_t P, size_t Q, float *out0,
-              float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, hipStream_t s);
+              float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, float *part,
+              int beta, hipStream_t s);
 int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, const float *topk_w,
                 const int32_t *token_row, const float *wrt, size_t T, size_t d, size_t k,
                 int weighting, int dtype, float *dlr, void *d_x, int dx_dtype, hipStream_t s);
+int bwd_zero_grads(float *d_router, size_t n_router, float *d_gate, float *d_up, float *d_down,
+                   size_t slot_stride, size_t G, size_t n_mat, hipStream_t s);
 size_t bwd_router_part_elems(size_t max_tokens, size_t k, size_t d, size_t E);
 int bwd_router_wgrad(const void *xg, const float *dlr, const int32_t *offsets, size_t T, size_t k,
-                     size_t d, size_t E, int dtype, float *part, float *dw, hipStream_t s);
+                     size_t d, size_t E, int dtype, float *part, float *dw, int beta,
+                     hipStream_t s);
 
 // Checkpoint reading shared by the engines' upload-from-checkpoint entry
 // points: parameter `index` must hold exactly `want` floats (`what` and

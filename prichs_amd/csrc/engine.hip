@@ -62,6 +62,7 @@ struct prichs_moe_engine {
   float *dlr = nullptr;      // [max_tokens * k] d_logit of each routed row
   float *wrt = nullptr;      // [E, d] router weights transposed
   float *rpart = nullptr;    // router weight-gradient partial sums
+  float *wpart = nullptr;    // weight-gradient split-K partials
 
   // Stage timing: `slots` sets of PRICHS_NUM_STAGES events, filled in turn
   // by timed forwards (created by set_timing, never inside forward).
@@ -459,6 +460,8 @@ extern "C" int prichs_moe_engine_enable_backward(prichs_moe_engine *eng) {
   const size_t o_dl = c.take(sizeof(float) * Tm * eng->k);
   const size_t o_wrt = c.take(sizeof(float) * E * d);
   const size_t o_rp = c.take(sizeof(float) * bwd_router_part_elems(Tm, eng->k, d, E));
+  const size_t o_wp =
+      c.take(sizeof(float) * std::max(bwd_wgrad_part_elems(rows, d, np), bwd_wgrad_part_elems(rows, f, d)));
   DeviceGuard g(eng->device);
   if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_enable_backward: cannot select device");
   hipError_t e = hipMalloc(&eng->bwd_arena, c.off);
@@ -477,6 +480,7 @@ extern "C" int prichs_moe_engine_enable_backward(prichs_moe_engine *eng) {
   eng->dlr = reinterpret_cast<float *>(base + o_dl);
   eng->wrt = reinterpret_cast<float *>(base + o_wrt);
   eng->rpart = reinterpret_cast<float *>(base + o_rp);
+  eng->wpart = reinterpret_cast<float *>(base + o_wp);
   eng->bwd = true;
   return PRICHS_OK;
 }
@@ -509,9 +513,16 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   PRICHS_REQUIRE(aligned16(grads->d_router) && aligned16(grads->d_gate) &&
                      aligned16(grads->d_up) && aligned16(grads->d_down),
                  "engine_backward: gradient buffers must be 16-byte aligned");
+  PRICHS_REQUIRE(grads->beta == 0 || grads->beta == 1,
+                 "engine_backward: beta=%d (1 = add to the gradients, 0 = overwrite them)",
+                 grads->beta);
   if (T == 0) {
     eng->stash_valid = false;
-    return PRICHS_OK;
+    if (grads->beta != 0) return PRICHS_OK;
+    DeviceGuard g(eng->device);
+    if (!g.ok) return fail(PRICHS_ERR_HIP, "engine_backward: cannot select device");
+    return bwd_zero_grads(grads->d_router, d * E, grads->d_gate, grads->d_up, grads->d_down,
+                          grads->slot_stride, G, d * f, as_stream(stream));
   }
   PRICHS_REQUIRE(x && d_out && d_x, "engine_backward: null pointer argument");
   PRICHS_REQUIRE(aligned16(x) && aligned16(d_out) && aligned16(d_x),
@@ -537,7 +548,7 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   if (rc) return rc;
   PRICHS_BWD_MARK(2);
   rc = bwd_wgrad(false, eng->act, f, eng->dy, d, rows, eng->offsets, G, E, f, d, grads->d_down,
-                 nullptr, d, grads->slot_stride, f, dt, s);
+                 nullptr, d, grads->slot_stride, f, dt, eng->wpart, grads->beta, s);
   if (rc) return rc;
   PRICHS_BWD_MARK(3);
   rc = grouped_gemm_rows(eng->dy, nullptr, d, eng->w_down_t, eng->dt_elems, np_f, d, eng->act, f,
@@ -548,7 +559,7 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   if (rc) return rc;
   PRICHS_BWD_MARK(5);
   rc = bwd_wgrad(true, eng->xg, d, eng->gu, np, rows, eng->offsets, G, E, d, np, grads->d_gate,
-                 grads->d_up, f, grads->slot_stride, f, dt, s);
+                 grads->d_up, f, grads->slot_stride, f, dt, eng->wpart, grads->beta, s);
   if (rc) return rc;
   PRICHS_BWD_MARK(6);
   rc = grouped_gemm_rows(eng->gu, nullptr, np, eng->w_cat, eng->cat_elems, np_d, np, eng->dy, d, d,
@@ -560,7 +571,7 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   if (rc) return rc;
   PRICHS_BWD_MARK(8);
   rc = bwd_router_wgrad(eng->xg, eng->dlr, eng->offsets, T, k, d, E, dt, eng->rpart,
-                        grads->d_router, s);
+                        grads->d_router, grads->beta, s);
   if (rc) return rc;
   PRICHS_BWD_MARK(9);
 #undef PRICHS_BWD_MARK

@@ -126,13 +126,14 @@ class MoEEngine:
 
     def backward(self, x: torch.Tensor, d_out: torch.Tensor, grads: dict,
                  dx_weighting: int = 2, d_x: torch.Tensor | None = None, d_x_dtype=None,
-                 stream=None) -> torch.Tensor:
+                 stream=None, beta: int = 1) -> torch.Tensor:
         """prichs_moe_engine_backward after the forward of the same x.
 
-        grads: device f32 tensors added to in place -- "d_router" [d, E] and
+        grads: device f32 tensors updated in place -- "d_router" [d, E] and
         "d_gate", "d_up" [G, d, f], "d_down" [G, f, d] (G = 1 + E, the shared
         expert first), or a "flat" [G, 3, d*f] buffer in the reference's
-        parameter order (gate, up, down of each slot).  Returns d_x [T, d]."""
+        parameter order (gate, up, down of each slot).  beta = 1 adds the
+        gradients to them, beta = 0 overwrites them.  Returns d_x [T, d]."""
         for t in (x, d_out):
             if ops.dtype_code(t) != self.dtype:
                 raise TypeError("x and d_out must have the engine dtype")
@@ -155,6 +156,7 @@ class MoEEngine:
         else:
             g.d_gate, g.d_up, g.d_down = (ptr(grads[k]) for k in ("d_gate", "d_up", "d_down"))
             g.slot_stride = df
+        g.beta = int(beta)
         L.check(self.lib.prichs_moe_engine_backward(
             self.handle, ops._p(ops._dev(x)), ops._p(ops._dev(d_out)), T, ops._p(d_x),
             ops.dtype_code(d_x), C.byref(g), int(dx_weighting), ops._stream(stream)))

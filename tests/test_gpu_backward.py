@@ -100,9 +100,10 @@ def test_backward_f32_matches_oracle(cuda, orc, T, d, f, E, k, weighting):
 
 # ------------------------------------------------------------- bf16 engine --
 # Config-1 shapes in bf16, a padded f (192: packed columns 384..511 are
-# padding), and a decode-sized batch whose groups take the skinny GEMM.
+# padding), a decode-sized batch whose groups take the skinny GEMM, and a
+# batch whose shared group (3000 rows) the weight-gradient kernels split over K.
 @pytest.mark.parametrize("T,d,f,E,k", [(512, 256, 128, 8, 2), (300, 128, 192, 8, 2),
-                                       (32, 256, 128, 8, 2)])
+                                       (32, 256, 128, 8, 2), (3000, 256, 128, 4, 2)])
 @pytest.mark.parametrize("weighting", [1, 2])
 def test_backward_bf16_matches_oracle(cuda, orc, T, d, f, E, k, weighting):
     say("bf16 backward", T, d, f, E, k, "weighting", weighting)
@@ -112,20 +113,28 @@ def test_backward_bf16_matches_oracle(cuda, orc, T, d, f, E, k, weighting):
     check_against_oracle(orc, inp, d_out, weighting, d_x, grads, TOL["bf16"])
 
 
-def test_backward_skewed_routing(cuda, orc):
+@pytest.mark.parametrize("T", [400, 6000])
+def test_backward_skewed_routing(cuda, orc, T):
     # Config-3 style bias: experts 0-1 take most rows, some experts may get none.
-    say("bf16 backward, skewed routing")
-    inp = synth.make_moe_inputs(400, 128, 128, E=8, k=2, dtype="bf16", bias_std=None,
-                                skew_beta=0.5, w_std=0.1, seed=4)
-    d_out = synth.round_bf16(np.random.default_rng(4).standard_normal((400, 128)).astype(np.float32))
+    # At T = 6000 the hot experts' groups (and the shared one) exceed the
+    # weight-gradient kernels' split size, so they are summed from K chunks.
+    say("bf16 backward, skewed routing", T)
+    inp = synth.make_moe_inputs(T, 128, 128, E=8, k=2, dtype="bf16", bias_std=None,
+                                skew_beta=0.5 if T < 1000 else 1.5, w_std=0.1, seed=4)
+    d_out = synth.round_bf16(np.random.default_rng(4).standard_normal((T, 128)).astype(np.float32))
     eng = make_engine(inp)
     d_x, grads = run(eng, inp, d_out, 2)
+    counts = np.bincount(eng.stash()["selected_experts"].cpu().numpy().ravel(), minlength=8)
+    say("  rows per routed expert", counts.tolist())
+    if T == 6000:
+        assert counts.max() > 2560
     check_against_oracle(orc, inp, d_out, 2, d_x, grads, TOL["bf16"])
 
 
 # --------------------------------------------------------- host semantics --
-def test_backward_deterministic_accumulating_and_flat_layout(cuda):
-    inp, d_out = inputs(512, 256, 128, 8, 2, "bf16", seed=21)
+@pytest.mark.parametrize("T", [512, 3000])
+def test_backward_deterministic_accumulating_and_flat_layout(cuda, T):
+    inp, d_out = inputs(T, 256, 128, 8, 2, "bf16", seed=21)
     eng = make_engine(inp)
     say("determinism")
     dx1, g1 = run(eng, inp, d_out, 2)
@@ -264,3 +273,52 @@ def test_backward_stage_timing(cuda):
     assert abs(parts - ms["total"]) <= 0.05 * ms["total"] + 1e-3
     with pytest.raises(L.PrichsError, match="no timed backward"):
         eng.backward_stage_ms()
+
+
+@pytest.mark.parametrize("T,dtype", [(512, "bf16"), (3000, "bf16"), (200, "f32")])
+def test_backward_beta0_overwrites(cuda, T, dtype):
+    # beta = 0 is zero_grads (engine.rs:710-720) followed by the backward: on
+    # NaN-filled buffers it must write every element, experts without rows
+    # included, and equal beta = 1 on zeroed buffers.  T = 3000 splits the
+    # shared group's weight gradients over K.
+    say("beta 0", T, dtype)
+    inp, d_out = inputs(T, 256, 128, 8, 2, dtype, seed=31)
+    inp.router_bias[7] = -1e4  # no token selects expert 7
+    eng = make_engine(inp)
+    x, go = dev(inp.x, dtype), dev(d_out, dtype)
+    eng.forward(x)
+    assert int((eng.stash()["selected_experts"] == 7).sum()) == 0
+    ref = zero_grads(inp)
+    dx1 = eng.backward(x, go, ref, d_x_dtype=torch.float32, beta=1)
+    for layout in ("separate", "flat"):
+        G, d, f = 1 + inp.E, inp.d, inp.f
+        if layout == "separate":
+            got = {k: torch.full_like(v, float("nan")) for k, v in ref.items()}
+        else:
+            got = {"d_router": torch.full_like(ref["d_router"], float("nan")),
+                   "flat": torch.full((G, 3, d * f), float("nan"), device="cuda")}
+        eng.forward(x)
+        dx0 = eng.backward(x, go, got, d_x_dtype=torch.float32, beta=0)
+        assert torch.equal(dx0, dx1)
+        if layout == "flat":
+            fl = got["flat"]
+            got = {"d_router": got["d_router"], "d_gate": fl[:, 0].reshape(G, d, f),
+                   "d_up": fl[:, 1].reshape(G, d, f), "d_down": fl[:, 2].reshape(G, f, d)}
+        for key in ref:
+            assert torch.equal(got[key], ref[key]), (layout, key)
+        assert not got["d_gate"][8].any() and not got["d_down"][8].any()  # slot 8 = expert 7
+
+
+def test_backward_empty_batch(cuda):
+    inp, _ = inputs(64, 128, 128, 4, 2, "bf16", seed=2)
+    eng = make_engine(inp)
+    x = dev(inp.x, "bf16")[:0]
+    g1 = {k: torch.ones_like(v) for k, v in zero_grads(inp).items()}
+    eng.forward(x)
+    eng.backward(x, x, g1, beta=1)
+    assert all(bool((v == 1).all()) for v in g1.values())
+    g0 = {k: torch.full_like(v, float("nan")) for k, v in zero_grads(inp).items()}
+    eng.forward(x)
+    eng.backward(x, x, g0, beta=0)
+    torch.cuda.synchronize()
+    assert all(not v.any() for v in g0.values())
