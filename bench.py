@@ -41,6 +41,32 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (Linux /proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def one_thread(run, n: int, unit_tokens: int):
+    """run(n) on one oracle thread (the rest of the baseline uses all of them)."""
+    from oracle import oracle
+
+    cores = oracle.num_threads()
+    oracle.set_num_threads(1)
+    try:
+        t = run(n)
+    finally:
+        oracle.set_num_threads(cores)
+    return {"value": unit_tokens / t, "unit": "tokens/s", "cores": 1,
+            "sample": f"first {n} tokens, {t:.2f} s"}
+
+
 def cpu_baseline(inp, target_s: float):
     """Times the CPU oracle on a token sample sized to about target_s seconds."""
     import numpy as np
@@ -68,6 +94,8 @@ def cpu_baseline(inp, target_s: float):
                   f"(reference CPU algorithm: naive k-outer f32 GEMM, serial gating/binning/"
                   f"scatter), OpenMP over rows on {cores} threads, {t:.1f} s",
         "seconds": t,
+        "cpu_model": cpu_model(),
+        "one_thread": one_thread(run, n0, n0),
     }
 
 
@@ -237,6 +265,8 @@ def cpu_baseline_train(inp, d_out, target_s: float):
                   f"+ backward (reference CPU algorithm, f32, naive GEMMs), OpenMP over rows on "
                   f"{cores} threads, {t:.1f} s",
         "seconds": t,
+        "cpu_model": cpu_model(),
+        "one_thread": one_thread(run, n0, n0),
     }
 
 
@@ -521,6 +551,8 @@ def cpu_baseline_block(inp, target_s: float):
                   f"forward (RMSNorm, f32 projections, causal GQA attention with RoPE, MoE, "
                   f"residuals), OpenMP over rows on {cores} threads, {t:.1f} s{note}",
         "seconds": t,
+        "cpu_model": cpu_model(),
+        "one_thread": one_thread(run, 64, 64),
     }
 
 

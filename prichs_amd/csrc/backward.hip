@@ -494,8 +494,7 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
 // Finishes the groups the tile kernel does not write whole: a split group
 // gets its partials in chunk order, dW = beta dW + (((p0 + p1) + p2) + ...);
 // with beta = 0 a group without rows gets zeros.  (split = 0: the f32 kernel,
-// which splits nothing.)  Grid-stride over those groups' P x Q elements, 4 at
-// a time.
+// which splits nothing.)
 template <bool GATEUP>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restrict__ part,
                                                            const int32_t *__restrict__ offsets,
@@ -506,11 +505,14 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restri
   __shared__ int sg[PRICHS_MAX_EXPERTS + 1], snc[PRICHS_MAX_EXPERTS + 1],
       sps[PRICHS_MAX_EXPERTS + 1];
   __shared__ int n_split;
+  __shared__ int offs_s[PRICHS_MAX_EXPERTS + 2];
+  if ((int)threadIdx.x <= G) offs_s[threadIdx.x] = offsets[threadIdx.x];
+  __syncthreads();
   if (threadIdx.x == 0) {
     int pslot = 0, n = 0;
     for (int gi = 0; gi < G; ++gi) {
       const int g = (gi + G - 1) % G;
-      const int m = offsets[g + 1] - offsets[g];
+      const int m = offs_s[g + 1] - offs_s[g];
       if (m <= 0) {
         if (beta == 0) {  // nc = 0: written as zeros
           sg[n] = g;
@@ -534,37 +536,49 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restri
     n_split = n;
   }
   __syncthreads();
-  const long long per = (long long)P * Q / 4;
-  const long long total = per * n_split;
+  // One (group, row) pair per workgroup step; threads walk the row's Q
+  // columns 4 at a time (no division per element).
   const long long PQ = (long long)P * Q;
-  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total;
-       e += (long long)gridDim.x * 256) {
-    const int s = (int)(e / per);
-    const long long q4 = (e - s * per) * 4;
-    const int i = (int)(q4 / Q), j = (int)(q4 - (long long)i * Q);
-    float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, (long long)slot_of(sg[s], E) * slot_stride,
-                                   i, j, P, Q, f);
-    if (dst == nullptr) continue;
-    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (snc[s] > 0) {
-      const float *p = part + (long long)sps[s] * PQ + q4;
-      sum = *reinterpret_cast<const float4 *>(p);
-      for (int c = 1; c < snc[s]; ++c) {
-        const float4 v = *reinterpret_cast<const float4 *>(p + (long long)c * PQ);
-        sum.x = sum.x + v.x;
-        sum.y = sum.y + v.y;
-        sum.z = sum.z + v.z;
-        sum.w = sum.w + v.w;
+  const int q4n = Q / 4;
+  for (int idx = blockIdx.x; idx < n_split * P; idx += gridDim.x) {
+    const int s = idx / P, i = idx - s * P;
+    const long long gbase = (long long)slot_of(sg[s], E) * slot_stride;
+    const float *prow = part + (long long)sps[s] * PQ + (long long)i * Q;
+    for (int c4 = threadIdx.x; c4 < q4n; c4 += 256) {
+      const int j = 4 * c4;
+      float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, gbase, i, j, P, Q, f);
+      if (dst == nullptr) continue;
+      // Chunk loads in batches of 8 issued together (a runtime-length loop
+      // would wait for each load before the next); added in chunk order.
+      const int nc = snc[s];
+      float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int c0 = 0; c0 < nc; c0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          v[u] = *reinterpret_cast<const float4 *>(prow + (long long)min(c0 + u, nc - 1) * PQ + j);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (c0 + u >= nc) break;
+          if (c0 + u == 0) {
+            sum = v[u];
+          } else {
+            sum.x = sum.x + v[u].x;
+            sum.y = sum.y + v[u].y;
+            sum.z = sum.z + v[u].z;
+            sum.w = sum.w + v[u].w;
+          }
+        }
       }
+      if (beta != 0) {
+        const float4 d = *reinterpret_cast<const float4 *>(dst);
+        sum.x = d.x + sum.x;
+        sum.y = d.y + sum.y;
+        sum.z = d.z + sum.z;
+        sum.w = d.w + sum.w;
+      }
+      *reinterpret_cast<float4 *>(dst) = sum;
     }
-    if (beta != 0) {
-      const float4 d = *reinterpret_cast<const float4 *>(dst);
-      sum.x = d.x + sum.x;
-      sum.y = d.y + sum.y;
-      sum.z = d.z + sum.z;
-      sum.w = d.w + sum.w;
-    }
-    *reinterpret_cast<float4 *>(dst) = sum;
   }
 }
 
@@ -799,8 +813,8 @@ __global__ __launch_bounds__(256) void combine_kernel(
 constexpr int kRouterChunk = 64;
 constexpr int kRouterUnroll = 8;  // rows whose loads are in flight together
 
-// Group and row range of chunk `ch` (-1 past the last chunk).
-__device__ inline int router_chunk(const int32_t *offsets, int E, int ch, int &r0, int &r1) {
+// Group and row range of chunk `ch` (-1 past the last chunk); offsets in LDS.
+__device__ inline int router_chunk(const int *offsets, int E, int ch, int &r0, int &r1) {
   int first = 0;
   for (int e = 0; e < E; ++e) {
     const int lo = offsets[e], hi = offsets[e + 1];
@@ -822,8 +836,11 @@ __global__ __launch_bounds__(256) void router_wgrad_part_kernel(const T *__restr
                                                                 int E, int d,
                                                                 float *__restrict__ part) {
 #pragma clang fp contract(off)
+  __shared__ int offs_s[PRICHS_MAX_EXPERTS + 1];
+  if ((int)threadIdx.x <= E) offs_s[threadIdx.x] = offsets[threadIdx.x];
+  __syncthreads();
   int r0 = 0, r1 = 0;
-  if (router_chunk(offsets, E, blockIdx.x, r0, r1) < 0) return;
+  if (router_chunk(offs_s, E, blockIdx.x, r0, r1) < 0) return;
   for (int c = threadIdx.x * 8; c < d; c += 256 * 8) {
     float acc[8];
 #pragma unroll
@@ -853,13 +870,16 @@ __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(const float *_
                                                                   int E, int d, int beta,
                                                                   float *__restrict__ dw) {
 #pragma clang fp contract(off)
+  __shared__ int offs_s[PRICHS_MAX_EXPERTS + 1];
+  if ((int)threadIdx.x <= E) offs_s[threadIdx.x] = offsets[threadIdx.x];
+  __syncthreads();
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= d * E) return;
   const int c = i / E, e = i - c * E;
   int first = 0;
   for (int g = 0; g < e; ++g)
-    first += (offsets[g + 1] - offsets[g] + kRouterChunk - 1) / kRouterChunk;
-  const int n = (offsets[e + 1] - offsets[e] + kRouterChunk - 1) / kRouterChunk;
+    first += (offs_s[g + 1] - offs_s[g] + kRouterChunk - 1) / kRouterChunk;
+  const int n = (offs_s[e + 1] - offs_s[e] + kRouterChunk - 1) / kRouterChunk;
   float s = 0.f;
   for (int ch = 0; ch < n; ch += 8) {
     float v[8];
