@@ -40,8 +40,9 @@
  *  - dtype codes: PRICHS_DTYPE_F32 (IEEE binary32) and PRICHS_DTYPE_BF16
  *    (bfloat16 bit patterns in uint16 storage).
  *  - Results of every entry point are deterministic: no floating-point
- *    atomics on any path except the legacy launch_moe_scatter_add, which
- *    keeps the reference's atomicAdd semantics.
+ *    atomics on any path except the legacy launch_moe_scatter_add and
+ *    launch_moe_scatter_add_grad, which keep the reference's atomicAdd
+ *    semantics.
  */
 #ifndef PRICHS_HIP_H
 #define PRICHS_HIP_H
@@ -117,6 +118,37 @@ void launch_moe_scatter_add(const float *dev_exp_out,
                             const int *dev_token_indices,
                             const float *dev_weights, float *dev_accum_out,
                             size_t n_tokens, size_t hidden_dim, void *stream);
+
+/* The backward launchers (Rust extern block engine.rs:152-160, 244-271).
+ * Replaces launch_swiglu_backward (kernels.cu:498-514, kernel 459-480):
+ * sig = 1/(1+exp(-g)), dup = dact*g*sig, dgate = (dact*up)*sig*(1+g*(1-sig)). */
+void launch_swiglu_backward(const float *dev_dact, const float *dev_gate,
+                            const float *dev_up, float *dev_dgate, float *dev_dup,
+                            size_t total_elements, void *stream);
+
+/* Replaces launch_moe_backward_gather_weighted (kernels.cu:1026-1041, kernel
+ * 926-944): d_y_e[i, :] = weights[i] * d_moe[token_indices[i], :]. */
+void launch_moe_backward_gather_weighted(const float *dev_d_moe,
+                                         const int *dev_token_indices,
+                                         const float *dev_weights, float *dev_d_y_e,
+                                         size_t n_tokens, size_t hidden_dim,
+                                         void *stream);
+
+/* Replaces launch_moe_router_dot (kernels.cu:1043-1057, kernel 946-969):
+ * scalars_out[i] = sum_c exp_out[i, c] * d_moe[token_indices[i], c] (one wave
+ * per row, summed in a fixed order). */
+void launch_moe_router_dot(const float *dev_exp_out, const float *dev_d_moe,
+                           const int *dev_token_indices, float *dev_scalars_out,
+                           size_t n_tokens, size_t hidden_dim, void *stream);
+
+/* Replaces launch_moe_scatter_add_grad (kernels.cu:1059-1075, kernel 971-991):
+ * d_normed2[token_indices[i], :] += weights[i] * (d_x_e[i, :] + d_x_e_tmp[i, :])
+ * (atomic add, as in the reference; order-free for the distinct indices of one
+ * expert's token list). */
+void launch_moe_scatter_add_grad(const float *dev_d_x_e, const float *dev_d_x_e_tmp,
+                                 const int *dev_token_indices,
+                                 const float *dev_weights, float *dev_d_normed2,
+                                 size_t n_tokens, size_t hidden_dim, void *stream);
 
 /* ---------------------------------------------------------------------- */
 /* 2. Stage entry points                                                   */

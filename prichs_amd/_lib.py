@@ -93,6 +93,10 @@ SIGNATURES = {
     "launch_rope": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _i, _vp]),
     "launch_moe_gather": (None, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "launch_moe_scatter_add": (None, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "launch_swiglu_backward": (None, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "launch_moe_backward_gather_weighted": (None, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "launch_moe_router_dot": (None, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "launch_moe_scatter_add_grad": (None, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "prichs_router_num_blocks": (_sz, [_sz, _sz]),
     "prichs_router_topk": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz,
                                _vp, _vp, _vp, _vp, _vp]),

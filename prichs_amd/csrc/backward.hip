@@ -915,6 +915,77 @@ __global__ __launch_bounds__(256) void zero_grads_kernel(float *d_router, long l
   }
 }
 
+// ---------------------------------------------------- legacy launchers --
+// The reference's backward launchers with their exact f32 signatures
+// (kernels.cu:498-514, 1026-1075; Rust extern block engine.rs:152-160,
+// 244-271), so its per-expert backward links unchanged.  Same arithmetic as
+// the reference kernels except: expf instead of __expf in the SwiGLU
+// derivative, and the router dot as one wave per row summed in a fixed order
+// (the reference's block reduction order is not part of its contract).
+
+// kernels.cu:459-480.
+__global__ __launch_bounds__(256) void legacy_swiglu_bwd_kernel(const float *__restrict__ dact,
+                                                                const float *__restrict__ gate,
+                                                                const float *__restrict__ up,
+                                                                float *__restrict__ dgate,
+                                                                float *__restrict__ dup, size_t n) {
+#pragma clang fp contract(off)
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float g = gate[i], u = up[i], dy = dact[i];
+  const float sig = 1.0f / (1.0f + expf(-g));
+  const float silu = g * sig;
+  const float dsilu = sig * (1.0f + g * (1.0f - sig));
+  dup[i] = dy * silu;
+  const float dyu = dy * u;
+  dgate[i] = dyu * dsilu;
+}
+
+// kernels.cu:926-944: d_y_e[i][c] = w[i] * d_moe[idx[i]][c].
+__global__ __launch_bounds__(256) void legacy_gather_weighted_kernel(
+    const float *__restrict__ d_moe, const int *__restrict__ idx, const float *__restrict__ w,
+    float *__restrict__ d_y_e, size_t n_tok, size_t hidden) {
+#pragma clang fp contract(off)
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_tok * hidden) return;
+  const size_t r = i / hidden, c = i - r * hidden;
+  d_y_e[i] = w[r] * d_moe[(size_t)idx[r] * hidden + c];
+}
+
+// kernels.cu:946-969: scalars[i] = <exp_out[i], d_moe[idx[i]]>, one wave per row.
+__global__ __launch_bounds__(256) void legacy_router_dot_kernel(
+    const float *__restrict__ exp_out, const float *__restrict__ d_moe,
+    const int *__restrict__ idx, float *__restrict__ scalars, size_t n_tok, size_t hidden) {
+#pragma clang fp contract(off)
+  const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= n_tok) return;
+  const float *a = exp_out + r * hidden;
+  const float *b = d_moe + (size_t)idx[r] * hidden;
+  float s = 0.f;
+  for (size_t c = lane; c < hidden; c += 64) {
+    const float p = a[c] * b[c];
+    s = s + p;
+  }
+  s = wave_sum(s);
+  if (lane == 0) scalars[r] = s;
+}
+
+// kernels.cu:971-991: d_normed2[idx[i]][c] += w[i] * (d_x_e[i][c] + d_x_e_tmp[i][c]),
+// with the reference's atomic add (an expert's token list has distinct
+// indices, so its use is order-free).
+__global__ __launch_bounds__(256) void legacy_scatter_add_grad_kernel(
+    const float *__restrict__ dxe, const float *__restrict__ dxe_tmp, const int *__restrict__ idx,
+    const float *__restrict__ w, float *__restrict__ d_normed2, size_t n_tok, size_t hidden) {
+#pragma clang fp contract(off)
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_tok * hidden) return;
+  const size_t r = i / hidden, c = i - r * hidden;
+  const float sum = dxe[i] + dxe_tmp[i];
+  const float val = w[r] * sum;
+  atomicAdd(d_normed2 + (size_t)idx[r] * hidden + c, val);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- launchers --
@@ -1080,3 +1151,70 @@ int bwd_router_wgrad(const void *xg, const float *dlr, const int32_t *offsets, s
 }
 
 }  // namespace prichs
+
+using namespace prichs;
+
+extern "C" void launch_swiglu_backward(const float *dev_dact, const float *dev_gate,
+                                       const float *dev_up, float *dev_dgate, float *dev_dup,
+                                       size_t total_elements, void *stream) {
+  if (total_elements == 0) return;
+  if (!dev_dact || !dev_gate || !dev_up || !dev_dgate || !dev_dup) {
+    set_error("launch_swiglu_backward: null pointer argument");
+    return;
+  }
+  hipLaunchKernelGGL(legacy_swiglu_bwd_kernel, dim3(blocks_for((long long)total_elements)),
+                     dim3(256), 0, as_stream(stream), dev_dact, dev_gate, dev_up, dev_dgate,
+                     dev_dup, total_elements);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("launch_swiglu_backward: %s", hipGetErrorString(e));
+}
+
+extern "C" void launch_moe_backward_gather_weighted(const float *dev_d_moe,
+                                                    const int *dev_token_indices,
+                                                    const float *dev_weights, float *dev_d_y_e,
+                                                    size_t n_tokens, size_t hidden_dim,
+                                                    void *stream) {
+  const size_t n = n_tokens * hidden_dim;
+  if (n == 0) return;
+  if (!dev_d_moe || !dev_token_indices || !dev_weights || !dev_d_y_e) {
+    set_error("launch_moe_backward_gather_weighted: null pointer argument");
+    return;
+  }
+  hipLaunchKernelGGL(legacy_gather_weighted_kernel, dim3(blocks_for((long long)n)), dim3(256), 0,
+                     as_stream(stream), dev_d_moe, dev_token_indices, dev_weights, dev_d_y_e,
+                     n_tokens, hidden_dim);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("launch_moe_backward_gather_weighted: %s", hipGetErrorString(e));
+}
+
+extern "C" void launch_moe_router_dot(const float *dev_exp_out, const float *dev_d_moe,
+                                      const int *dev_token_indices, float *dev_scalars_out,
+                                      size_t n_tokens, size_t hidden_dim, void *stream) {
+  if (n_tokens == 0) return;
+  if (!dev_exp_out || !dev_d_moe || !dev_token_indices || !dev_scalars_out) {
+    set_error("launch_moe_router_dot: null pointer argument");
+    return;
+  }
+  hipLaunchKernelGGL(legacy_router_dot_kernel, dim3((unsigned)cdiv(n_tokens, 4)), dim3(256), 0,
+                     as_stream(stream), dev_exp_out, dev_d_moe, dev_token_indices,
+                     dev_scalars_out, n_tokens, hidden_dim);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("launch_moe_router_dot: %s", hipGetErrorString(e));
+}
+
+extern "C" void launch_moe_scatter_add_grad(const float *dev_d_x_e, const float *dev_d_x_e_tmp,
+                                            const int *dev_token_indices,
+                                            const float *dev_weights, float *dev_d_normed2,
+                                            size_t n_tokens, size_t hidden_dim, void *stream) {
+  const size_t n = n_tokens * hidden_dim;
+  if (n == 0) return;
+  if (!dev_d_x_e || !dev_d_x_e_tmp || !dev_token_indices || !dev_weights || !dev_d_normed2) {
+    set_error("launch_moe_scatter_add_grad: null pointer argument");
+    return;
+  }
+  hipLaunchKernelGGL(legacy_scatter_add_grad_kernel, dim3(blocks_for((long long)n)), dim3(256), 0,
+                     as_stream(stream), dev_d_x_e, dev_d_x_e_tmp, dev_token_indices, dev_weights,
+                     dev_d_normed2, n_tokens, hidden_dim);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error("launch_moe_scatter_add_grad: %s", hipGetErrorString(e));
+}

@@ -49,6 +49,36 @@ def test_legacy_signatures_match_reference_extern_block():
         assert re.search(sig, text), sig
 
 
+def test_legacy_backward_signatures_match_reference_extern_block():
+    # engine.rs:152-160 and 244-271 declare the backward launchers.
+    text = open(HEADER).read()
+    for sig in [
+        r"void launch_swiglu_backward\(const float \*dev_dact, const float \*dev_gate,\s+const float \*dev_up, float \*dev_dgate, float \*dev_dup,\s+size_t total_elements, void \*stream\)",
+        r"void launch_moe_backward_gather_weighted\(const float \*dev_d_moe,\s+const int \*dev_token_indices,\s+const float \*dev_weights, float \*dev_d_y_e,\s+size_t n_tokens, size_t hidden_dim,\s+void \*stream\)",
+        r"void launch_moe_router_dot\(const float \*dev_exp_out, const float \*dev_d_moe,\s+const int \*dev_token_indices, float \*dev_scalars_out,\s+size_t n_tokens, size_t hidden_dim, void \*stream\)",
+        r"void launch_moe_scatter_add_grad\(const float \*dev_d_x_e, const float \*dev_d_x_e_tmp,\s+const int \*dev_token_indices,\s+const float \*dev_weights, float \*dev_d_normed2,\s+size_t n_tokens, size_t hidden_dim, void \*stream\)",
+    ]:
+        assert re.search(sig, text), sig
+
+
+def test_legacy_backward_launchers_record_null_arguments(lib):
+    p = C.c_void_p(16)
+    for call, name in [
+        (lambda: lib.launch_swiglu_backward(None, p, p, p, p, 8, None), "launch_swiglu_backward"),
+        (lambda: lib.launch_moe_backward_gather_weighted(p, None, p, p, 2, 4, None),
+         "launch_moe_backward_gather_weighted"),
+        (lambda: lib.launch_moe_router_dot(p, p, p, None, 2, 4, None), "launch_moe_router_dot"),
+        (lambda: lib.launch_moe_scatter_add_grad(p, p, p, p, None, 2, 4, None),
+         "launch_moe_scatter_add_grad"),
+    ]:
+        lib.prichs_clear_error()
+        call()
+        assert name in L.last_error() and "null" in L.last_error()
+    lib.prichs_clear_error()
+    lib.launch_moe_router_dot(None, None, None, None, 0, 4, None)  # empty: no-op, no error
+    assert L.last_error() == ""
+
+
 def test_abi_version_and_error_slot(lib):
     assert lib.prichs_abi_version() == 100
     lib.prichs_clear_error()

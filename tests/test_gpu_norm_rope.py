@@ -131,3 +131,82 @@ def test_legacy_swiglu_gather_scatter(cuda, orc):
     for i, t in enumerate(uniq):
         expect[t] = expect[t] + wts[i] * y[i]
     np.testing.assert_array_equal(host(acc), expect)
+
+
+def test_legacy_backward_launchers_run_the_reference_expert_backward(cuda, orc):
+    # The reference's per-expert MoE backward (model.rs:1474-1561 driving
+    # engine.rs:2242-2789) composed from the four legacy backward launchers,
+    # with torch f32 matmuls in place of its cuBLAS SGEMMs and the router VJP
+    # (backward.rs:269-287) on the host, reproduces the oracle's gradients
+    # (reference weighting) within 1e-4.
+    torch.backends.cuda.matmul.allow_tf32 = False
+    lib = L.load()
+    inp = synth.config_inputs(1)
+    T, d, f, E, k = inp.T, inp.d, inp.f, inp.E, inp.k
+    rng = np.random.default_rng(6)
+    d_out = rng.standard_normal((T, d)).astype(np.float32)
+    fwd = orc.moe_forward(inp)
+    sel, gw = fwd["sel"], fwd["gw"]
+    x = inp.x.astype(np.float32)
+    dm = dev(d_out)
+    d_normed2 = torch.zeros((T, d), device="cuda")
+    grads = {"gate": [np.zeros((d, f), np.float32) for _ in range(E + 1)],
+             "up": [np.zeros((d, f), np.float32) for _ in range(E + 1)],
+             "down": [np.zeros((f, d), np.float32) for _ in range(E + 1)]}
+    scal = np.zeros((T, E), np.float32)
+
+    def expert(j, xe):
+        g = xe @ inp.gate[j]
+        u = xe @ inp.up[j]
+        a = orc.swiglu(g, u)
+        return g, u, a, a @ inp.down[j]
+
+    def backward_rows(j, xe, dy, g, u, a):
+        wg, wu, wd = dev(inp.gate[j]), dev(inp.up[j]), dev(inp.down[j])
+        grads["down"][j] += host(dev(a).T @ dy)
+        dact = (dy @ wd.T).contiguous()
+        dg, du = torch.empty_like(dact), torch.empty_like(dact)
+        gd, ud = dev(g), dev(u)
+        lib.launch_swiglu_backward(ptr(dact), ptr(gd), ptr(ud), ptr(dg), ptr(du), dact.numel(), None)
+        xd = dev(xe)
+        grads["gate"][j] += host(xd.T @ dg)
+        grads["up"][j] += host(xd.T @ du)
+        return (dg @ wg.T).contiguous(), (du @ wu.T).contiguous()
+
+    for e in range(E):  # gpu_moe_backward_expert, experts ascending
+        toks = np.nonzero((sel == e).any(1))[0].astype(np.int32)
+        if toks.size == 0:
+            continue
+        w = np.array([gw[t][list(sel[t]).index(e)] for t in toks], np.float32)
+        g, u, a, y = expert(1 + e, x[toks])
+        idx_d, w_d, y_d = torch.from_numpy(toks).to("cuda"), dev(w), dev(y)
+        n = len(toks)
+        dy = torch.empty((n, d), device="cuda")
+        lib.launch_moe_backward_gather_weighted(ptr(dm), ptr(idx_d), ptr(w_d), ptr(dy), n, d, None)
+        sc = torch.empty(n, device="cuda")
+        lib.launch_moe_router_dot(ptr(y_d), ptr(dm), ptr(idx_d), ptr(sc), n, d, None)
+        scal[toks, e] = host(sc)
+        dxg, dxu = backward_rows(1 + e, x[toks], dy, g, u, a)
+        lib.launch_moe_scatter_add_grad(ptr(dxg), ptr(dxu), ptr(idx_d), ptr(w_d), ptr(d_normed2),
+                                        n, d, None)
+        torch.cuda.synchronize()
+    g, u, a, _ = expert(0, x)  # gpu_moe_backward_shared: dY = d_moe
+    dxg, dxu = backward_rows(0, x, dm, g, u, a)
+    d_normed2 += dxg
+    d_normed2 += dxu
+    # Router VJP on the host, then gpu_moe_backward_router's two products.
+    dlog = np.zeros((T, E), np.float32)
+    for t in range(T):
+        ws = np.float32(0)
+        for j in range(k):
+            ws = np.float32(ws + gw[t, j] * scal[t, sel[t, j]])
+        for j in range(k):
+            dlog[t, sel[t, j]] = gw[t, j] * (scal[t, sel[t, j]] - ws)
+    d_router = host(dev(x).T @ dev(dlog))
+    d_normed2 += dev(dlog) @ dev(inp.w_router).T
+    ref = orc.moe_backward(inp, d_out, dx_weighting=2)
+    assert rel_err(host(d_normed2), ref["d_x"]) <= 1e-4
+    assert rel_err(d_router, ref["d_router"]) <= 1e-4
+    for key in ("gate", "up", "down"):
+        for j in range(E + 1):
+            assert rel_err(grads[key][j], ref["d_" + key][j]) <= 1e-4, (key, j)
