@@ -195,9 +195,7 @@ template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
   static constexpr int kStgStride = BN + 8;
   static constexpr size_t kStgBytes = (size_t)BM * kStgStride * sizeof(bf16_t);
   static constexpr size_t kLdsBytes = kRingBytes > kStgBytes ? kRingBytes : kStgBytes;
-  static_assert(WN % (2 * kIl) == 0 && MI % 2 == 0,
-                "whole [gate | up] blocks and two A halves per wave");
-  static_assert(BN % (2 * kIl) == 0, "packed gate/up rows are padded to a multiple of BN");
+  static_assert(MI % 2 == 0 && WN % 16 == 0, "two A halves and whole fragments per wave");
   static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
                 "the DMA instructions of one stage cover the A and B tiles exactly");
   static_assert(3 * kInstPerStage <= 63, "vmcnt immediates");
@@ -226,29 +224,26 @@ static_assert(Bf16::BN % Bf16Down::BN == 0,
 // substitute in the host pass).
 constexpr int kBf16Threads = 64 * PRICHS_BF16_WGM * PRICHS_BF16_WGN;
 
+// One output tile of the grouped GEMM: M-tile mt (global over the groups of
+// tm) and N-tile nt of width Cf::BN, computed by the whole workgroup.
 template <class Cf, bool GATEUP>
-__global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
+__device__ __forceinline__ void bf16_tile(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
-    bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
-    int G, int dense_m, int stage_c, bf16_t *__restrict__ P) {
+    bf16_t *__restrict__ C, int ldc, int n_store, const TileMap &tm, int G, int stage_c,
+    bf16_t *__restrict__ P, bf16_t *lds, int mt, int nt) {
   constexpr int BM = Cf::BM, BN = Cf::BN, BK = Cf::BK, kStages = Cf::kStages;
   constexpr int WGN = Cf::WGN, WM = Cf::WM, WN = Cf::WN, MI = Cf::MI, NJ = Cf::NJ;
   constexpr int kRowsPerInst = Cf::kRowsPerInst, kInstA = Cf::kInstA, kInstB = Cf::kInstB;
   constexpr int kInstPerStage = Cf::kInstPerStage, kStageElems = Cf::kStageElems;
   static_assert(Cf::kThreads == kBf16Threads, "launch bound of the bf16 kernels");
-
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  __shared__ TileMap tm;
-  build_tile_map(tm, offsets, G, BM, dense_m);
+  static_assert(!GATEUP || (WN % (2 * Cf::kIl) == 0 && BN % (2 * Cf::kIl) == 0),
+                "whole [gate | up] blocks per wave; packed gate/up rows padded to BN");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
-  const int n_tiles = Np / BN;
-  const int m_tiles = tm.prefix[G];
-  const int total = m_tiles * n_tiles;
   const int KT = K / BK;
 
   // DMA lane mapping: instruction i of wave w fills rows r0 = 16 (w kInst + i)
@@ -263,260 +258,304 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
   // B stage: whole packed fragments in weight order, lane-major (1 KiB each).
   const int b_rd = wn * WN * BK + lane * 8;
 
-  const int nblk = gridDim.x;
-  for (int t = xcd_block_id(); t < total; t += nblk) {
-    int mt, nt;
-    tile_coords(t, m_tiles, n_tiles, mt, nt);
-    const int g = find_group(tm, G, mt);
-    const int row0 = tm.offs[g];
-    const int mg = tm.offs[g + 1] - row0;
-    const int m0 = (mt - tm.prefix[g]) * BM;
-    const int n0 = nt * BN;
+  const int g = find_group(tm, G, mt);
+  const int row0 = tm.offs[g];
+  const int mg = tm.offs[g + 1] - row0;
+  const int m0 = (mt - tm.prefix[g]) * BM;
+  const int n0 = nt * BN;
 
-    uint32_t a_goff[kInstA], b_goff[kInstB];
+  uint32_t a_goff[kInstA], b_goff[kInstB];
 #pragma unroll
-    for (int i = 0; i < kInstA; ++i) {
-      int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
-      lr = lr < mg ? lr : mg - 1;  // rows past the group repeat its last row
-      const int vr = row0 + lr;
-      const int src = a_rows ? a_rows[vr] : vr;
-      a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
+  for (int i = 0; i < kInstA; ++i) {
+    int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
+    lr = lr < mg ? lr : mg - 1;  // rows past the group repeat its last row
+    const int vr = row0 + lr;
+    const int src = a_rows ? a_rows[vr] : vr;
+    a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < kInstB; ++i) {
+    // Instruction i moves fragment (16-row block nb, K-step kt): 1 KiB at
+    // (nb * KT + kt) * 512 elements, lane l's 16 bytes at l * 8.
+    const int nb = n0 / kRowsPerInst + wave * kInstB + i;
+    b_goff[i] = (uint32_t)nb * (uint32_t)KT * 512u + (uint32_t)(lane * 8);
+  }
+  const bf16_t *Bg = B + (long long)g * b_group_stride;
+
+  f32x4 acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // The previous tile's stores drain and every wave is past its last LDS
+  // read before the ring is refilled.
+  wait_vmcnt(0);
+  lds_barrier();
+
+  // DMA instruction `which` of stage kt_: A rows first, then B fragments.
+  auto issue_one = [&](int kt_, int which) {
+    bf16_t *st_ = lds + (kt_ & (kStages - 1)) * kStageElems;
+    if (which < kInstA) {
+      dma_16b(A + a_goff[which] + kt_ * BK, st_ + (wave * kInstA + which) * kRowsPerInst * BK);
+    } else {
+      const int i_ = which - kInstA;
+      dma_16b(Bg + b_goff[i_] + kt_ * 512,
+              st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK);
     }
+  };
+  auto issue_stage = [&](int kt_) {
 #pragma unroll
-    for (int i = 0; i < kInstB; ++i) {
-      // Instruction i moves fragment (16-row block nb, K-step kt): 1 KiB at
-      // (nb * KT + kt) * 512 elements, lane l's 16 bytes at l * 8.
-      const int nb = n0 / kRowsPerInst + wave * kInstB + i;
-      b_goff[i] = (uint32_t)nb * (uint32_t)KT * 512u + (uint32_t)(lane * 8);
-    }
-    const bf16_t *Bg = B + (long long)g * b_group_stride;
+    for (int w = 0; w < kInstPerStage; ++w) issue_one(kt_, w);
+  };
 
-    f32x4 acc[MI][NJ];
+  // Prologue: stages 0..3 in flight; stage 0 lands and is read.
+  issue_stage(0);
+  if (KT > 1) issue_stage(1);
+  if (KT > 2) issue_stage(2);
+  if (KT > 3) issue_stage(3);
+  {
+    const int ahead = min(3, KT - 1);  // stages issued after stage 0
+    if (ahead == 3)
+      wait_vmcnt(3 * kInstPerStage);
+    else if (ahead == 2)
+      wait_vmcnt(2 * kInstPerStage);
+    else if (ahead == 1)
+      wait_vmcnt(kInstPerStage);
+    else
+      wait_vmcnt(0);
+  }
+  lds_barrier();
+
+  // Fragments of one stage in registers: B (w) and the second half of A
+  // (ahi).  Two sets swap roles from step to step; the first half of A
+  // (alo) is consumed before the barrier, so one set of it is enough.
+  struct Frags {
+    bf16x8 w[NJ], ahi[MI / 2];
+  };
+  Frags fa, fb;
+  bf16x8 alo[MI / 2];
+  auto read_stage = [&](int st, Frags &f) {
+    const bf16_t *as = lds + (st & (kStages - 1)) * kStageElems;
+    const bf16_t *bs = as + BM * BK;
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int jj = 0; jj < NJ; ++jj)
+      f.w[jj] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + jj * 16 * BK);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // The previous tile's stores drain and every wave is past its last LDS
-    // read before the ring is refilled.
-    wait_vmcnt(0);
-    lds_barrier();
-
-    // DMA instruction `which` of stage kt_: A rows first, then B fragments.
-    auto issue_one = [&](int kt_, int which) {
-      bf16_t *st_ = lds + (kt_ & (kStages - 1)) * kStageElems;
-      if (which < kInstA) {
-        dma_16b(A + a_goff[which] + kt_ * BK, st_ + (wave * kInstA + which) * kRowsPerInst * BK);
-      } else {
-        const int i_ = which - kInstA;
-        dma_16b(Bg + b_goff[i_] + kt_ * 512,
-                st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK);
-      }
-    };
-    auto issue_stage = [&](int kt_) {
+    for (int ii = 0; ii < MI / 2; ++ii)
+      alo[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + ii * 16 * BK);
 #pragma unroll
-      for (int w = 0; w < kInstPerStage; ++w) issue_one(kt_, w);
-    };
+    for (int ii = 0; ii < MI / 2; ++ii)
+      f.ahi[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + (MI / 2 + ii) * 16 * BK);
+  };
+  read_stage(0, fa);
 
-    // Prologue: stages 0..3 in flight; stage 0 lands and is read.
-    issue_stage(0);
-    if (KT > 1) issue_stage(1);
-    if (KT > 2) issue_stage(2);
-    if (KT > 3) issue_stage(3);
-    {
-      const int ahead = min(3, KT - 1);  // stages issued after stage 0
-      if (ahead == 3)
-        wait_vmcnt(3 * kInstPerStage);
-      else if (ahead == 2)
+  // One K-step: MFMAs of stage kt (fragments in cur) in two halves around
+  // the barrier that hands stage kt's slot to stage kt + 4 (issued here
+  // when kDma).  All of stage kt+1's fragments are read right after the
+  // barrier, into nxt and alo, so they land during the second half.
+  auto step = [&](int kt, auto dma_c, auto last_c, Frags &cur, Frags &nxt) {
+    constexpr bool kDma = decltype(dma_c)::value;    // issue stage kt + 4
+    constexpr bool kLast = decltype(last_c)::value;  // kt == KT - 1
+#pragma unroll
+    for (int i = 0; i < MI / 2; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(cur.w[j], alo[i], acc[i][j]);
+
+    if constexpr (!kLast) {
+      // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
+      const int ahead = min(2, KT - 2 - kt);
+      if (ahead == 2)
         wait_vmcnt(2 * kInstPerStage);
       else if (ahead == 1)
         wait_vmcnt(kInstPerStage);
       else
         wait_vmcnt(0);
+      lds_barrier();
+      // Every wave has read stage kt (in the previous step), so its slot
+      // takes stage kt + 4.
+      if constexpr (kDma) issue_stage(kt + 4);
+      read_stage(kt + 1, nxt);
+      // Keep these reads ahead of the second half's MFMAs (the scheduler
+      // would otherwise sink them next to their use in the next step).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < MI / 2; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        acc[MI / 2 + i][j] = mfma_bf16(cur.w[j], cur.ahi[i], acc[MI / 2 + i][j]);
+  };
+
+  // Steps that refill the ring (in pairs, the fragment sets swapping
+  // roles), then the ones without loads, then the last step (no next
+  // stage).  An odd leftover step moves its next set into fa once.
+  int kt = 0;
+  for (; kt + 5 < KT; kt += 2) {
+    step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
+    step(kt + 1, bool_c<true>{}, bool_c<false>{}, fb, fa);
+  }
+  if (kt + 4 < KT) {
+    step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
+    fa = fb;
+    ++kt;
+  }
+  for (; kt + 2 < KT; kt += 2) {
+    step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
+    step(kt + 1, bool_c<false>{}, bool_c<false>{}, fb, fa);
+  }
+  if (kt + 1 < KT) {
+    step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
+    fa = fb;
+    ++kt;
+  }
+  step(kt, bool_c<false>{}, bool_c<true>{}, fa, fb);
+
+  // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
+  //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
+  const int lr = m0 + wm * WM + fr;
+  const int cq = 4 * (lane >> 4);
+  if (!GATEUP && stage_c) {
+    // Staged (down / dense): each lane's 8-byte pieces go to a row-major
+    // copy of the tile in LDS, then the workgroup writes whole rows with
+    // 16-byte lanes (a wave store covers 8 full 128-byte lines instead of
+    // 32-byte pieces of 16 rows).  C is 16-byte aligned and ldc, n_store
+    // are multiples of 8.  (The gate/up epilogue writes half as many
+    // columns and gains nothing from it.)
+    constexpr int kS = Cf::kStgStride;
+    lds_barrier();  // every wave is done reading the ring
+    const int tcol = wn * WN + cq;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      bf16_t *srow = lds + (wm * WM + fr + 16 * i) * kS + tcol;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const f32x4 a = acc[i][j];
+        *reinterpret_cast<u32x2 *>(srow + 16 * j) =
+            u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+      }
     }
     lds_barrier();
-
-    // Fragments of one stage in registers: B (w) and the second half of A
-    // (ahi).  Two sets swap roles from step to step; the first half of A
-    // (alo) is consumed before the barrier, so one set of it is enough.
-    struct Frags {
-      bf16x8 w[NJ], ahi[MI / 2];
-    };
-    Frags fa, fb;
-    bf16x8 alo[MI / 2];
-    auto read_stage = [&](int st, Frags &f) {
-      const bf16_t *as = lds + (st & (kStages - 1)) * kStageElems;
-      const bf16_t *bs = as + BM * BK;
-#pragma unroll
-      for (int jj = 0; jj < NJ; ++jj)
-        f.w[jj] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + jj * 16 * BK);
-#pragma unroll
-      for (int ii = 0; ii < MI / 2; ++ii)
-        alo[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + ii * 16 * BK);
-#pragma unroll
-      for (int ii = 0; ii < MI / 2; ++ii)
-        f.ahi[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + (MI / 2 + ii) * 16 * BK);
-    };
-    read_stage(0, fa);
-
-    // One K-step: MFMAs of stage kt (fragments in cur) in two halves around
-    // the barrier that hands stage kt's slot to stage kt + 4 (issued here
-    // when kDma).  All of stage kt+1's fragments are read right after the
-    // barrier, into nxt and alo, so they land during the second half.
-    auto step = [&](int kt, auto dma_c, auto last_c, Frags &cur, Frags &nxt) {
-      constexpr bool kDma = decltype(dma_c)::value;    // issue stage kt + 4
-      constexpr bool kLast = decltype(last_c)::value;  // kt == KT - 1
-#pragma unroll
-      for (int i = 0; i < MI / 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(cur.w[j], alo[i], acc[i][j]);
-
-      if constexpr (!kLast) {
-        // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
-        const int ahead = min(2, KT - 2 - kt);
-        if (ahead == 2)
-          wait_vmcnt(2 * kInstPerStage);
-        else if (ahead == 1)
-          wait_vmcnt(kInstPerStage);
-        else
-          wait_vmcnt(0);
-        lds_barrier();
-        // Every wave has read stage kt (in the previous step), so its slot
-        // takes stage kt + 4.
-        if constexpr (kDma) issue_stage(kt + 4);
-        read_stage(kt + 1, nxt);
-        // Keep these reads ahead of the second half's MFMAs (the scheduler
-        // would otherwise sink them next to their use in the next step).
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int i = 0; i < MI / 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[MI / 2 + i][j] = mfma_bf16(cur.w[j], cur.ahi[i], acc[MI / 2 + i][j]);
-    };
-
-    // Steps that refill the ring (in pairs, the fragment sets swapping
-    // roles), then the ones without loads, then the last step (no next
-    // stage).  An odd leftover step moves its next set into fa once.
-    int kt = 0;
-    for (; kt + 5 < KT; kt += 2) {
-      step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
-      step(kt + 1, bool_c<true>{}, bool_c<false>{}, fb, fa);
-    }
-    if (kt + 4 < KT) {
-      step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
-      fa = fb;
-      ++kt;
-    }
-    for (; kt + 2 < KT; kt += 2) {
-      step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
-      step(kt + 1, bool_c<false>{}, bool_c<false>{}, fb, fa);
-    }
-    if (kt + 1 < KT) {
-      step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
-      fa = fb;
-      ++kt;
-    }
-    step(kt, bool_c<false>{}, bool_c<true>{}, fa, fb);
-
-    // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
-    //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
-    const int lr = m0 + wm * WM + fr;
-    const int cq = 4 * (lane >> 4);
-    if (!GATEUP && stage_c) {
-      // Staged (down / dense): each lane's 8-byte pieces go to a row-major
-      // copy of the tile in LDS, then the workgroup writes whole rows with
-      // 16-byte lanes (a wave store covers 8 full 128-byte lines instead of
-      // 32-byte pieces of 16 rows).  C is 16-byte aligned and ldc, n_store
-      // are multiples of 8.  (The gate/up epilogue writes half as many
-      // columns and gains nothing from it.)
-      constexpr int kS = Cf::kStgStride;
-      lds_barrier();  // every wave is done reading the ring
-      const int tcol = wn * WN + cq;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        bf16_t *srow = lds + (wm * WM + fr + 16 * i) * kS + tcol;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const f32x4 a = acc[i][j];
-          *reinterpret_cast<u32x2 *>(srow + 16 * j) =
-              u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-        }
-      }
-      lds_barrier();
-      constexpr int kChunksRow = BN / 8;  // 16-byte chunks per tile row
+    constexpr int kChunksRow = BN / 8;  // 16-byte chunks per tile row
 #pragma unroll 4
-      for (int c = tid; c < BM * kChunksRow; c += Cf::kThreads) {
-        const int r = c / kChunksRow, ch = c - r * kChunksRow;
-        const int m = m0 + r, col = n0 + 8 * ch;
-        if (m < mg && col < n_store)
-          *reinterpret_cast<u32x4 *>(C + (long long)(row0 + m) * ldc + col) =
-              *reinterpret_cast<const u32x4 *>(lds + r * kS + 8 * ch);
-      }
-      continue;  // the next tile's barrier keeps the ring refill behind these reads
+    for (int c = tid; c < BM * kChunksRow; c += Cf::kThreads) {
+      const int r = c / kChunksRow, ch = c - r * kChunksRow;
+      const int m = m0 + r, col = n0 + 8 * ch;
+      if (m < mg && col < n_store)
+        *reinterpret_cast<u32x4 *>(C + (long long)(row0 + m) * ldc + col) =
+            *reinterpret_cast<const u32x4 *>(lds + r * kS + 8 * ch);
     }
-    if (GATEUP) {
-      // Packed rows [n0 + wn*WN, +WN) are WN / (2 kIl) [kIl gate | kIl up]
-      // blocks: in block q, gate column c (16-column piece jj) pairs with up
-      // column c, kIl / 16 pieces on.
-      constexpr int kPieces = Cf::kIl / 16;  // 16-column pieces per gate (or up) half
-      if (P != nullptr) {
-        // Training forward: the gate/up pre-activations too, [rows][Np] in
-        // packed column order (the backward's SwiGLU derivative needs them).
-#pragma unroll
-        for (int i = 0; i < MI; ++i) {
-          const int m = lr + 16 * i;
-          if (m < mg) {
-            bf16_t *prow = P + (long long)(row0 + m) * Np + n0 + wn * WN + cq;
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              const f32x4 a = acc[i][j];
-              *reinterpret_cast<u32x2 *>(prow + 16 * j) =
-                  u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-            }
-          }
-        }
-      }
+    return;  // the next tile's barrier keeps the ring refill behind these reads
+  }
+  if (GATEUP) {
+    // Packed rows [n0 + wn*WN, +WN) are WN / (2 kIl) [kIl gate | kIl up]
+    // blocks: in block q, gate column c (16-column piece jj) pairs with up
+    // column c, kIl / 16 pieces on.
+    constexpr int kPieces = Cf::kIl / 16;  // 16-column pieces per gate (or up) half
+    if (P != nullptr) {
+      // Training forward: the gate/up pre-activations too, [rows][Np] in
+      // packed column order (the backward's SwiGLU derivative needs them).
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = lr + 16 * i;
         if (m < mg) {
-          bf16_t *crow = C + (long long)(row0 + m) * ldc;
-#pragma unroll
-          for (int jg = 0; jg < NJ / 2; ++jg) {
-            const int q = jg / kPieces, jj = jg - q * kPieces;
-            const int j = 2 * kPieces * q + jj;  // gate piece; up piece is j + kPieces
-            const int col = (n0 + wn * WN + 2 * Cf::kIl * q) / 2 + 16 * jj + cq;
-            if (col < n_store) {
-              float h[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + kPieces][r];
-              *reinterpret_cast<u32x2 *>(crow + col) =
-                  u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-            }
-          }
-        }
-      }
-    } else {
-      const int cbase = n0 + wn * WN + cq;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int m = lr + 16 * i;
-        if (m < mg) {
-          bf16_t *crow = C + (long long)(row0 + m) * ldc;
+          bf16_t *prow = P + (long long)(row0 + m) * Np + n0 + wn * WN + cq;
 #pragma unroll
           for (int j = 0; j < NJ; ++j) {
-            const int col = cbase + 16 * j;
-            if (col < n_store) {
-              const f32x4 a = acc[i][j];
-              *reinterpret_cast<u32x2 *>(crow + col) =
-                  u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-            }
+            const f32x4 a = acc[i][j];
+            *reinterpret_cast<u32x2 *>(prow + 16 * j) =
+                u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
           }
         }
       }
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = lr + 16 * i;
+      if (m < mg) {
+        bf16_t *crow = C + (long long)(row0 + m) * ldc;
+#pragma unroll
+        for (int jg = 0; jg < NJ / 2; ++jg) {
+          const int q = jg / kPieces, jj = jg - q * kPieces;
+          const int j = 2 * kPieces * q + jj;  // gate piece; up piece is j + kPieces
+          const int col = (n0 + wn * WN + 2 * Cf::kIl * q) / 2 + 16 * jj + cq;
+          if (col < n_store) {
+            float h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + kPieces][r];
+            *reinterpret_cast<u32x2 *>(crow + col) =
+                u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+          }
+        }
+      }
+    }
+  } else {
+    const int cbase = n0 + wn * WN + cq;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = lr + 16 * i;
+      if (m < mg) {
+        bf16_t *crow = C + (long long)(row0 + m) * ldc;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int col = cbase + 16 * j;
+          if (col < n_store) {
+            const f32x4 a = acc[i][j];
+            *reinterpret_cast<u32x2 *>(crow + col) =
+                u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+          }
+        }
+      }
+    }
+  }
+}
+
+// Persistent grouped GEMM: workgroups walk the (group, M-tile, N-tile) list
+// in the XCD-aware order.  CfT is the configuration of the last partial
+// round (wave quantisation): when its tiles fill at most half of the
+// workgroups, each of them is computed as two half-width tiles (CfT::BN =
+// Cf::BN / 2) on two workgroups, so that round takes about half as long.
+// Every output element is the same MFMA chain over K either way, so the
+// results are bit-identical.  CfT == Cf turns this off.
+template <class Cf, class CfT, bool GATEUP>
+__global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
+    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
+    const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
+    bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
+    int G, int dense_m, int stage_c, bf16_t *__restrict__ P) {
+  constexpr bool kSplit = !std::is_same<Cf, CfT>::value;
+  static_assert(!kSplit || (CfT::BM == Cf::BM && 2 * CfT::BN == Cf::BN && !GATEUP),
+                "tail tiles are the two column halves of a down / dense tile");
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  __shared__ TileMap tm;
+  build_tile_map(tm, offsets, G, Cf::BM, dense_m);
+
+  const int n_tiles = Np / Cf::BN;
+  const int m_tiles = tm.prefix[G];
+  const int total = m_tiles * n_tiles;
+  const int nblk = gridDim.x;
+  int n_full = total, n_items = total;  // tiles computed whole; work items
+  if (kSplit) {
+    const int tail = total % nblk;
+    if (tail > 0 && 2 * tail <= nblk) {
+      n_full = total - tail;
+      n_items = n_full + 2 * tail;
+    }
+  }
+  for (int t = xcd_block_id(); t < n_items; t += nblk) {
+    int mt, nt;
+    if (t < n_full) {
+      tile_coords(t, m_tiles, n_tiles, mt, nt);
+      bf16_tile<Cf, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm, G,
+                            stage_c, P, lds, mt, nt);
+    } else if constexpr (kSplit) {
+      // Items 2u, 2u + 1 are the halves of tail tile n_full + u (consecutive
+      // items run on one XCD, so both halves share the A panel in its L2).
+      const int u = t - n_full;
+      tile_coords(n_full + u / 2, m_tiles, n_tiles, mt, nt);
+      bf16_tile<CfT, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm, G,
+                             stage_c, P, lds, mt, 2 * nt + (u & 1));
     }
   }
 }
@@ -936,17 +975,24 @@ template <typename T> void pack_down_impl(const float *down, size_t d, size_t f,
       put<T>(out, packed_index(n, k, f, sizeof(T) == 2), n < d ? down[k * d + n] : 0.0f);
 }
 
+// Half-width configuration of the last partial round (down / dense only).
+template <class Cf, bool GATEUP>
+using TailCfg = typename std::conditional<GATEUP, Cf,
+                                          Bf16Cfg<Cf::BM, Cf::BN / 2, Cf::WGM, Cf::WGN>>::type;
+
 template <class Cf, bool GATEUP>
 int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                 int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
                 int dense_m, size_t max_rows, int cus, hipStream_t s, void *pre) {
   // Persistent grid: one workgroup per CU (the LDS ring allows one), fewer
-  // when the launch has fewer tiles.
-  const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN);
+  // when the launch has fewer tiles (twice the tiles when the last round may
+  // be split into halves).
+  using CfT = TailCfg<Cf, GATEUP>;
+  const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN) * (GATEUP ? 1 : 2);
   const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus));
   static bool attr_set = false;
   if (!attr_set) {
-    PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&bf16_gemm_kernel<Cf, GATEUP>),
+    PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&bf16_gemm_kernel<Cf, CfT, GATEUP>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)Cf::kLdsBytes),
                    "grouped gemm: set LDS size");
@@ -957,7 +1003,8 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
   const int stage_c = !GATEUP && PRICHS_GEMM_STAGE_C &&
                       reinterpret_cast<uintptr_t>(Cp) % 16 == 0 && ldc % 8 == 0 &&
                       n_store % 8 == 0;
-  hipLaunchKernelGGL((bf16_gemm_kernel<Cf, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
+  static_assert(CfT::kLdsBytes <= Cf::kLdsBytes, "tail tiles fit the launch's LDS");
+  hipLaunchKernelGGL((bf16_gemm_kernel<Cf, CfT, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
                      b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G, dense_m,
                      stage_c, static_cast<bf16_t *>(pre));

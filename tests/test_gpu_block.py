@@ -50,6 +50,41 @@ def test_dense_gemm(cuda, orc, M, K, N):
     assert not hw[:, :32].any() and not hw[:, 32 + N:].any()
 
 
+def _tail_split(M, n_tiles, cus, bm=256):
+    """Whether the dense GEMM computes its last partial round as half-width
+    tiles: the launcher's grid is min(2 (M/bm + 1) n_tiles, CUs), and a tail
+    of t tiles is split when 2 t fits the grid."""
+    tiles = -(-M // bm) * n_tiles
+    grid = min(2 * (M // bm + 1) * n_tiles, cus)
+    tail = tiles % grid
+    return 0 < tail and 2 * tail <= grid
+
+
+def test_gemm_tail_round_halves_bit_identical(cuda):
+    """The last partial round of the down / dense GEMM runs as half-width
+    tiles: every output element is the same MFMA chain over K, so rows
+    computed that way are bit-identical to the same rows of a launch that
+    computes them as whole tiles, and within the 1e-2 bar of float64."""
+    K = N = 1536
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = np.random.default_rng(11)
+    a = synth.round_bf16(rng.standard_normal((20000, K)))
+    w = synth.round_bf16(0.05 * rng.standard_normal((K, N)))
+    wp = ops.to_device_packed([ops.pack_weight(w, "bf16")], "bf16")
+    assert not _tail_split(20000, N // 256, cus)
+    whole = host(ops.gemm(dev(a), wp, N))
+    split_seen = False
+    for M in (4096, 12000, 12288):
+        split_seen |= _tail_split(M, N // 256, cus)
+        say(f"dense gemm M={M}: tail split {_tail_split(M, N // 256, cus)} on {cus} CUs")
+        c = host(ops.gemm(dev(a[:M]), wp, N))
+        np.testing.assert_array_equal(c, whole[:M])
+        lo = max(0, M - 2048)  # the tail tiles hold the last M-tiles
+        ref = a[lo:M].astype(np.float64) @ w.astype(np.float64)
+        assert rel_err(c[lo:], ref) <= 1e-2
+    assert split_seen or cus > 512, "no shape exercised the half-width tail tiles"
+
+
 def test_residual_add_bit_exact(cuda):
     rng = np.random.default_rng(1)
     a = synth.round_bf16(rng.standard_normal(4096))
