@@ -60,22 +60,27 @@ template <typename T> bool aligned16(const T *p) {
 // ------------------------------------------------------------- combine --
 // out[t] = shared[t] (or 0); then for the token's experts in ascending id:
 // out = out + w * y[row]  (crates/prichs-model/src/moe.rs:146, 149, 177-184).
-template <typename YT, typename OT, bool VEC>
+// KC is the top-k as a compile-time constant (the common k = 1, 2 keep the
+// index loads and the ordering to a few instructions); KC = 0 takes k at run
+// time (k <= PRICHS_MAX_TOPK).
+template <typename YT, typename OT, bool VEC, int KC>
 __global__ __launch_bounds__(256) void combine_kernel(
     const YT *__restrict__ y, const int32_t *__restrict__ topk_idx,
     const float *__restrict__ topk_w, const int32_t *__restrict__ token_row, int T, int d,
-    int k, int has_shared, OT *__restrict__ out) {
+    int k_rt, int has_shared, OT *__restrict__ out) {
 #pragma clang fp contract(off)
+  constexpr int kMax = KC > 0 ? KC : PRICHS_MAX_TOPK;
+  const int k = KC > 0 ? KC : k_rt;
   const int per_tok = VEC ? d / 8 : d;
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (long long)T * per_tok) return;
   const int t = (int)(gid / per_tok);
   const int c = (int)(gid - (long long)t * per_tok) * (VEC ? 8 : 1);
 
-  int ex[PRICHS_MAX_TOPK], rows[PRICHS_MAX_TOPK];
-  float wt[PRICHS_MAX_TOPK];
+  int ex[kMax], rows[kMax];
+  float wt[kMax];
 #pragma unroll
-  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+  for (int s = 0; s < kMax; ++s) {
     if (s < k) {
       ex[s] = topk_idx[(size_t)t * k + s];
       rows[s] = token_row[(size_t)t * k + s];
@@ -86,12 +91,12 @@ __global__ __launch_bounds__(256) void combine_kernel(
       wt[s] = 0.f;
     }
   }
-  // Ascending expert id (k <= 8: a fixed compare-exchange network would do,
-  // but k is runtime; a bubble pass over registers stays in registers).
+  // Ascending expert id: a bubble pass over registers (a single
+  // compare-exchange for k = 2).
 #pragma unroll
-  for (int a = 0; a < PRICHS_MAX_TOPK - 1; ++a)
+  for (int a = 0; a < kMax - 1; ++a)
 #pragma unroll
-    for (int b = 0; b < PRICHS_MAX_TOPK - 1 - a; ++b)
+    for (int b = 0; b < kMax - 1 - a; ++b)
       if (ex[b] > ex[b + 1]) {
         int te = ex[b]; ex[b] = ex[b + 1]; ex[b + 1] = te;
         int tr = rows[b]; rows[b] = rows[b + 1]; rows[b + 1] = tr;
@@ -108,7 +113,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
       for (int j = 0; j < 8; ++j) acc.v[j] = 0.f;
     }
 #pragma unroll
-    for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+    for (int s = 0; s < kMax; ++s) {
       if (s < k) {
         const V8 yv = ld8(y + (size_t)rows[s] * d + c);
 #pragma unroll
@@ -280,7 +285,10 @@ void launch_combine_t(const void *y, const int32_t *idx, const float *w, const i
   const bool vec =
       d % 8 == 0 && aligned16(static_cast<const YT *>(y)) && aligned16(static_cast<OT *>(out));
   const size_t n = T * (vec ? d / 8 : d);
-  auto kern = vec ? combine_kernel<YT, OT, true> : combine_kernel<YT, OT, false>;
+  auto kern = vec ? (k == 2   ? combine_kernel<YT, OT, true, 2>
+                     : k == 1 ? combine_kernel<YT, OT, true, 1>
+                              : combine_kernel<YT, OT, true, 0>)
+                  : combine_kernel<YT, OT, false, 0>;
   hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(256), 0, s, static_cast<const YT *>(y), idx, w,
                      tr, (int)T, (int)d, (int)k, has_shared, static_cast<OT *>(out));
 }
