@@ -26,6 +26,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #define PRICHS_ROUTER_THREADS 256
 #endif
 constexpr int kRouterThreads = PRICHS_ROUTER_THREADS;  // >= PRICHS_MAX_EXPERTS
+// Quad-broadcast router for E <= 8 (1) or always the staged router (0).
+#ifndef PRICHS_ROUTER_QUAD
+#define PRICHS_ROUTER_QUAD 1
+#endif
 constexpr int kRouterLdsBytes = 60 * 1024;  // simple kernel: W chunk [E][kc + 4] f32
 
 int lanes_per_token_log2(int E) {
@@ -396,6 +400,175 @@ router_topk_staged_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Quad-broadcast router (E <= 8, eight lanes per token, d % 128 == 0).  The
+// block's router weights sit transposed in LDS for the whole kernel (staged
+// once, no barrier in the K loop), and x never goes through LDS: in chunks of
+// 128, lane r = e % 4 of each quad loads its quarter (32 values) of the
+// token's chunk straight into registers, and every product takes x from the
+// quad's holder lane by a DPP quad broadcast folded into the multiply.  Per
+// k a lane thus reads 4 bytes of LDS (its expert's weight) instead of 8, and
+// at one wave per SIMD nothing waits on a workgroup barrier.  The arithmetic
+// is the reference's (k ascending, product rounded, then sum rounded).
+// ---------------------------------------------------------------------------
+template <typename XT> struct QuadRouter {
+  static constexpr int kKC = 128;                 // k per chunk
+  static constexpr int kQ = kKC / 4;              // x values a lane holds per chunk
+  static constexpr int kVe = 16 / (int)sizeof(XT);
+  static constexpr int kLoads = kQ / kVe;         // 16-byte loads per lane per chunk
+  static constexpr int kRing = sizeof(XT) == 2 ? 4 : 2;  // chunks in flight
+};
+
+// x broadcast from lane h of each quad (quad_perm [h, h, h, h]).
+template <int H> __device__ __forceinline__ float quad_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), H * 0x55, 0xF, 0xF, true));
+}
+
+template <typename XT>
+__global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
+    const XT *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
+    const float *__restrict__ concept, int n_concept, int T, int d, int E, int k,
+    float *__restrict__ logits, int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
+    int32_t *__restrict__ block_counts) {
+#pragma clang fp contract(off)
+  using Cf = QuadRouter<XT>;
+  constexpr int kTpb = kRouterThreads / 8;
+  extern __shared__ __attribute__((aligned(16))) float wt_s[];  // W^T [8][d + 4]
+  __shared__ int cnt_s[PRICHS_MAX_EXPERTS];
+  const int tid = threadIdx.x;
+  const int e = tid & 7, tl = tid >> 3, r = e & 3;
+  const int t = blockIdx.x * kTpb + tl;
+  const bool valid = (t < T) && (e < E);
+  const int ws = d + 4;
+  const int nch = d / Cf::kKC;
+  if (tid < E) cnt_s[tid] = 0;
+
+  // This lane's quarter of each chunk (rows past T read row T-1, never summed).
+  const XT *xq = x + (size_t)min(t, T - 1) * d + r * Cf::kQ;
+  u32x4 ring[Cf::kRing][Cf::kLoads];
+  auto fetch = [&](int c, u32x4(&dst)[Cf::kLoads]) {
+    const XT *src = xq + (size_t)min(c, nch - 1) * Cf::kKC;
+#pragma unroll
+    for (int l = 0; l < Cf::kLoads; ++l)
+      dst[l] = *reinterpret_cast<const u32x4 *>(src + l * Cf::kVe);
+  };
+#pragma unroll
+  for (int j = 0; j < Cf::kRing; ++j) fetch(j, ring[j]);
+
+  // W [d][E] (row-major, the reference layout) -> W^T [e][k] in LDS, in
+  // batches of 8 float4 loads per thread issued before their stores (d * E
+  // is a multiple of 4 since d % 128 == 0).
+  {
+    const int n4 = d * E / 4;
+    const f32x4 *w4 = reinterpret_cast<const f32x4 *>(w);
+    for (int base = 0; base < n4; base += 8 * kRouterThreads) {
+      f32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = w4[min(base + u * kRouterThreads + tid, n4 - 1)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * kRouterThreads + tid;
+        if (i < n4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int f = 4 * i + j;  // flat index in [d][E]
+            const int kk = E == 8 ? f >> 3 : f / E;
+            const int ee = f - kk * E;
+            wt_s[ee * ws + kk] = v[u][j];
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const float *wrow = wt_s + (e < E ? e : 0) * ws;
+  float acc = 0.0f;
+  for (int c0 = 0; c0 < nch; c0 += Cf::kRing) {
+#pragma unroll
+    for (int j = 0; j < Cf::kRing; ++j) {
+      const int c = c0 + j;
+      float xf[Cf::kQ];
+#pragma unroll
+      for (int l = 0; l < Cf::kLoads; ++l) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t u = ring[j][l][q];
+          if constexpr (sizeof(XT) == 2) {
+            xf[l * 8 + 2 * q] = __uint_as_float(u << 16);
+            xf[l * 8 + 2 * q + 1] = __uint_as_float(u & 0xffff0000u);
+          } else {
+            xf[l * 4 + q] = __uint_as_float(u);
+          }
+        }
+      }
+      // Refill on every path (unpredicated) so the compiler's waits stay exact.
+      fetch(c + Cf::kRing, ring[j]);
+      if (c < nch) {
+        const float *wc = wrow + c * Cf::kKC;
+        // Pinned interleave: the chunk's weight reads run kAhead groups ahead
+        // of the products and sums (mask 0x100: LDS read, 0x2: VALU).
+        constexpr int kG = Cf::kKC / 4, kAhead = 6;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          const f32x4 wv = *reinterpret_cast<const f32x4 *>(wc + 4 * g);
+          // The four products first (independent), then the dependent sums.
+          float p[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int kk = 4 * g + q;  // holder lane kk / kQ, its value kk % kQ
+            float xv;
+            switch (kk / Cf::kQ) {
+              case 0: xv = quad_bcast<0>(xf[kk % Cf::kQ]); break;
+              case 1: xv = quad_bcast<1>(xf[kk % Cf::kQ]); break;
+              case 2: xv = quad_bcast<2>(xf[kk % Cf::kQ]); break;
+              default: xv = quad_bcast<3>(xf[kk % Cf::kQ]); break;
+            }
+            p[q] = xv * wv[q];
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc = acc + p[q];
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x2, 8, 0);
+          if (g + kAhead < kG) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  // adj = (raw + bias[e]) (+ concept[e]), moe.rs:126-133.
+  float adj = 0.0f;
+  if (valid) {
+    adj = acc + bias[e];
+    if (concept != nullptr && e < n_concept) adj = adj + concept[e];
+  }
+  topk_epilogue(acc, adj, valid, e, t, T, E, k, 8, logits, topk_idx, topk_w, cnt_s);
+  __syncthreads();
+  if (tid < E) block_counts[(size_t)blockIdx.x * E + tid] = cnt_s[tid];
+}
+
+template <typename XT>
+int launch_quad_t(const XT *x, const float *w, const float *bias, const float *concept, int nc,
+                  int T, int d, int E, int k, float *logits, int32_t *idx, float *wt, int32_t *bc,
+                  int nb, hipStream_t s) {
+  const size_t lds = (size_t)8 * (d + 4) * sizeof(float);
+  static int attr_bytes = 0;
+  if ((int)lds > attr_bytes) {
+    PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&router_topk_quad_kernel<XT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                   "router: set LDS size");
+    attr_bytes = (int)lds;
+  }
+  hipLaunchKernelGGL((router_topk_quad_kernel<XT>), dim3(nb), dim3(kRouterThreads), lds, s, x, w,
+                     bias, concept, nc, T, d, E, k, logits, idx, wt, bc);
+  return PRICHS_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Simple router (any d): W chunks in LDS, x read straight from global.
 // ---------------------------------------------------------------------------
 template <typename XT>
@@ -597,7 +770,20 @@ extern "C" int prichs_router_topk(const void *x, int x_dtype, const float *w_rou
   const int nc = (int)(n_concept < E ? n_concept : E);
   const bool staged = (d % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(w_router) % 16 == 0);
-  if (staged) {
+  // The quad-broadcast kernel: eight lanes per token, whole 128-wide chunks,
+  // and W^T within one CU's LDS.
+  const bool quad = staged && lg == 3 && d % 128 == 0 && (size_t)8 * (d + 4) * 4 <= 150 * 1024 &&
+                    PRICHS_ROUTER_QUAD;
+  if (quad) {
+    int rc = x_dtype == PRICHS_DTYPE_BF16
+                 ? launch_quad_t<bf16_t>(static_cast<const bf16_t *>(x), w_router, router_bias,
+                                         concept_bias, nc, (int)T, (int)d, (int)E, (int)k, logits,
+                                         topk_idx, topk_w, block_counts, nb, s)
+                 : launch_quad_t<float>(static_cast<const float *>(x), w_router, router_bias,
+                                        concept_bias, nc, (int)T, (int)d, (int)E, (int)k, logits,
+                                        topk_idx, topk_w, block_counts, nb, s);
+    if (rc) return rc;
+  } else if (staged) {
     int rc = x_dtype == PRICHS_DTYPE_BF16
                  ? launch_staged<bf16_t>(lg, static_cast<const bf16_t *>(x), w_router,
                                          router_bias, concept_bias, nc, (int)T, (int)d, (int)E,

@@ -48,11 +48,15 @@ def test_router_bit_exact(cuda, orc, cfg):
 
 
 # Staged kernel (d % 8 == 0; whole and partial K chunks, 1..64 lanes per
-# token) and the simple kernel (d % 8 != 0, or x not 16-byte aligned).
+# token), the simple kernel (d % 8 != 0, or x not 16-byte aligned) and the
+# quad-broadcast kernel (5..8 experts, d % 128 == 0; chunk counts below, at
+# and above its register ring, ragged T).
 @pytest.mark.parametrize("E,k,T,d", [(4, 2, 77, 64), (8, 1, 33, 96), (16, 3, 200, 128),
                                      (64, 8, 129, 40), (3, 3, 5, 8), (1, 1, 9, 16),
                                      (8, 2, 300, 200), (2, 2, 500, 104), (32, 4, 70, 328),
-                                     (6, 2, 100, 37), (8, 2, 64, 13)])
+                                     (6, 2, 100, 37), (8, 2, 64, 13), (8, 2, 77, 128),
+                                     (6, 2, 100, 384), (5, 3, 33, 256), (8, 2, 1000, 1536),
+                                     (7, 1, 3, 640)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_router_shapes(cuda, orc, E, k, T, d, dtype):
     rng = np.random.default_rng(E * 100 + k)
@@ -84,8 +88,9 @@ def test_router_unaligned_x(cuda, orc):
     np.testing.assert_array_equal(host(idx), rs)
 
 
-def test_router_ties_nan_and_concept_bias(cuda, orc):
-    T, d, E, k = 64, 16, 8, 2
+@pytest.mark.parametrize("d", [16, 128])
+def test_router_ties_nan_and_concept_bias(cuda, orc, d):
+    T, E, k = 64, 8, 2
     rng = np.random.default_rng(11)
     x = rng.standard_normal((T, d)).astype(np.float32)
     x[:16] = 0.0  # raw logits exactly +0: selection decided by the bias, with ties
