@@ -7,8 +7,8 @@
 //   qkv = n1 [Wq | Wk | Wv]                         prichs_gemm (one fused GEMM)
 //   RoPE on the q and k columns of qkv in place     prichs_rope_forward_ld
 //   attn = causal GQA attention(q, k, v)            prichs_attention_forward
-//   x1 = x + attn Wo                                prichs_gemm + prichs_add (x1 in f32)
-//   n2 = rms_norm(x1, post_attn_norm)               prichs_rmsnorm_forward
+//   x1 = x + attn Wo                                prichs_gemm, then one kernel for the
+//   n2 = rms_norm(x1, post_attn_norm)               residual add (x1 in f32) and the norm
 //   out = x1 + MoE(n2)                              prichs_moe_engine_forward + prichs_add
 // Everything is allocated at creation; a forward is a fixed sequence of
 // launches on one stream with no host synchronisation.
@@ -267,10 +267,8 @@ extern "C" int prichs_block_engine_forward(prichs_block_engine *eng, const void 
                                      seq_len, eng->Hq, eng->Hkv, eng->hd, bf, stream)))
     return rc;
   if ((rc = prichs_gemm(eng->attn, d, T, d, eng->w_o, d, eng->attn_out, d, bf, stream))) return rc;
-  if ((rc = prichs_add(x, bf, eng->attn_out, bf, eng->x1, PRICHS_DTYPE_F32, T * d, stream)))
-    return rc;
-  if ((rc = prichs_rmsnorm_forward(eng->x1, PRICHS_DTYPE_F32, eng->post_norm, eng->n2, bf, nullptr,
-                                   T, d, eng->eps, stream)))
+  if ((rc = add_rmsnorm_forward(x, bf, eng->attn_out, bf, eng->x1, eng->post_norm, eng->n2, T, d,
+                                 eng->eps, stream)))
     return rc;
   if ((rc = prichs_moe_engine_forward(eng->moe, eng->n2, T, concept_bias, n_concept, eng->moe_out,
                                       bf, stream)))

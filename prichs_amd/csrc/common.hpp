@@ -169,4 +169,9 @@ struct CheckpointMoe {
 int checkpoint_moe_weights(const prichs_checkpoint *ck, size_t layer, size_t d, size_t f,
                            size_t E, CheckpointMoe &w);
 
+// The block's residual add and post-attention norm in one pass:
+// x1 = a + b (f32), out = rms_norm(x1, w) (bf16) (elementwise.hip).
+int add_rmsnorm_forward(const void *a, int a_dtype, const void *b, int b_dtype, float *x1,
+                        const float *w, void *out, size_t T, size_t d, float eps, void *stream);
+
 }  // namespace prichs

@@ -185,6 +185,58 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT *__restrict__ x,
   }
 }
 
+// ------------------------------------------------- residual add + RMSNorm --
+// The block's x1 = x + attn_out (f32) and n2 = rms_norm(x1, w) in one pass
+// (crates/prichs-model/src/block.rs:50-68; ops.rs:109-135, 250-267): one wave
+// per row keeps its NCH 8-wide chunks of x1 in registers between the sum of
+// squares and the scaling.  Every operation, and the order of the sum, is
+// that of add_kernel followed by rmsnorm_kernel, so x1 and n2 are
+// bit-identical to the two-kernel path.
+template <typename A, typename B, int NCH>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const A *__restrict__ a,
+                                                          const B *__restrict__ b,
+                                                          const float *__restrict__ w,
+                                                          float *__restrict__ x1,
+                                                          bf16_t *__restrict__ out, int T, int d,
+                                                          float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const size_t base = (size_t)row * d;
+  V8 v[NCH];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane * 8 + 512 * i;
+    if (c < d) {
+      const V8 va = ld8(a + base + c), vb = ld8(b + base + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[i].v[j] = va.v[j] + vb.v[j];
+      st8(x1 + base + c, v[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = ss + v[i].v[j] * v[i].v[j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float rms = sqrtf(ss / (float)d + eps);
+  const float inv = 1.0f / rms;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane * 8 + 512 * i;
+    if (c < d) {
+      const V8 wv = ld8(w + c);
+      V8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float t = v[i].v[j] * inv;
+        o.v[j] = t * wv.v[j];
+      }
+      st8(out + base + c, o);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- RoPE --
 // crates/prichs-core/src/backward.rs:160-188: pairs (2i, 2i+1) at position
 // p -> (q0 c - q1 s, q0 s + q1 c), c/s = cache[p * hd/2 + i]; sign * s for
@@ -291,6 +343,14 @@ void launch_combine_t(const void *y, const int32_t *idx, const float *w, const i
                   : combine_kernel<YT, OT, false, 0>;
   hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(256), 0, s, static_cast<const YT *>(y), idx, w,
                      tr, (int)T, (int)d, (int)k, has_shared, static_cast<OT *>(out));
+}
+
+template <typename A, typename B, int NCH>
+void launch_add_rmsnorm_nch(const void *a, const void *b, const float *w, float *x1, void *out,
+                            size_t T, size_t d, float eps, hipStream_t s) {
+  hipLaunchKernelGGL((add_rmsnorm_kernel<A, B, NCH>), dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s,
+                     static_cast<const A *>(a), static_cast<const B *>(b), w, x1,
+                     static_cast<bf16_t *>(out), (int)T, (int)d, eps);
 }
 
 template <typename T>
@@ -422,6 +482,41 @@ void launch_add_t(const void *a, const void *b, void *out, size_t n, hipStream_t
                      static_cast<const A *>(a), static_cast<const B *>(b), static_cast<O *>(out),
                      n8);
 }
+
+namespace prichs {
+// x1 = a + b (f32) and out = rms_norm(x1, w) (bf16) in one kernel when every
+// row fits the register chunks (d % 8 == 0, d <= 2048, 16-byte aligned);
+// otherwise prichs_add then prichs_rmsnorm_forward.  Same results either way.
+int add_rmsnorm_forward(const void *a, int a_dtype, const void *b, int b_dtype, float *x1,
+                        const float *w, void *out, size_t T, size_t d, float eps, void *stream) {
+  PRICHS_REQUIRE(dtype_ok(a_dtype) && dtype_ok(b_dtype), "add_rmsnorm: bad dtype");
+  if (T == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(a && b && x1 && w && out, "add_rmsnorm: null pointer argument");
+  const bool fused = d % 8 == 0 && d <= 2048 &&
+                     ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                       reinterpret_cast<uintptr_t>(x1) | reinterpret_cast<uintptr_t>(w) |
+                       reinterpret_cast<uintptr_t>(out)) & 15) == 0 &&
+                     a_dtype == PRICHS_DTYPE_BF16 && b_dtype == PRICHS_DTYPE_BF16;
+  if (!fused) {
+    int rc = prichs_add(a, a_dtype, b, b_dtype, x1, PRICHS_DTYPE_F32, T * d, stream);
+    if (rc) return rc;
+    return prichs_rmsnorm_forward(x1, PRICHS_DTYPE_F32, w, out, PRICHS_DTYPE_BF16, nullptr, T, d,
+                                  eps, stream);
+  }
+  hipStream_t s = as_stream(stream);
+  const size_t nch = cdiv(d, (size_t)512);
+  if (nch <= 1)
+    launch_add_rmsnorm_nch<bf16_t, bf16_t, 1>(a, b, w, x1, out, T, d, eps, s);
+  else if (nch == 2)
+    launch_add_rmsnorm_nch<bf16_t, bf16_t, 2>(a, b, w, x1, out, T, d, eps, s);
+  else if (nch == 3)
+    launch_add_rmsnorm_nch<bf16_t, bf16_t, 3>(a, b, w, x1, out, T, d, eps, s);
+  else
+    launch_add_rmsnorm_nch<bf16_t, bf16_t, 4>(a, b, w, x1, out, T, d, eps, s);
+  PRICHS_LAUNCH_CHECK("add_rmsnorm launch");
+  return PRICHS_OK;
+}
+}  // namespace prichs
 
 extern "C" int prichs_add(const void *a, int a_dtype, const void *b, int b_dtype, void *out,
                           int out_dtype, size_t n, void *stream) {

@@ -163,6 +163,12 @@ def _check_block(orc, inp):
     st = {n: host(t) if t.dtype != torch.int32 else t.cpu().numpy()
           for n, t in blk.engine.stash().items()}
     r = orc.block_forward(inp)
+    # 0. The fused residual add + post-attention norm is bit-identical to an
+    #    f32 add of the bf16 operands followed by the stand-alone RMSNorm kernel.
+    np.testing.assert_array_equal(st["x1"], synth.round_bf16(inp.x) + st["attn_out"])
+    n2_alone, _ = ops.rmsnorm(dev(st["x1"], torch.float32), dev(inp.post_norm, torch.float32),
+                              eps=inp.eps, out_dtype=torch.bfloat16, want_rstd=False)
+    np.testing.assert_array_equal(st["normed2"], host(n2_alone))
     # 1. attention sub-layer (input: x itself, identical on both sides).
     e_att = rel_err(st["attn_out"], r["attn"])
     # 2. MoE sub-layer on the GPU's own normed2 (bf16 values): routing bit-exact.
