@@ -505,15 +505,15 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
       fetch(c + Cf::kRing, ring[j]);
       if (c < nch) {
         const float *wc = wrow + c * Cf::kKC;
-        // Pinned interleave: the chunk's weight reads run kAhead groups ahead
-        // of the products and sums (mask 0x100: LDS read, 0x2: VALU).
-        constexpr int kG = Cf::kKC / 4, kAhead = 6;
-        __builtin_amdgcn_sched_barrier(0);
+        // All of the chunk's weights are read at once (the LDS returns them
+        // in order while the sums run), and the products of group g + 1 are
+        // formed before the four dependent sums of group g, so each add waits
+        // only on the previous add.
+        constexpr int kG = Cf::kKC / 4;
+        f32x4 wv[kG];
 #pragma unroll
-        for (int g = 0; g < kG; ++g) {
-          const f32x4 wv = *reinterpret_cast<const f32x4 *>(wc + 4 * g);
-          // The four products first (independent), then the dependent sums.
-          float p[4];
+        for (int g = 0; g < kG; ++g) wv[g] = *reinterpret_cast<const f32x4 *>(wc + 4 * g);
+        auto products = [&](int g, float (&p)[4]) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int kk = 4 * g + q;  // holder lane kk / kQ, its value kk % kQ
@@ -524,18 +524,22 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
               case 2: xv = quad_bcast<2>(xf[kk % Cf::kQ]); break;
               default: xv = quad_bcast<3>(xf[kk % Cf::kQ]); break;
             }
-            p[q] = xv * wv[q];
+            p[q] = xv * wv[g][q];
           }
+        };
+        float pa[4], pb[4];
+        products(0, pa);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) acc = acc + p[q];
-        }
-        __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
+        for (int g = 0; g < kG; g += 2) {
+          if (g + 1 < kG) products(g + 1, pb);
 #pragma unroll
-        for (int g = 0; g < kG; ++g) {
-          __builtin_amdgcn_sched_group_barrier(0x2, 8, 0);
-          if (g + kAhead < kG) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          for (int q = 0; q < 4; ++q) acc = acc + pa[q];
+          if (g + 2 < kG) products(g + 2, pa);
+          if (g + 1 < kG) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = acc + pb[q];
+          }
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
