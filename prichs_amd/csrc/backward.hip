@@ -712,24 +712,27 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_f32_kernel(
 // comes transposed, wrt [E, d], so a selection's 8 columns are one vector
 // load.  The thread of column 0 also writes d_logit_j at the row of each
 // selection (dlr [T*k], in row-space order) for the router's weight gradient.
-template <typename T, typename OT>
+// KC: the top-k as a compile-time constant (k = 1, 2), or 0 for k at run time.
+template <typename T, typename OT, int KC>
 __global__ __launch_bounds__(256) void combine_kernel(
     const T *__restrict__ dX, const float *__restrict__ scal, const int32_t *__restrict__ topk_idx,
     const float *__restrict__ topk_w, const int32_t *__restrict__ token_row,
-    const float *__restrict__ wrt, int T_, int d, int k, int weighting,
+    const float *__restrict__ wrt, int T_, int d, int k_rt, int weighting,
     float *__restrict__ dlr, OT *__restrict__ d_x) {
 #pragma clang fp contract(off)
+  constexpr int kMax = KC > 0 ? KC : PRICHS_MAX_TOPK;
+  const int k = KC > 0 ? KC : k_rt;
   const int per_tok = d / 8;
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (long long)T_ * per_tok) return;
   const int t = (int)(gid / per_tok);
   const int c = (int)(gid - (long long)t * per_tok) * 8;
 
-  int ex[PRICHS_MAX_TOPK], rows[PRICHS_MAX_TOPK];
-  float wt[PRICHS_MAX_TOPK], dl[PRICHS_MAX_TOPK];
+  int ex[kMax], rows[kMax];
+  float wt[kMax], dl[kMax];
   float ws = 0.f;
 #pragma unroll
-  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+  for (int s = 0; s < kMax; ++s) {
     if (s < k) {
       ex[s] = topk_idx[(size_t)t * k + s];
       rows[s] = token_row[(size_t)t * k + s];
@@ -745,15 +748,15 @@ __global__ __launch_bounds__(256) void combine_kernel(
     }
   }
 #pragma unroll
-  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+  for (int s = 0; s < kMax; ++s) {
     const float diff = dl[s] - ws;
     dl[s] = s < k ? wt[s] * diff : 0.f;
   }
   // Ascending expert id (bubble passes over registers, as in the forward combine).
 #pragma unroll
-  for (int a = 0; a < PRICHS_MAX_TOPK - 1; ++a)
+  for (int a = 0; a < kMax - 1; ++a)
 #pragma unroll
-    for (int b = 0; b < PRICHS_MAX_TOPK - 1 - a; ++b)
+    for (int b = 0; b < kMax - 1 - a; ++b)
       if (ex[b] > ex[b + 1]) {
         int te = ex[b]; ex[b] = ex[b + 1]; ex[b + 1] = te;
         int tr = rows[b]; rows[b] = rows[b + 1]; rows[b + 1] = tr;
@@ -762,14 +765,14 @@ __global__ __launch_bounds__(256) void combine_kernel(
       }
   if (c == 0) {
 #pragma unroll
-    for (int s = 0; s < PRICHS_MAX_TOPK; ++s)
+    for (int s = 0; s < kMax; ++s)
       if (s < k) dlr[rows[s]] = dl[s];
   }
   float acc[8], v[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
 #pragma unroll
-  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+  for (int s = 0; s < kMax; ++s) {
     if (s < k) {
       V8<T>::load(dX + (size_t)rows[s] * d + c, v);
       const float wx = weighting == 2 ? wt[s] : 1.0f;
@@ -787,7 +790,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
   for (int j = 0; j < 8; ++j) rs[j] = 0.f;
 #pragma unroll
-  for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
+  for (int s = 0; s < kMax; ++s) {
     if (s < k) {
       V8<float>::load(wrt + (size_t)ex[s] * d + c, v);
 #pragma unroll
@@ -1097,10 +1100,19 @@ int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, cons
                 int weighting, int dtype, float *dlr, void *d_x, int dx_dtype, hipStream_t s) {
   if (T == 0) return PRICHS_OK;
   const unsigned grid = blocks_for((long long)T * (long long)(d / 8));
-#define PRICHS_BWD_COMBINE(TT, OT)                                                              \
-  hipLaunchKernelGGL((combine_kernel<TT, OT>), dim3(grid), dim3(256), 0, s,                    \
+#define PRICHS_BWD_COMBINE_K(TT, OT, KC)                                                        \
+  hipLaunchKernelGGL((combine_kernel<TT, OT, KC>), dim3(grid), dim3(256), 0, s,                \
                      static_cast<const TT *>(dX), scal, topk_idx, topk_w, token_row, wrt,      \
                      (int)T, (int)d, (int)k, weighting, dlr, static_cast<OT *>(d_x))
+#define PRICHS_BWD_COMBINE(TT, OT)         \
+  do {                                     \
+    if (k == 2)                            \
+      PRICHS_BWD_COMBINE_K(TT, OT, 2);     \
+    else if (k == 1)                       \
+      PRICHS_BWD_COMBINE_K(TT, OT, 1);     \
+    else                                   \
+      PRICHS_BWD_COMBINE_K(TT, OT, 0);     \
+  } while (0)
   if (dtype == PRICHS_DTYPE_BF16) {
     if (dx_dtype == PRICHS_DTYPE_BF16)
       PRICHS_BWD_COMBINE(bf16_t, bf16_t);
@@ -1113,6 +1125,7 @@ int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, cons
       PRICHS_BWD_COMBINE(float, float);
   }
 #undef PRICHS_BWD_COMBINE
+#undef PRICHS_BWD_COMBINE_K
   PRICHS_LAUNCH_CHECK("moe backward: combine");
   return PRICHS_OK;
 }

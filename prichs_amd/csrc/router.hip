@@ -645,12 +645,33 @@ __global__ __launch_bounds__(256) void permute_kernel(
   }
   __syncthreads();
   // Expert totals over all blocks and over the blocks before this one.
-  for (int i = tid; i < nb * E; i += blockDim.x) {
-    const int bb = i / E;
-    const int ee = i - bb * E;
-    const int c = block_counts[i];
-    atomicAdd(&tot_s[ee], c);
-    if (bb < b) atomicAdd(&pre_s[ee], c);
+  if ((blockDim.x % E) == 0 && (64 % E) == 0) {
+    // E divides the block and the wave (a power of two <= 64): every element a
+    // thread visits has expert tid % E, so it sums them in registers, the
+    // lanes of one expert reduce by shuffles, and each wave adds once per
+    // expert (integer sums: order-free).
+    int tot = 0, pre = 0;
+    for (int i = tid; i < nb * E; i += blockDim.x) {
+      const int c = block_counts[i];
+      tot += c;
+      if (i / E < b) pre += c;
+    }
+    for (int m = E; m < 64; m <<= 1) {
+      tot += __shfl_xor(tot, m);
+      pre += __shfl_xor(pre, m);
+    }
+    if ((tid & 63) < E) {
+      atomicAdd(&tot_s[tid & 63], tot);
+      atomicAdd(&pre_s[tid & 63], pre);
+    }
+  } else {
+    for (int i = tid; i < nb * E; i += blockDim.x) {
+      const int bb = i / E;
+      const int ee = i - bb * E;
+      const int c = block_counts[i];
+      atomicAdd(&tot_s[ee], c);
+      if (bb < b) atomicAdd(&pre_s[ee], c);
+    }
   }
   __syncthreads();
   if (tid == 0) {
