@@ -169,6 +169,15 @@ struct CheckpointMoe {
 int checkpoint_moe_weights(const prichs_checkpoint *ck, size_t layer, size_t d, size_t f,
                            size_t E, CheckpointMoe &w);
 
+// prichs_router_topk then prichs_permute; when one router workgroup covers
+// the batch (decode-sized T) the router writes the permutation itself
+// (router.hip).  Same outputs either way.
+int router_topk_permute(const void *x, int x_dtype, const float *w_router,
+                        const float *router_bias, const float *concept_bias, size_t n_concept,
+                        size_t T, size_t d, size_t E, size_t k, float *logits, int32_t *topk_idx,
+                        float *topk_w, int32_t *block_counts, int32_t *offsets,
+                        int32_t *row_token, float *row_weight, int32_t *token_row, void *stream);
+
 // The block's residual add and post-attention norm in one pass:
 // x1 = a + b (f32), out = rms_norm(x1, w) (bf16) (elementwise.hip).
 int add_rmsnorm_forward(const void *a, int a_dtype, const void *b, int b_dtype, float *x1,

@@ -397,14 +397,25 @@ extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, 
   const size_t rows = T * eng->k + eng->S * T;
   int rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[0], s), "engine_forward: event");
-  rc = prichs_router_topk(x, eng->dtype, eng->w_router, eng->router_bias, concept_bias, n_concept,
-                          T, eng->d, eng->E, eng->k, eng->logits, eng->topk_idx, eng->topk_w,
-                          eng->block_counts, stream);
-  if (rc) return rc;
-  if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[1], s), "engine_forward: event");
-  rc = prichs_permute(eng->topk_idx, eng->topk_w, eng->block_counts, T, eng->E, eng->k,
-                      eng->offsets, eng->row_token, eng->row_weight, eng->token_row, stream);
-  if (rc) return rc;
+  if (prichs_router_num_blocks(T, eng->E) == 1) {
+    // Decode-sized batch: the router's one workgroup also writes the
+    // permutation (the permute stage then times as zero).
+    rc = router_topk_permute(x, eng->dtype, eng->w_router, eng->router_bias, concept_bias,
+                             n_concept, T, eng->d, eng->E, eng->k, eng->logits, eng->topk_idx,
+                             eng->topk_w, eng->block_counts, eng->offsets, eng->row_token,
+                             eng->row_weight, eng->token_row, stream);
+    if (rc) return rc;
+    if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[1], s), "engine_forward: event");
+  } else {
+    rc = prichs_router_topk(x, eng->dtype, eng->w_router, eng->router_bias, concept_bias,
+                            n_concept, T, eng->d, eng->E, eng->k, eng->logits, eng->topk_idx,
+                            eng->topk_w, eng->block_counts, stream);
+    if (rc) return rc;
+    if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[1], s), "engine_forward: event");
+    rc = prichs_permute(eng->topk_idx, eng->topk_w, eng->block_counts, T, eng->E, eng->k,
+                        eng->offsets, eng->row_token, eng->row_weight, eng->token_row, stream);
+    if (rc) return rc;
+  }
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[2], s), "engine_forward: event");
   // No group holds more than T rows (a token picks an expert at most once).
   // With the backward enabled the GEMM also keeps the gate/up pre-activations.

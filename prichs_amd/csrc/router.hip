@@ -399,6 +399,56 @@ router_topk_staged_kernel(
   if (tid < E) block_counts[(size_t)blockIdx.x * E + tid] = cnt_s[tid];
 }
 
+// Places tokens [t0, t1)'s (token, slot) entries given each expert's first
+// row for them (base_s[e]), in (t, s) order, one 64-wide window per wave
+// step.  An expert occurs at most once per token, so (t, s) order within one
+// expert is token order; each entry's place is the expert's running base
+// plus the number of earlier entries of that expert in the window (a ballot
+// per expert).  The 64-lane windows are taken in order by wave 0 alone,
+// which keeps the running bases sequential.  All threads then write the
+// shared-expert rows, which follow the routed rows in token order.
+__device__ inline void place_entries(const int32_t *__restrict__ topk_idx,
+                                     const float *__restrict__ topk_w, int t0, int t1, int T,
+                                     int E, int k, const int *base_s, int32_t *__restrict__ row_token,
+                                     float *__restrict__ row_weight,
+                                     int32_t *__restrict__ token_row) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    const int lane = tid;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int base = lane < E ? base_s[lane] : 0;  // running base of expert `lane`
+    const size_t s0 = (size_t)t0 * k, s1 = (size_t)t1 * k;
+    for (size_t w0 = s0; w0 < s1; w0 += 64) {
+      const size_t ts = w0 + lane;
+      const bool live = ts < s1;
+      const int e_me = live ? topk_idx[ts] : -1;
+      const float wt = live ? topk_w[ts] : 0.0f;
+      int r = -1;
+      for (int e = 0; e < E; ++e) {
+        const uint64_t m = __ballot(e_me == e);
+        const int be = __shfl(base, e);
+        if (e_me == e) r = be + __popcll(m & lt);
+        if (lane == e) base += __popcll(m);
+      }
+      if (live && r >= 0) {
+        row_token[r] = (int32_t)(ts / k);
+        row_weight[r] = wt;
+        token_row[ts] = r;
+      }
+    }
+  }
+  for (int t = t0 + tid; t < t1; t += blockDim.x) row_token[(size_t)T * k + t] = t;
+}
+
+// Outputs of the permutation, filled by the router's own workgroup when one
+// workgroup covers every token (decode-sized batches); offsets == nullptr
+// leaves the permutation to permute_kernel.
+struct FusedPerm {
+  int32_t *offsets, *row_token;
+  float *row_weight;
+  int32_t *token_row;
+};
+
 // ---------------------------------------------------------------------------
 // Quad-broadcast router (E <= 8, eight lanes per token, d % 128 == 0).  The
 // block's router weights sit transposed in LDS for the whole kernel (staged
@@ -428,7 +478,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
     const XT *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     const float *__restrict__ concept, int n_concept, int T, int d, int E, int k,
     float *__restrict__ logits, int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
-    int32_t *__restrict__ block_counts) {
+    int32_t *__restrict__ block_counts, FusedPerm perm) {
 #pragma clang fp contract(off)
   using Cf = QuadRouter<XT>;
   constexpr int kTpb = kRouterThreads / 8;
@@ -553,12 +603,32 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
   topk_epilogue(acc, adj, valid, e, t, T, E, k, 8, logits, topk_idx, topk_w, cnt_s);
   __syncthreads();
   if (tid < E) block_counts[(size_t)blockIdx.x * E + tid] = cnt_s[tid];
+  if (perm.offsets != nullptr) {
+    // The only workgroup: the histogram is the expert totals, the exclusive
+    // scan gives the bases (as permute_kernel's block 0 computes them), and
+    // the block's entries (written above, visible after the barrier) are
+    // placed here.
+    __shared__ int base_s[PRICHS_MAX_EXPERTS];
+    if (tid == 0) {
+      int run = 0;
+      for (int ee = 0; ee < E; ++ee) {
+        base_s[ee] = run;
+        perm.offsets[ee] = run;
+        run += cnt_s[ee];
+      }
+      perm.offsets[E] = run;  // == T * k
+      perm.offsets[E + 1] = run + T;
+    }
+    __syncthreads();
+    place_entries(topk_idx, topk_w, 0, T, T, E, k, base_s, perm.row_token, perm.row_weight,
+                  perm.token_row);
+  }
 }
 
 template <typename XT>
 int launch_quad_t(const XT *x, const float *w, const float *bias, const float *concept, int nc,
                   int T, int d, int E, int k, float *logits, int32_t *idx, float *wt, int32_t *bc,
-                  int nb, hipStream_t s) {
+                  int nb, hipStream_t s, FusedPerm perm = FusedPerm{nullptr, nullptr, nullptr, nullptr}) {
   const size_t lds = (size_t)8 * (d + 4) * sizeof(float);
   static int attr_bytes = 0;
   if ((int)lds > attr_bytes) {
@@ -568,7 +638,7 @@ int launch_quad_t(const XT *x, const float *w, const float *bias, const float *c
     attr_bytes = (int)lds;
   }
   hipLaunchKernelGGL((router_topk_quad_kernel<XT>), dim3(nb), dim3(kRouterThreads), lds, s, x, w,
-                     bias, concept, nc, T, d, E, k, logits, idx, wt, bc);
+                     bias, concept, nc, T, d, E, k, logits, idx, wt, bc, perm);
   return PRICHS_OK;
 }
 
@@ -687,40 +757,8 @@ __global__ __launch_bounds__(256) void permute_kernel(
     }
   }
   __syncthreads();
-  const int t0 = b * tpb;
-  const int t1 = min(T, t0 + tpb);
-  // The block's (token, slot) entries in (t, s) order, one 64-wide window per
-  // wave step.  An expert occurs at most once per token, so (t, s) order
-  // within one expert is token order; each entry's place is the expert's
-  // running base plus the number of earlier entries of that expert in the
-  // window (a ballot per expert).  The 64-lane windows are taken in order by
-  // wave 0 alone, which keeps the running bases sequential.
-  if (tid < 64) {
-    const int lane = tid;
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int base = lane < E ? base_s[lane] : 0;  // running base of expert `lane`
-    const size_t s0 = (size_t)t0 * k, s1 = (size_t)t1 * k;
-    for (size_t w0 = s0; w0 < s1; w0 += 64) {
-      const size_t ts = w0 + lane;
-      const bool live = ts < s1;
-      const int e_me = live ? topk_idx[ts] : -1;
-      const float wt = live ? topk_w[ts] : 0.0f;
-      int r = -1;
-      for (int e = 0; e < E; ++e) {
-        const uint64_t m = __ballot(e_me == e);
-        const int be = __shfl(base, e);
-        if (e_me == e) r = be + __popcll(m & lt);
-        if (lane == e) base += __popcll(m);
-      }
-      if (live && r >= 0) {
-        row_token[r] = (int32_t)(ts / k);
-        row_weight[r] = wt;
-        token_row[ts] = r;
-      }
-    }
-  }
-  // Shared-expert rows follow the routed rows in token order.
-  for (int t = t0 + tid; t < t1; t += blockDim.x) row_token[(size_t)T * k + t] = t;
+  place_entries(topk_idx, topk_w, b * tpb, min(T, (b + 1) * tpb), T, E, k, base_s, row_token,
+                row_weight, token_row);
 }
 
 template <typename XT, int LPT, int KC>
@@ -770,11 +808,14 @@ extern "C" size_t prichs_router_num_blocks(size_t T, size_t E) {
   return cdiv(T, (size_t)tpb);
 }
 
-extern "C" int prichs_router_topk(const void *x, int x_dtype, const float *w_router,
-                                  const float *router_bias, const float *concept_bias,
-                                  size_t n_concept, size_t T, size_t d, size_t E, size_t k,
-                                  float *logits, int32_t *topk_idx, float *topk_w,
-                                  int32_t *block_counts, void *stream) {
+// The router; with perm.offsets set and a batch one workgroup covers, the
+// quad kernel also writes the permutation (*fused = true).
+static int router_topk_impl(const void *x, int x_dtype, const float *w_router,
+                            const float *router_bias, const float *concept_bias, size_t n_concept,
+                            size_t T, size_t d, size_t E, size_t k, float *logits,
+                            int32_t *topk_idx, float *topk_w, int32_t *block_counts, void *stream,
+                            FusedPerm perm, bool *fused) {
+  *fused = false;
   PRICHS_REQUIRE(dtype_ok(x_dtype), "router: bad x dtype %d", x_dtype);
   PRICHS_REQUIRE(E >= 1 && E <= PRICHS_MAX_EXPERTS, "router: E=%zu outside [1, %d]", E,
                  PRICHS_MAX_EXPERTS);
@@ -800,14 +841,16 @@ extern "C" int prichs_router_topk(const void *x, int x_dtype, const float *w_rou
   const bool quad = staged && lg == 3 && d % 128 == 0 && (size_t)8 * (d + 4) * 4 <= 150 * 1024 &&
                     PRICHS_ROUTER_QUAD;
   if (quad) {
+    if (nb != 1 || perm.offsets == nullptr) perm = FusedPerm{nullptr, nullptr, nullptr, nullptr};
     int rc = x_dtype == PRICHS_DTYPE_BF16
                  ? launch_quad_t<bf16_t>(static_cast<const bf16_t *>(x), w_router, router_bias,
                                          concept_bias, nc, (int)T, (int)d, (int)E, (int)k, logits,
-                                         topk_idx, topk_w, block_counts, nb, s)
+                                         topk_idx, topk_w, block_counts, nb, s, perm)
                  : launch_quad_t<float>(static_cast<const float *>(x), w_router, router_bias,
                                         concept_bias, nc, (int)T, (int)d, (int)E, (int)k, logits,
-                                        topk_idx, topk_w, block_counts, nb, s);
+                                        topk_idx, topk_w, block_counts, nb, s, perm);
     if (rc) return rc;
+    *fused = perm.offsets != nullptr;
   } else if (staged) {
     int rc = x_dtype == PRICHS_DTYPE_BF16
                  ? launch_staged<bf16_t>(lg, static_cast<const bf16_t *>(x), w_router,
@@ -834,6 +877,39 @@ extern "C" int prichs_router_topk(const void *x, int x_dtype, const float *w_rou
   PRICHS_LAUNCH_CHECK("router_topk launch");
   return PRICHS_OK;
 }
+
+extern "C" int prichs_router_topk(const void *x, int x_dtype, const float *w_router,
+                                  const float *router_bias, const float *concept_bias,
+                                  size_t n_concept, size_t T, size_t d, size_t E, size_t k,
+                                  float *logits, int32_t *topk_idx, float *topk_w,
+                                  int32_t *block_counts, void *stream) {
+  bool fused;
+  return router_topk_impl(x, x_dtype, w_router, router_bias, concept_bias, n_concept, T, d, E, k,
+                          logits, topk_idx, topk_w, block_counts, stream,
+                          FusedPerm{nullptr, nullptr, nullptr, nullptr}, &fused);
+}
+
+namespace prichs {
+int router_topk_permute(const void *x, int x_dtype, const float *w_router,
+                        const float *router_bias, const float *concept_bias, size_t n_concept,
+                        size_t T, size_t d, size_t E, size_t k, float *logits, int32_t *topk_idx,
+                        float *topk_w, int32_t *block_counts, int32_t *offsets,
+                        int32_t *row_token, float *row_weight, int32_t *token_row,
+                        void *stream) {
+  bool fused = false;
+  if (T > 0) {
+    PRICHS_REQUIRE(offsets && row_token && row_weight && token_row,
+                   "router_permute: null permutation output");
+    int rc = router_topk_impl(x, x_dtype, w_router, router_bias, concept_bias, n_concept, T, d, E,
+                              k, logits, topk_idx, topk_w, block_counts, stream,
+                              FusedPerm{offsets, row_token, row_weight, token_row}, &fused);
+    if (rc) return rc;
+  }
+  if (fused) return PRICHS_OK;
+  return prichs_permute(topk_idx, topk_w, block_counts, T, E, k, offsets, row_token, row_weight,
+                        token_row, stream);
+}
+}  // namespace prichs
 
 extern "C" int prichs_permute(const int32_t *topk_idx, const float *topk_w,
                               const int32_t *block_counts, size_t T, size_t E, size_t k,

@@ -220,6 +220,16 @@ def test_moe_layer_decode_shapes(cuda, orc, T):
     np.testing.assert_array_equal(stash.selected_experts, r["sel"])
     np.testing.assert_array_equal(stash.row_token, r["row_token"])
     assert rel_err(out, r["out"]) <= TOL["bf16"]
+    # Up to 32 tokens the router's single workgroup writes the permutation
+    # itself; every permutation output equals the separate permute kernel's.
+    _, idx, w, bc = ops.router_topk(dev(inp.x, inp.dtype), dev(inp.w_router),
+                                    dev(inp.router_bias), inp.k)
+    off, rt, rw, tr = ops.permute(idx, w, bc, inp.E)
+    h = layer.engine.stash()
+    np.testing.assert_array_equal(host(h["offsets"]), host(off))
+    np.testing.assert_array_equal(host(h["row_token"]), host(rt))
+    np.testing.assert_array_equal(host(h["row_weight"]).view(np.uint32), host(rw).view(np.uint32))
+    np.testing.assert_array_equal(host(h["token_row"]), host(tr))
     layer.engine.close()
 
 
