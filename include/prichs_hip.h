@@ -404,7 +404,11 @@ int prichs_moe_engine_stash(const prichs_moe_engine *eng,
  * stage_ms waits for those forwards and writes the AVERAGE milliseconds of:
  * [0] router, [1] permute, [2] gate/up GEMM, [3] down GEMM, [4] combine,
  * [5] whole forward; *n_forwards (may be NULL) gets the number averaged.
- * It then re-arms recording for another n forwards. */
+ * It then re-arms recording for another n forwards.  When one router
+ * workgroup covers the batch (decode-sized T), the router also writes the
+ * permutation and [1] times only the gap between two events.  Each event
+ * costs a few microseconds on the stream, so time throughput with timing
+ * off. */
 #define PRICHS_NUM_STAGES 6
 int prichs_moe_engine_set_timing(prichs_moe_engine *eng, int max_forwards);
 int prichs_moe_engine_stage_ms(prichs_moe_engine *eng, float *ms_out,
