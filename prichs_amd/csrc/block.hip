@@ -9,7 +9,8 @@
 //   attn = causal GQA attention(q, k, v)            prichs_attention_forward
 //   x1 = x + attn Wo                                prichs_gemm, then one kernel for the
 //   n2 = rms_norm(x1, post_attn_norm)               residual add (x1 in f32) and the norm
-//   out = x1 + MoE(n2)                              prichs_moe_engine_forward + prichs_add
+//   out = x1 + MoE(n2)                              the MoE engine forward, whose combine
+//                                                   also adds x1
 // Everything is allocated at creation; a forward is a fixed sequence of
 // launches on one stream with no host synchronisation.
 #include <cstring>
@@ -270,10 +271,8 @@ extern "C" int prichs_block_engine_forward(prichs_block_engine *eng, const void 
   if ((rc = add_rmsnorm_forward(x, bf, eng->attn_out, bf, eng->x1, eng->post_norm, eng->n2, T, d,
                                  eng->eps, stream)))
     return rc;
-  if ((rc = prichs_moe_engine_forward(eng->moe, eng->n2, T, concept_bias, n_concept, eng->moe_out,
-                                      bf, stream)))
-    return rc;
-  if ((rc = prichs_add(eng->x1, PRICHS_DTYPE_F32, eng->moe_out, bf, out, out_dtype, T * d, stream)))
+  if ((rc = moe_engine_forward_residual(eng->moe, eng->n2, T, concept_bias, n_concept,
+                                       eng->moe_out, eng->x1, out, out_dtype, stream)))
     return rc;
   eng->last_T = T;
   return PRICHS_OK;

@@ -178,6 +178,17 @@ int router_topk_permute(const void *x, int x_dtype, const float *w_router,
                         float *topk_w, int32_t *block_counts, int32_t *offsets,
                         int32_t *row_token, float *row_weight, int32_t *token_row, void *stream);
 
+// moe_out = the MoE combine (bf16) and out = res + moe_out (the block's final
+// residual add) in one kernel (elementwise.hip).
+int moe_combine_residual(const void *y, const int32_t *topk_idx, const float *topk_w,
+                         const int32_t *token_row, size_t T, size_t d, size_t k, int has_shared,
+                         void *moe_out, const float *res, void *out, int out_dtype, void *stream);
+// prichs_moe_engine_forward whose combine also adds the f32 residual:
+// moe_out gets the layer output (bf16), out = residual + moe_out (engine.hip).
+int moe_engine_forward_residual(prichs_moe_engine *eng, const void *x, size_t T,
+                                const float *concept_bias, size_t n_concept, void *moe_out,
+                                const float *residual, void *out, int out_dtype, void *stream);
+
 // The block's residual add and post-attention norm in one pass:
 // x1 = a + b (f32), out = rms_norm(x1, w) (bf16) (elementwise.hip).
 int add_rmsnorm_forward(const void *a, int a_dtype, const void *b, int b_dtype, float *x1,

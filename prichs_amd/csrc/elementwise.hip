@@ -134,6 +134,78 @@ __global__ __launch_bounds__(256) void combine_kernel(
   }
 }
 
+// The block's MoE combine followed by its final residual add in one pass
+// (crates/prichs-model/src/block.rs:50-68): moe = the combine above (rounded
+// to bf16 into moe_out, the sub-layer output), then out = res + moe with res
+// the f32 residual x1, rounded to OT -- the arithmetic of combine_kernel
+// followed by add_kernel, so both outputs are bit-identical to that pair.
+template <typename OT, int KC>
+__global__ __launch_bounds__(256) void combine_residual_kernel(
+    const bf16_t *__restrict__ y, const int32_t *__restrict__ topk_idx,
+    const float *__restrict__ topk_w, const int32_t *__restrict__ token_row, int T, int d,
+    int k_rt, int has_shared, bf16_t *__restrict__ moe_out, const float *__restrict__ res,
+    OT *__restrict__ out) {
+#pragma clang fp contract(off)
+  constexpr int kMax = KC > 0 ? KC : PRICHS_MAX_TOPK;
+  const int k = KC > 0 ? KC : k_rt;
+  const int per_tok = d / 8;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (long long)T * per_tok) return;
+  const int t = (int)(gid / per_tok);
+  const int c = (int)(gid - (long long)t * per_tok) * 8;
+  int ex[kMax], rows[kMax];
+  float wt[kMax];
+#pragma unroll
+  for (int s = 0; s < kMax; ++s) {
+    if (s < k) {
+      ex[s] = topk_idx[(size_t)t * k + s];
+      rows[s] = token_row[(size_t)t * k + s];
+      wt[s] = topk_w[(size_t)t * k + s];
+    } else {
+      ex[s] = 0x7fffffff;
+      rows[s] = 0;
+      wt[s] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < kMax - 1; ++a)
+#pragma unroll
+    for (int b = 0; b < kMax - 1 - a; ++b)
+      if (ex[b] > ex[b + 1]) {
+        int te = ex[b]; ex[b] = ex[b + 1]; ex[b + 1] = te;
+        int tr = rows[b]; rows[b] = rows[b + 1]; rows[b + 1] = tr;
+        float tw = wt[b]; wt[b] = wt[b + 1]; wt[b + 1] = tw;
+      }
+  V8 acc;
+  if (has_shared) {
+    acc = ld8(y + ((size_t)T * k + t) * d + c);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc.v[j] = 0.f;
+  }
+#pragma unroll
+  for (int s = 0; s < kMax; ++s) {
+    if (s < k) {
+      const V8 yv = ld8(y + (size_t)rows[s] * d + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = wt[s] * yv.v[j];
+        acc.v[j] = acc.v[j] + p;
+      }
+    }
+  }
+  const size_t o = (size_t)t * d + c;
+  st8(moe_out + o, acc);
+  const V8 r = ld8(res + o);
+  V8 sum;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float m = bf16_to_f32(f32_to_bf16(acc.v[j]));  // the stored (rounded) moe value
+    sum.v[j] = r.v[j] + m;
+  }
+  st8(out + o, sum);
+}
+
 // ------------------------------------------------------------- RMSNorm --
 // One wave64 per row (crates/prichs-core/src/ops.rs:109-135):
 // inv = 1/sqrt(sum(x^2)/d + eps), out = (x * inv) * w.
@@ -514,6 +586,53 @@ int add_rmsnorm_forward(const void *a, int a_dtype, const void *b, int b_dtype, 
   else
     launch_add_rmsnorm_nch<bf16_t, bf16_t, 4>(a, b, w, x1, out, T, d, eps, s);
   PRICHS_LAUNCH_CHECK("add_rmsnorm launch");
+  return PRICHS_OK;
+}
+}  // namespace prichs
+
+namespace prichs {
+// moe_out = combine (bf16) and out = res + moe_out in one kernel when the
+// vector path applies (bf16 y, d % 8 == 0, 16-byte aligned); otherwise
+// prichs_moe_combine then prichs_add.  Same results either way.
+int moe_combine_residual(const void *y, const int32_t *topk_idx, const float *topk_w,
+                         const int32_t *token_row, size_t T, size_t d, size_t k, int has_shared,
+                         void *moe_out, const float *res, void *out, int out_dtype,
+                         void *stream) {
+  PRICHS_REQUIRE(dtype_ok(out_dtype), "combine_residual: bad out dtype");
+  PRICHS_REQUIRE(k >= 1 && k <= PRICHS_MAX_TOPK, "combine_residual: bad k=%zu", k);
+  if (T == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(y && topk_idx && topk_w && token_row && moe_out && res && out,
+                 "combine_residual: null pointer argument");
+  const bool fused = d % 8 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(moe_out) |
+                       reinterpret_cast<uintptr_t>(res) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  if (!fused) {
+    int rc = prichs_moe_combine(y, PRICHS_DTYPE_BF16, topk_idx, topk_w, token_row, T, d, k,
+                                has_shared, moe_out, PRICHS_DTYPE_BF16, stream);
+    if (rc) return rc;
+    return prichs_add(res, PRICHS_DTYPE_F32, moe_out, PRICHS_DTYPE_BF16, out, out_dtype, T * d,
+                      stream);
+  }
+  hipStream_t s = as_stream(stream);
+  const unsigned grid = grid_for(T * (d / 8));
+#define PRICHS_COMBINE_RES(OT_, KC_)                                                          \
+  hipLaunchKernelGGL((combine_residual_kernel<OT_, KC_>), dim3(grid), dim3(256), 0, s,        \
+                     static_cast<const bf16_t *>(y), topk_idx, topk_w, token_row, (int)T,     \
+                     (int)d, (int)k, has_shared, static_cast<bf16_t *>(moe_out), res,         \
+                     static_cast<OT_ *>(out))
+  if (out_dtype == PRICHS_DTYPE_BF16) {
+    if (k == 2)
+      PRICHS_COMBINE_RES(bf16_t, 2);
+    else
+      PRICHS_COMBINE_RES(bf16_t, 0);
+  } else {
+    if (k == 2)
+      PRICHS_COMBINE_RES(float, 2);
+    else
+      PRICHS_COMBINE_RES(float, 0);
+  }
+#undef PRICHS_COMBINE_RES
+  PRICHS_LAUNCH_CHECK("combine_residual launch");
   return PRICHS_OK;
 }
 }  // namespace prichs

@@ -370,9 +370,12 @@ extern "C" int prichs_moe_engine_get_router_bias(const prichs_moe_engine *eng, f
   return PRICHS_OK;
 }
 
-extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, size_t T,
-                                         const float *concept_bias, size_t n_concept, void *out,
-                                         int out_dtype, void *stream) {
+// The forward; with residual != nullptr the combine writes the layer output
+// to moe_out (bf16) and residual + that output to out (the block's final
+// residual add, in the same kernel).
+static int moe_forward_impl(prichs_moe_engine *eng, const void *x, size_t T,
+                            const float *concept_bias, size_t n_concept, void *out, int out_dtype,
+                            void *stream, const float *residual, void *moe_out) {
   PRICHS_REQUIRE(eng != nullptr, "engine_forward: null engine");
   PRICHS_REQUIRE(dtype_ok(out_dtype), "engine_forward: bad out dtype %d", out_dtype);
   if (!eng->uploaded) return fail(PRICHS_ERR_STATE, "engine_forward: weights not uploaded");
@@ -428,8 +431,19 @@ extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, 
                          eng->dtype, eng->y, stream);
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[4], s), "engine_forward: event");
-  rc = prichs_moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T,
-                          eng->d, eng->k, (int)eng->S, out, out_dtype, stream);
+  if (residual != nullptr && eng->dtype == PRICHS_DTYPE_BF16) {
+    rc = moe_combine_residual(eng->y, eng->topk_idx, eng->topk_w, eng->token_row, T, eng->d,
+                              eng->k, (int)eng->S, moe_out, residual, out, out_dtype, stream);
+  } else if (residual != nullptr) {
+    rc = prichs_moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T,
+                            eng->d, eng->k, (int)eng->S, moe_out, PRICHS_DTYPE_BF16, stream);
+    if (!rc)
+      rc = prichs_add(residual, PRICHS_DTYPE_F32, moe_out, PRICHS_DTYPE_BF16, out, out_dtype,
+                      T * eng->d, stream);
+  } else {
+    rc = prichs_moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T,
+                            eng->d, eng->k, (int)eng->S, out, out_dtype, stream);
+  }
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[5], s), "engine_forward: event");
   if (tm) ++eng->recorded;
@@ -437,6 +451,24 @@ extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, 
   eng->stash_valid = true;
   return PRICHS_OK;
 }
+
+extern "C" int prichs_moe_engine_forward(prichs_moe_engine *eng, const void *x, size_t T,
+                                         const float *concept_bias, size_t n_concept, void *out,
+                                         int out_dtype, void *stream) {
+  return moe_forward_impl(eng, x, T, concept_bias, n_concept, out, out_dtype, stream, nullptr,
+                          nullptr);
+}
+
+namespace prichs {
+int moe_engine_forward_residual(prichs_moe_engine *eng, const void *x, size_t T,
+                                const float *concept_bias, size_t n_concept, void *moe_out,
+                                const float *residual, void *out, int out_dtype, void *stream) {
+  PRICHS_REQUIRE(residual != nullptr && moe_out != nullptr,
+                 "engine_forward_residual: null residual or moe_out");
+  return moe_forward_impl(eng, x, T, concept_bias, n_concept, out, out_dtype, stream, residual,
+                          moe_out);
+}
+}  // namespace prichs
 
 extern "C" int prichs_moe_engine_enable_backward(prichs_moe_engine *eng) {
   PRICHS_REQUIRE(eng != nullptr, "engine_enable_backward: null engine");

@@ -169,6 +169,11 @@ def _check_block(orc, inp):
     n2_alone, _ = ops.rmsnorm(dev(st["x1"], torch.float32), dev(inp.post_norm, torch.float32),
                               eps=inp.eps, out_dtype=torch.bfloat16, want_rstd=False)
     np.testing.assert_array_equal(st["normed2"], host(n2_alone))
+    #    The final residual add rides in the MoE combine: out = x1 + moe_out
+    #    (f32 add of the bf16 sub-layer output), bit for bit, in f32 and bf16.
+    np.testing.assert_array_equal(out, st["x1"] + st["moe_out"])
+    out_bf = host(blk.engine.forward(x, inp.batch, inp.seq_len, out_dtype=torch.bfloat16))
+    np.testing.assert_array_equal(out_bf, synth.round_bf16(st["x1"] + st["moe_out"]))
     # 1. attention sub-layer (input: x itself, identical on both sides).
     e_att = rel_err(st["attn_out"], r["attn"])
     # 2. MoE sub-layer on the GPU's own normed2 (bf16 values): routing bit-exact.
