@@ -257,6 +257,52 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT *__restrict__ x,
   }
 }
 
+// RMSNorm of rows with d <= 512 * NCH, each row held in registers between the sum of squares
+// and the scaling (one read of x instead of two); the operations and the
+// order of the sum are rmsnorm_kernel's vector path, so the results are
+// bit-identical to it.
+template <typename XT, typename OT, int NCH>
+__global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const XT *__restrict__ x,
+                                                          const float *__restrict__ w,
+                                                          OT *__restrict__ out,
+                                                          float *__restrict__ rstd, int T, int d,
+                                                          float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const size_t base = (size_t)row * d;
+  V8 v[NCH];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane * 8 + 512 * i;
+    if (c < d) {
+      v[i] = ld8(x + base + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = ss + v[i].v[j] * v[i].v[j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float rms = sqrtf(ss / (float)d + eps);
+  const float inv = 1.0f / rms;
+  if (rstd != nullptr && lane == 0) rstd[row] = inv;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane * 8 + 512 * i;
+    if (c < d) {
+      const V8 wv = ld8(w + c);
+      V8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = v[i].v[j] * inv;
+        o.v[j] = a * wv.v[j];
+      }
+      st8(out + base + c, o);
+    }
+  }
+}
+
 // ------------------------------------------------- residual add + RMSNorm --
 // The block's x1 = x + attn_out (f32) and n2 = rms_norm(x1, w) in one pass
 // (crates/prichs-model/src/block.rs:50-68; ops.rs:109-135, 250-267): one wave
@@ -398,6 +444,10 @@ void launch_rmsnorm_t(const void *x, const float *w, void *out, float *rstd, siz
   const bool vec = d % 8 == 0 && aligned16(static_cast<const XT *>(x)) &&
                    aligned16(static_cast<OT *>(out)) && aligned16(w);
   auto kern = vec ? rmsnorm_kernel<XT, OT, true> : rmsnorm_kernel<XT, OT, false>;
+  if (vec && d <= 1024)
+    kern = d <= 512 ? rmsnorm_reg_kernel<XT, OT, 1> : rmsnorm_reg_kernel<XT, OT, 2>;
+  else if (vec && d <= 2048)
+    kern = d <= 1536 ? rmsnorm_reg_kernel<XT, OT, 3> : rmsnorm_reg_kernel<XT, OT, 4>;
   hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s,
                      static_cast<const XT *>(x), w, static_cast<OT *>(out), rstd, (int)T, (int)d,
                      eps);
