@@ -592,6 +592,73 @@ int prichs_moe_engine_upload_checkpoint(prichs_moe_engine *eng, const prichs_che
 int prichs_block_engine_upload_checkpoint(prichs_block_engine *eng, const prichs_checkpoint *ck,
                                           size_t layer, const float *router_bias);
 
+/* ---------------------------------------------------------------------- */
+/* 6. General f32 GEMMs: the GPU dispatch target of prichs-core's CPU ops   */
+/*    (crates/prichs-core/src/ops.rs:3, 24-31; crates/prichs-cuda/src/      */
+/*    cublas.rs:46-327, re-exported at crates/prichs-cuda/src/lib.rs:6-8)   */
+/* ---------------------------------------------------------------------- */
+
+/* Operations, in the reference's (m, k, n) naming (cublas.rs:117, 170, 221):
+ *   PRICHS_MATMUL_AB:  a [m, k], b [k, n]  -> c [m, n] = a b
+ *   PRICHS_MATMUL_ATB: a [m, k], b [m, n]  -> c [k, n] = a^T b
+ *   PRICHS_MATMUL_ABT: a [m, k], b [n, k]  -> c [m, n] = a b^T
+ * All row-major f32, any sizes (0 included: c = 0 when the reduction is
+ * empty).  f32 products and accumulation on v_mfma_f32_16x16x4f32. */
+enum { PRICHS_MATMUL_AB = 0, PRICHS_MATMUL_ATB = 1, PRICHS_MATMUL_ABT = 2 };
+
+/* Device pointers, enqueued on `stream`; c is overwritten. */
+int prichs_matmul_f32(int op, const float *a, const float *b, float *c, size_t m,
+                      size_t k, size_t n, void *stream);
+
+/* GpuWorkspace (cublas.rs:46-115): three device slabs for A, B and C, sized in
+ * bytes; 0 selects the reference's sizes (16 MB, 32 MB, 16 MB,
+ * cublas.rs:77-84).  The workspace belongs to the device current at
+ * creation.  A handle is not internally synchronised. */
+typedef struct prichs_gpu_workspace prichs_gpu_workspace;
+int prichs_gpu_workspace_create(size_t a_bytes, size_t b_bytes, size_t c_bytes,
+                                prichs_gpu_workspace **out);
+int prichs_gpu_workspace_destroy(prichs_gpu_workspace *ws);
+/* Slab sizes in bytes (any output pointer may be NULL). */
+int prichs_gpu_workspace_slabs(const prichs_gpu_workspace *ws, size_t *a_bytes,
+                               size_t *b_bytes, size_t *c_bytes);
+
+/* Host slices in and out, synchronous: H2D into slabs A and B, the product
+ * into slab C, D2H, device synchronisation.  Operands larger than their slab
+ * fail with PRICHS_ERR_CAPACITY before any copy (the reference's "Matrix
+ * dimensions exceed preallocated GPU workspace slabs" bail).
+ *   matmul      : c  [m, n] = a [m, k] b [k, n]          (cublas.rs:117-166)
+ *   matmul_at_b : dw [k, n] = a [m, k]^T b [m, n]         (cublas.rs:170-219)
+ *   matmul_a_bt : dx [m, n] = dy [m, k] w [n, k]^T        (cublas.rs:221-268)
+ * dw and dx are overwritten, like the reference's GPU path (beta = 0); the
+ * reference's CPU matmul_at_b instead adds to dw (ops.rs:72-80). */
+int prichs_gpu_workspace_matmul(prichs_gpu_workspace *ws, const float *a,
+                                const float *b, float *c, size_t m, size_t k,
+                                size_t n);
+int prichs_gpu_workspace_matmul_at_b(prichs_gpu_workspace *ws, const float *a,
+                                     const float *b, float *dw, size_t m, size_t k,
+                                     size_t n);
+int prichs_gpu_workspace_matmul_a_bt(prichs_gpu_workspace *ws, const float *dy,
+                                     const float *w, float *dx, size_t m, size_t k,
+                                     size_t n);
+
+/* get_gpu_workspace (cublas.rs:283-300): the process-wide workspace with the
+ * reference's slab sizes, created on first use on the then-current device;
+ * NULL (with the reason in prichs_last_error) if that creation failed, and
+ * every later call then returns NULL too, as the reference's Lazy does. */
+prichs_gpu_workspace *prichs_get_gpu_workspace(void);
+
+/* matmul_gpu / matmul_at_b_gpu / matmul_a_bt_gpu (cublas.rs:302-327): the
+ * workspace methods above on the process-wide workspace, serialised by one
+ * mutex (the reference's Mutex<GpuWorkspace>).  Without a workspace they
+ * return PRICHS_ERR_HIP ("GPU workspace unavailable"), the status on which
+ * prichs-core falls back to its CPU loop (ops.rs:27-31). */
+int prichs_matmul_gpu(const float *a, const float *b, float *c, size_t m, size_t k,
+                      size_t n);
+int prichs_matmul_at_b_gpu(const float *a, const float *b, float *dw, size_t m,
+                           size_t k, size_t n);
+int prichs_matmul_a_bt_gpu(const float *dy, const float *w, float *dx, size_t m,
+                           size_t k, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

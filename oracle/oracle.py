@@ -39,6 +39,10 @@ def lib():
         sz = C.c_size_t
         L.orc_matmul_2d.argtypes = [_f32p, _f32p, _f32p, sz, sz, sz]
         L.orc_matmul_2d.restype = None
+        L.orc_matmul_at_b.argtypes = [_f32p, _f32p, _f32p, sz, sz, sz]
+        L.orc_matmul_at_b.restype = None
+        L.orc_matmul_a_bt.argtypes = [_f32p, _f32p, _f32p, sz, sz, sz]
+        L.orc_matmul_a_bt.restype = None
         L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, sz, sz, C.c_float]
         L.orc_rms_norm.restype = None
         L.orc_silu.argtypes = [C.c_float]
@@ -102,6 +106,28 @@ def matmul_2d(a, b):
     assert k == k2
     out = np.empty((m, n), np.float32)
     lib().orc_matmul_2d(a, b, out, m, k, n)
+    return out
+
+
+def matmul_at_b(a, b, dw=None):
+    """ops.rs:63-83 CPU branch: dw += a^T b (dw [k, n] starts at zero when None)."""
+    a, b = _c(a), _c(b)
+    m, k = a.shape
+    m2, n = b.shape
+    assert m == m2
+    out = np.zeros((k, n), np.float32) if dw is None else np.array(dw, np.float32, copy=True)
+    lib().orc_matmul_at_b(a, b, out, m, k, n)
+    return out
+
+
+def matmul_a_bt(dy, w):
+    """ops.rs:85-107 CPU branch: dx = dy w^T (w [n, k])."""
+    dy, w = _c(dy), _c(w)
+    m, k = dy.shape
+    n, k2 = w.shape
+    assert k == k2
+    out = np.empty((m, n), np.float32)
+    lib().orc_matmul_a_bt(dy, w, out, m, k, n)
     return out
 
 

@@ -20,6 +20,12 @@
  * Pinning (what checks each function besides this restatement):
  *   orc_matmul_2d            GEMM known-answer test (engine.rs:2881-2910),
  *                            float64 recomputation, exact small-integer case.
+ *   orc_matmul_at_b / orc_matmul_a_bt
+ *                            bit-identical to orc_matmul_2d on the transposed
+ *                            operand (the same summation order), the GEMM
+ *                            KAT's backward-data and -weight products
+ *                            (engine.rs:2912-2936), float64 recomputation;
+ *                            at_b accumulates into dw (its loop adds).
  *   orc_rms_norm             KAT row [2,2,2,2] -> 1.0 (engine.rs:3041-3053),
  *                            float64 closed form.
  *   orc_swiglu / orc_silu    closed form in float64, silu(0)=0, odd/limit cases.
@@ -80,6 +86,49 @@ ORC_API void orc_matmul_2d(const float *a, const float *b, float *out,
         float prod = a_val * b_row[j];
         out_row[j] = out_row[j] + prod;
       }
+    }
+  }
+}
+
+/* crates/prichs-core/src/ops.rs:63-83, CPU branch of matmul_at_b: dW[k, n]
+ * += A[m, k]^T B[m, n].  For each row i of dW, t ascending, j ascending:
+ * dw[i][j] = dw[i][j] + a[t][i] * b[t][j] (product rounded, then the sum).
+ * Like the reference's CPU loop it ACCUMULATES into dw (its GPU branch,
+ * cublas.rs:170-219, overwrites). */
+ORC_API void orc_matmul_at_b(const float *a, const float *b, float *dw,
+                             size_t m, size_t k, size_t n) {
+  long long ii;
+#pragma omp parallel for schedule(static)
+  for (ii = 0; ii < (long long)k; ++ii) {
+    float *dw_row = dw + (size_t)ii * n;
+    for (size_t t = 0; t < m; ++t) {
+      const float a_val = a[t * k + (size_t)ii];
+      const float *b_row = b + t * n;
+      for (size_t j = 0; j < n; ++j) {
+        float prod = a_val * b_row[j];
+        dw_row[j] = dw_row[j] + prod;
+      }
+    }
+  }
+}
+
+/* ops.rs:85-107, CPU branch of matmul_a_bt: dX[m, n] = dY[m, k] W[n, k]^T,
+ * each element a sequential dot product from 0 over c ascending (the result
+ * overwrites dx). */
+ORC_API void orc_matmul_a_bt(const float *dy, const float *w, float *dx,
+                             size_t m, size_t k, size_t n) {
+  long long mi;
+#pragma omp parallel for schedule(static)
+  for (mi = 0; mi < (long long)m; ++mi) {
+    const float *dy_row = dy + (size_t)mi * k;
+    for (size_t j = 0; j < n; ++j) {
+      const float *w_row = w + j * k;
+      float dot = 0.0f;
+      for (size_t c = 0; c < k; ++c) {
+        float prod = dy_row[c] * w_row[c];
+        dot = dot + prod;
+      }
+      dx[(size_t)mi * n + j] = dot;
     }
   }
 }

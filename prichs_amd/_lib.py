@@ -148,7 +148,21 @@ SIGNATURES = {
     "prichs_moe_engine_enable_backward": (_i, [_vp]),
     "prichs_moe_engine_backward_stage_ms": (_i, [_vp, C.POINTER(_f), C.POINTER(_i)]),
     "prichs_moe_engine_backward": (_i, [_vp, _vp, _vp, _sz, _vp, _i, C.POINTER(MoEGrads), _i, _vp]),
+    "prichs_matmul_f32": (_i, [_i, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "prichs_gpu_workspace_create": (_i, [_sz, _sz, _sz, C.POINTER(_vp)]),
+    "prichs_gpu_workspace_destroy": (_i, [_vp]),
+    "prichs_gpu_workspace_slabs": (_i, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
+    "prichs_gpu_workspace_matmul": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz]),
+    "prichs_gpu_workspace_matmul_at_b": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz]),
+    "prichs_gpu_workspace_matmul_a_bt": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz]),
+    "prichs_get_gpu_workspace": (_vp, []),
+    "prichs_matmul_gpu": (_i, [_vp, _vp, _vp, _sz, _sz, _sz]),
+    "prichs_matmul_at_b_gpu": (_i, [_vp, _vp, _vp, _sz, _sz, _sz]),
+    "prichs_matmul_a_bt_gpu": (_i, [_vp, _vp, _vp, _sz, _sz, _sz]),
 }
+MATMUL_AB = 0
+MATMUL_ATB = 1
+MATMUL_ABT = 2
 
 _lib = None
 

@@ -68,6 +68,11 @@ constexpr int kBf16KMultiple = 64;   // bf16 kernels need d and f to be multiple
 #ifndef PRICHS_BAND_M
 #define PRICHS_BAND_M 4
 #endif
+// K loop of the bf16 tiles: 1 = ping-pong (wave groups alternate MFMA and
+// memory phases), 0 = both groups in step.
+#ifndef PRICHS_PINGPONG
+#define PRICHS_PINGPONG 1
+#endif
 
 // ------------------------------------------------------------------------
 // Tile scheduler shared by the kernels.
@@ -264,14 +269,18 @@ __device__ __forceinline__ void bf16_tile(
   const int m0 = (mt - tm.prefix[g]) * BM;
   const int n0 = nt * BN;
 
-  uint32_t a_goff[kInstA], b_goff[kInstB];
+  // A offsets are 64-bit (gathered rows: src * lda can pass 2^32 elements for
+  // a large row space); B offsets stay within one group's packed weights,
+  // which the host bounds to 2^32 elements.
+  long long a_goff[kInstA];
+  uint32_t b_goff[kInstB];
 #pragma unroll
   for (int i = 0; i < kInstA; ++i) {
     int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
     lr = lr < mg ? lr : mg - 1;  // rows past the group repeat its last row
     const int vr = row0 + lr;
     const int src = a_rows ? a_rows[vr] : vr;
-    a_goff[i] = (uint32_t)src * (uint32_t)lda + (uint32_t)(dma_chunk * 8);
+    a_goff[i] = (long long)src * lda + dma_chunk * 8;
   }
 #pragma unroll
   for (int i = 0; i < kInstB; ++i) {
@@ -309,6 +318,69 @@ __device__ __forceinline__ void bf16_tile(
     for (int w = 0; w < kInstPerStage; ++w) issue_one(kt_, w);
   };
 
+#if PRICHS_PINGPONG
+  // Ping-pong K loop.  Waves 0-3 (group 0) and 4-7 (group 1) sit one per
+  // SIMD each, so every SIMD hosts one wave of each group.  Every wave runs
+  // the same sequence per K-step kt -- a memory phase (read its fragments of
+  // stage kt from LDS, issue its share of stage kt + 3, wait for its share of
+  // stage kt + 1 and for its own LDS reads), a barrier, an MFMA phase on
+  // those fragments, a barrier -- but group 1 starts one barrier late, so on
+  // each SIMD one wave issues MFMAs while the other does its LDS reads and
+  // DMA, and they swap at every barrier: between barriers b(2kt) and
+  // b(2kt+1) group 0 multiplies stage kt while group 1 reads it; between
+  // b(2kt+1) and b(2kt+2) group 1 multiplies it while group 0 reads stage
+  // kt + 1.
+  //  - Stage s is first read after b(2s-1); both groups waited for their
+  //    shares of it in their memory phases of step s - 1, which end at b(2s-2)
+  //    and b(2s-1).
+  //  - The share of stage kt + 3 issued in step kt's memory phase goes to
+  //    stage kt - 1's slot; both groups' LDS reads of stage kt - 1 completed
+  //    before b(2kt-2) and b(2kt-1), and step kt's memory phases start after
+  //    b(2kt-1) and b(2kt).
+  // Each output element is the same MFMA chain over K as with the in-step
+  // loop, so the results are bit-identical.
+  const int grp = wave >> 2;
+  // Barrier that nothing is scheduled across (MFMAs touch no memory, so the
+  // memory clobber alone would let the scheduler move them over it).
+  auto pp_barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  struct Frags {
+    bf16x8 w[NJ], a[MI];
+  } F;
+  auto read_frags = [&](int st) {
+    const bf16_t *as = lds + (st & (kStages - 1)) * kStageElems;
+    const bf16_t *bs = as + BM * BK;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj)
+      F.w[jj] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + jj * 16 * BK);
+#pragma unroll
+    for (int ii = 0; ii < MI; ++ii)
+      F.a[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + ii * 16 * BK);
+  };
+  issue_stage(0);
+  if (KT > 1) issue_stage(1);
+  if (KT > 2) issue_stage(2);
+  wait_vmcnt(min(2, KT - 1) * kInstPerStage);  // own share of stage 0
+  pp_barrier();
+  if (grp == 1) pp_barrier();  // group 1 runs one phase behind
+  for (int kt = 0; kt < KT; ++kt) {
+    read_frags(kt);
+    if (kt + 3 < KT) issue_stage(kt + 3);
+    // Own shares still allowed in flight: stages kt + 2 .. min(kt + 3, KT - 1).
+    wait_vmcnt(max(0, min(kt + 3, KT - 1) - kt - 1) * kInstPerStage);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS reads done
+    pp_barrier();
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(F.w[j], F.a[i], acc[i][j]);
+    pp_barrier();
+  }
+  if (grp == 0) pp_barrier();  // both groups leave after the same barrier count
+#else
   // Prologue: stages 0..3 in flight; stage 0 lands and is read.
   issue_stage(0);
   if (KT > 1) issue_stage(1);
@@ -410,6 +482,8 @@ __device__ __forceinline__ void bf16_tile(
     ++kt;
   }
   step(kt, bool_c<false>{}, bool_c<true>{}, fa, fb);
+
+#endif
 
   // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
   //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
@@ -929,6 +1003,12 @@ int check_gemm_shape(size_t d, size_t f, int dtype, const char *who) {
                 who, d, f, q);
   if (d > (1u << 20) || f > (1u << 20))
     return fail(PRICHS_ERR_UNSUPPORTED, "%s: d=%zu or f=%zu too large", who, d, f);
+  // The kernels address one group's packed weights with 32-bit element
+  // offsets: [Np, d] gate/up (Np <= 2 roundup(f, 32) + 256) and [roundup(d,
+  // 256), f] down must stay below 2^32 elements.
+  if ((2 * roundup(f, 32) + 256) * d > (size_t)UINT32_MAX || roundup(d, 256) * f > (size_t)UINT32_MAX)
+    return fail(PRICHS_ERR_UNSUPPORTED, "%s: packed weights of d=%zu, f=%zu exceed 2^32 elements",
+                who, d, f);
   return PRICHS_OK;
 }
 
@@ -1183,9 +1263,8 @@ int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const vo
   PRICHS_REQUIRE(lda >= K && ldc >= n_store && n_store <= Np && lda % 8 == 0 && ldc % 4 == 0,
                  "grouped gemm: lda=%zu, ldc=%zu, n_store=%zu invalid for K=%zu, Np=%zu", lda,
                  ldc, n_store, K, Np);
-  PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX && max_rows * lda <= (size_t)UINT32_MAX &&
-                     max_rows * ldc <= (size_t)UINT32_MAX &&
-                     b_group_stride * G <= (size_t)INT64_MAX,
+  PRICHS_REQUIRE(max_rows <= (size_t)INT32_MAX && lda <= (size_t)INT32_MAX &&
+                     ldc <= (size_t)INT32_MAX && b_group_stride * G <= (size_t)INT64_MAX,
                  "grouped gemm: operands too large");
   return launch_grouped(false, A, a_rows, (int)lda, B, (long long)b_group_stride, (int)Np,
                         (int)K, C, (int)ldc, (int)n_store, offsets, (int)G, 0, max_rows, dtype,
@@ -1230,8 +1309,7 @@ extern "C" int prichs_gemm(const void *a, size_t lda, size_t M, size_t K, const 
                            size_t N, void *c, size_t ldc, int dtype, void *stream) {
   if (int rc = check_gemm_shape(N, K, dtype, "gemm")) return rc;
   PRICHS_REQUIRE(lda >= K && ldc >= N, "gemm: lda=%zu < K=%zu or ldc=%zu < N=%zu", lda, K, ldc, N);
-  PRICHS_REQUIRE(M <= (size_t)INT32_MAX && lda <= (size_t)INT32_MAX && ldc <= (size_t)INT32_MAX &&
-                     M * lda <= (size_t)UINT32_MAX,
+  PRICHS_REQUIRE(M <= (size_t)INT32_MAX && lda <= (size_t)INT32_MAX && ldc <= (size_t)INT32_MAX,
                  "gemm: M=%zu or leading dimensions too large", M);
   PRICHS_REQUIRE(lda % 8 == 0 && ldc % 4 == 0, "gemm: lda must be a multiple of 8, ldc of 4");
   if (M == 0) return PRICHS_OK;

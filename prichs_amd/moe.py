@@ -184,8 +184,9 @@ class MoEEngine:
         out["n"] = n.value
         return out
 
-    def stash(self) -> dict:
-        """Device views (cloned) of the last forward's intermediates (the MoEStash)."""
+    def stash(self, names=None) -> dict:
+        """Device views (cloned) of the last forward's intermediates (the MoEStash);
+        `names` selects a subset."""
         st = L.MoEStash()
         L.check(self.lib.prichs_moe_engine_stash(self.handle, C.byref(st)))
         T, k, E, S = st.T, self.k, self.E, self.S
@@ -202,7 +203,7 @@ class MoEEngine:
             "act": _device_tensor(st.act, (rows, self.f), gdt),
             "y": _device_tensor(st.y, (rows, self.d), gdt),
         }
-        return {name: t.clone() for name, t in v.items()}
+        return {name: t.clone() for name, t in v.items() if names is None or name in names}
 
 
 @dataclass

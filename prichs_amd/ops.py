@@ -220,6 +220,30 @@ def gemm(a, w_packed, N, out=None, stream=None):
     return out
 
 
+def matmul_f32(op, a, b, out=None, stream=None):
+    """prichs_matmul_f32 on f32 device tensors, in the reference's (m, k, n)
+    naming: op MATMUL_AB: a [m, k] @ b [k, n]; MATMUL_ATB: a [m, k]^T @ b [m, n];
+    MATMUL_ABT: a [m, k] @ b [n, k]^T.  Any sizes."""
+    lib = L.load()
+    a, b = _dev(a), _dev(b)
+    if a.dtype != torch.float32 or b.dtype != torch.float32:
+        raise TypeError("matmul_f32 takes float32 tensors")
+    m, k = a.shape
+    if op == L.MATMUL_AB:
+        assert b.shape[0] == k
+        n, shape = b.shape[1], (m, b.shape[1])
+    elif op == L.MATMUL_ATB:
+        assert b.shape[0] == m
+        n, shape = b.shape[1], (k, b.shape[1])
+    else:
+        assert b.shape[1] == k
+        n, shape = b.shape[0], (m, b.shape[0])
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=a.device)
+    L.check(lib.prichs_matmul_f32(op, _p(a), _p(b), _p(_dev(out)), m, k, n, _stream(stream)))
+    return out
+
+
 def add(a, b, out_dtype=None, stream=None):
     """prichs_add: a + b in f32 arithmetic."""
     lib = L.load()

@@ -157,6 +157,46 @@ def test_engine_argument_errors(lib):
                                            None), L.PRICHS_ERR_INVALID_ARGUMENT, "null pointer")
 
 
+def test_matmul_argument_errors(lib):
+    p = C.c_void_p(16)
+    _expect(lib.prichs_matmul_f32(3, p, p, p, 2, 2, 2, None), L.PRICHS_ERR_INVALID_ARGUMENT,
+            "unknown op")
+    _expect(lib.prichs_matmul_f32(L.MATMUL_AB, None, p, p, 2, 2, 2, None),
+            L.PRICHS_ERR_INVALID_ARGUMENT, "null")
+    _expect(lib.prichs_matmul_f32(L.MATMUL_ABT, p, p, p, 2**40, 2**20, 2, None),
+            L.PRICHS_ERR_INVALID_ARGUMENT, "too large")
+    # an empty output is a no-op before any pointer is used
+    assert lib.prichs_matmul_f32(L.MATMUL_AB, None, None, None, 0, 5, 7, None) == L.PRICHS_OK
+    assert lib.prichs_matmul_f32(L.MATMUL_ATB, None, None, None, 5, 0, 7, None) == L.PRICHS_OK
+    for fn in (lib.prichs_gpu_workspace_matmul, lib.prichs_gpu_workspace_matmul_at_b,
+               lib.prichs_gpu_workspace_matmul_a_bt):
+        _expect(fn(None, p, p, p, 2, 2, 2), L.PRICHS_ERR_INVALID_ARGUMENT, "null workspace")
+    _expect(lib.prichs_gpu_workspace_slabs(None, None, None, None), L.PRICHS_ERR_INVALID_ARGUMENT,
+            "null workspace")
+    _expect(lib.prichs_gpu_workspace_create(0, 0, 0, None), L.PRICHS_ERR_INVALID_ARGUMENT, "null")
+    assert lib.prichs_gpu_workspace_destroy(None) == L.PRICHS_OK
+
+
+def test_process_wide_workspace_absent_without_a_gpu(lib):
+    # get_gpu_workspace is None when the workspace cannot be created
+    # (cublas.rs:285-296), and matmul_gpu then fails with "GPU workspace
+    # unavailable" (cublas.rs:302-309) -- prichs-core's cue to use its CPU loop.
+    import torch
+
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is visible: the workspace exists")
+    from prichs_amd import workspace
+
+    assert lib.prichs_get_gpu_workspace() is None
+    assert "unavailable" in L.last_error()
+    assert workspace.get_gpu_workspace() is None
+    out = np.zeros(6, np.float32)
+    with pytest.raises(L.PrichsError) as e:
+        workspace.matmul_gpu(np.ones(8, np.float32), np.ones(12, np.float32), out, 2, 4, 3)
+    assert e.value.status == L.PRICHS_ERR_HIP and "unavailable" in e.value.message
+    assert not out.any()
+
+
 # ----------------------------------------------------------------- packing --
 @pytest.mark.parametrize("dtype", [L.DTYPE_F32, L.DTYPE_BF16])
 def test_pack_gate_up_layout(lib, dtype):

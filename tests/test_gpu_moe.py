@@ -156,14 +156,12 @@ def test_grouped_gemms_against_oracle(cuda, orc, cfg):
     h_off, h_rt = host(off), host(rt)
     h_act, h_y = host(act), host(y)
     tol = TOL[inp.dtype]
-    rng = np.random.default_rng(0)
+    # Every row of every group (config 2: 24,576 rows).
     for g in range(G):
         r0, r1 = h_off[g], h_off[g + 1]
         if r1 == r0:
             continue
         sel = np.arange(r0, r1)
-        if sel.size > 256:
-            sel = np.sort(rng.choice(sel, 256, replace=False))
         j = order[g]
         xr = inp.x[h_rt[sel]]
         ga = orc.matmul_2d(xr, inp.gate[j])
@@ -272,10 +270,9 @@ def test_moe_layer_full_against_oracle(cuda, orc, cfg):
     layer.engine.close()
 
 
-def test_moe_layer_skewed_config3_sampled_rows(cuda, orc):
-    # Full size (16384 tokens, ~60% of rows on experts 0-1).  Routing and the
-    # permutation are checked on every token; outputs on 384 sampled tokens
-    # (per-token results do not depend on the rest of the batch).
+def test_moe_layer_skewed_config3_full(cuda, orc):
+    # Full size (16384 tokens, ~60% of rows on experts 0-1): routing, the
+    # permutation and the output of every token against the oracle.
     inp = synth.config_inputs(3)
     say("layer skew", inp.T)
     layer = moe.MoELayer.from_inputs(inp)
@@ -287,11 +284,37 @@ def test_moe_layer_skewed_config3_sampled_rows(cuda, orc):
     o_off, o_rt, _, _ = orc.bin_tokens(rs, stash.gating_weights, inp.E)
     np.testing.assert_array_equal(stash.expert_offsets, o_off)
     np.testing.assert_array_equal(stash.row_token, o_rt)
-    rows = np.sort(np.random.default_rng(3).choice(inp.T, 384, replace=False))
-    sub = synth.MoEInputs(**{**inp.__dict__, "x": inp.x[rows], "T": len(rows)})
-    r = orc.moe_forward(sub)
-    assert rel_err(out[rows], r["out"]) <= TOL["bf16"]
+    r = orc.moe_forward(inp)
+    np.testing.assert_array_equal(stash.row_token, r["row_token"])
+    assert rel_err(out, r["out"]) <= TOL["bf16"]
     layer.engine.close()
+
+
+def test_moe_row_space_past_2_32_elements(cuda, orc):
+    # A configuration-2 layer over T = 1.2M tokens: the down GEMM's A operand
+    # (act, T (k + 1) x f = 4.6e9 elements) and y (5.5e9) pass 2^32 elements,
+    # so the shared rows of the last ~245k tokens sit past any 32-bit element
+    # offset.  Rows are independent (test_moe_rows_are_independent), so the
+    # first and last tokens are checked against the oracle on those tokens
+    # alone: routing bit-exact, outputs within 2e-2.
+    T = 1_200_000
+    inp = synth.config_inputs(2, T=64)
+    say("large row space", T)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((T, inp.d), generator=gen, device="cuda").to(torch.bfloat16)
+    eng = moe.MoEEngine(inp.d, inp.f, inp.E, inp.k, 1, "bf16", max_tokens=T)
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    out = eng.forward(x)
+    assert (T * (inp.k + 1) - 1) * inp.f >= 2**32
+    rows = torch.cat([torch.arange(0, 64), torch.arange(T - 256, T)]).cuda()
+    got = out[rows].float().cpu().numpy()
+    sel = eng.stash(["selected_experts"])["selected_experts"][rows].cpu().numpy()
+    sub = synth.MoEInputs(**{**inp.__dict__, "x": x[rows].float().cpu().numpy(), "T": len(rows)})
+    r = orc.moe_forward(sub)
+    np.testing.assert_array_equal(sel, r["sel"])
+    assert rel_err(got, r["out"]) <= TOL["bf16"]
+    del x, out
+    eng.close()
 
 
 def test_moe_forward_deterministic_and_ragged(cuda, orc):

@@ -50,6 +50,39 @@ def test_gemm_sums_k_in_ascending_order(orc):
     assert orc.matmul_2d(a2, b)[0, 0] == 1.0
 
 
+def test_gemm_backward_products_known_answer_from_reference(orc):
+    # engine.rs:2912-2936: dX = dY W^T (backward_data_gemm) and dW = x^T dY
+    # (backward_weight_gemm) on the KAT's data, CPU triple loops within 1e-4.
+    w = np.arange(1, 13, dtype=np.float32).reshape(4, 3)
+    x = np.array([[1.0, 0.5, 0.2, 0.1], [2.0, 1.0, 0.0, -1.0]], np.float32)
+    dy = np.array([[0.5, -0.5, 1.0], [1.0, 2.0, -1.0]], np.float32)
+    dx = orc.matmul_a_bt(dy, w)
+    assert np.abs(dx - np.array([[2.5, 5.5, 8.5, 11.5], [2.0, 8.0, 14.0, 20.0]])).max() < 1e-4
+    dw = orc.matmul_at_b(x, dy)
+    assert np.abs(dw - np.array([[2.5, 3.5, -1.0], [1.25, 1.75, -0.5], [0.1, -0.1, 0.2],
+                                 [-0.95, -2.05, 1.1]])).max() < 1e-4
+
+
+def test_gemm_backward_products_share_the_forward_order(orc):
+    # ops.rs:72-80 sums dw[i][j] over t ascending and ops.rs:97-104 dx[i][j] over
+    # c ascending, each product rounded then added, from 0: the order of
+    # matmul_2d (ops.rs:49-56) on the transposed operand, so bit-identical.
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((33, 19)).astype(np.float32)
+    b = rng.standard_normal((33, 21)).astype(np.float32)
+    np.testing.assert_array_equal(orc.matmul_at_b(a, b), orc.matmul_2d(a.T.copy(), b))
+    w = rng.standard_normal((21, 19)).astype(np.float32)
+    np.testing.assert_array_equal(orc.matmul_a_bt(a, w), orc.matmul_2d(a, w.T.copy()))
+    assert rel_err(orc.matmul_at_b(a, b), a.T.astype(np.float64) @ b) < 1e-6
+    assert rel_err(orc.matmul_a_bt(a, w), a.astype(np.float64) @ w.T) < 1e-6
+    # The CPU matmul_at_b adds to dw (ops.rs:72-80): starting from dw0 it is
+    # dw0 + A^T B up to rounding, and exactly A^T B from zero.
+    dw0 = rng.standard_normal((19, 21)).astype(np.float32)
+    acc = orc.matmul_at_b(a, b, dw0)
+    assert rel_err(acc, dw0.astype(np.float64) + a.T.astype(np.float64) @ b) < 1e-6
+    assert not np.array_equal(acc, orc.matmul_at_b(a, b))
+
+
 # -------------------------------------------------------------- RMSNorm --
 def test_rmsnorm_known_answer_from_reference(orc):
     # engine.rs:3041-3053: row [2,2,2,2], w = 1 -> 1.0 within 1e-4.
