@@ -659,6 +659,35 @@ int prichs_matmul_at_b_gpu(const float *a, const float *b, float *dw, size_t m,
 int prichs_matmul_a_bt_gpu(const float *dy, const float *w, float *dx, size_t m,
                            size_t k, size_t n);
 
+/* ---------------------------------------------------------------------- */
+/* 7. MoE layer forward that allocates nothing                             */
+/* ---------------------------------------------------------------------- */
+
+/* No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It computes prichs_moe_engine_forward
+ * (same kernels, same results) without an engine: the caller passes x [T, d]
+ * of `dtype`, w_router f32 [d, E], router_bias f32 [E], the packed weights of
+ * the n_shared + E experts in the grouped GEMMs' group order (routed 0..E-1,
+ * then the shared expert; one prichs_pack_gate_up / prichs_pack_down block
+ * each, prichs_packed_gate_up_elems / prichs_packed_down_elems apart), the
+ * optional concept bias and out [T, d] of out_dtype -- all device memory.
+ * The intermediates (the engine's workspace for T tokens: logits, top-k,
+ * permutation, act [T (k + n_shared), f], y [T (k + n_shared), d], 256-byte
+ * aligned pieces) live in a library-owned static device array of
+ * PRICHS_NOALLOC_SCRATCH_BYTES per GPU; a T that does not fit fails with
+ * PRICHS_ERR_CAPACITY before any GPU work (at d = 1536, f = 1280, E = 8,
+ * k = 2 about 1,900 tokens fit).  Nothing is allocated or freed.  Calls on
+ * one GPU share the array: two calls that overlap on one GPU (other streams
+ * or threads) race on it. */
+#define PRICHS_NOALLOC_SCRATCH_BYTES (32u << 20)
+int prichs_moe_forward_noalloc(const void *x, size_t T, size_t d, size_t f, size_t E,
+                               size_t k, size_t n_shared, int dtype,
+                               const float *w_router, const float *router_bias,
+                               const void *w_gate_up, const void *w_down,
+                               const float *concept_bias, size_t n_concept, void *out,
+                               int out_dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

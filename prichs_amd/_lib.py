@@ -159,7 +159,10 @@ SIGNATURES = {
     "prichs_matmul_gpu": (_i, [_vp, _vp, _vp, _sz, _sz, _sz]),
     "prichs_matmul_at_b_gpu": (_i, [_vp, _vp, _vp, _sz, _sz, _sz]),
     "prichs_matmul_a_bt_gpu": (_i, [_vp, _vp, _vp, _sz, _sz, _sz]),
+    "prichs_moe_forward_noalloc": (_i, [_vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _vp, _vp, _vp, _vp,
+                                        _vp, _sz, _vp, _i, _vp]),
 }
+NOALLOC_SCRATCH_BYTES = 32 << 20
 MATMUL_AB = 0
 MATMUL_ATB = 1
 MATMUL_ABT = 2
