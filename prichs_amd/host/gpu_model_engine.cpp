@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "prichs_hip.h"
 
@@ -486,6 +487,85 @@ std::vector<float> GpuModelEngine::moe_router_bias(size_t layer_id) const {
   lib_ok(prichs_moe_engine_get_router_bias(layers_[layer_id].eng, b.data()),
          "prichs_moe_engine_get_router_bias");
   return b;
+}
+
+// ---- GpuWorkspace and the host-slice GEMMs (cublas.rs:46-327) -------------
+namespace {
+void need(const std::vector<float> &v, size_t elems, const char *what) {
+  if (v.size() < elems) bail(fmt("%s holds %zu elements, %zu needed", what, v.size(), elems));
+}
+}  // namespace
+
+GpuWorkspace::GpuWorkspace(size_t a_bytes, size_t b_bytes, size_t c_bytes) {
+  lib_ok(prichs_gpu_workspace_create(a_bytes, b_bytes, c_bytes, &ws_), "GpuWorkspace::new");
+}
+
+GpuWorkspace::GpuWorkspace(prichs_gpu_workspace *borrowed) : ws_(borrowed), owned_(false) {}
+
+GpuWorkspace::~GpuWorkspace() {
+  if (owned_ && ws_) (void)prichs_gpu_workspace_destroy(ws_);
+}
+
+void GpuWorkspace::matmul(const std::vector<float> &a, const std::vector<float> &b,
+                          std::vector<float> &c, size_t m, size_t k, size_t n) const {
+  need(a, m * k, "a");
+  need(b, k * n, "b");
+  need(c, m * n, "c");
+  lib_ok(prichs_gpu_workspace_matmul(ws_, a.data(), b.data(), c.data(), m, k, n), "matmul");
+}
+
+void GpuWorkspace::matmul_at_b(const std::vector<float> &a, const std::vector<float> &b,
+                               std::vector<float> &dw, size_t m, size_t k, size_t n) const {
+  need(a, m * k, "a");
+  need(b, m * n, "b");
+  need(dw, k * n, "dw");
+  lib_ok(prichs_gpu_workspace_matmul_at_b(ws_, a.data(), b.data(), dw.data(), m, k, n),
+         "matmul_at_b");
+}
+
+void GpuWorkspace::matmul_a_bt(const std::vector<float> &dy, const std::vector<float> &w,
+                               std::vector<float> &dx, size_t m, size_t k, size_t n) const {
+  need(dy, m * k, "dy");
+  need(w, n * k, "w");
+  need(dx, m * n, "dx");
+  lib_ok(prichs_gpu_workspace_matmul_a_bt(ws_, dy.data(), w.data(), dx.data(), m, k, n),
+         "matmul_a_bt");
+}
+
+GpuWorkspace *get_gpu_workspace() {
+  static GpuWorkspace *wrapped = nullptr;
+  static std::mutex mu;
+  std::lock_guard<std::mutex> lock(mu);
+  if (wrapped == nullptr) {
+    prichs_gpu_workspace *ws = prichs_get_gpu_workspace();
+    if (ws == nullptr) return nullptr;
+    wrapped = new GpuWorkspace(ws);
+  }
+  return wrapped;
+}
+
+void matmul_gpu(const std::vector<float> &a, const std::vector<float> &b, std::vector<float> &c,
+                size_t m, size_t k, size_t n) {
+  need(a, m * k, "a");
+  need(b, k * n, "b");
+  need(c, m * n, "c");
+  lib_ok(prichs_matmul_gpu(a.data(), b.data(), c.data(), m, k, n), "matmul_gpu");
+}
+
+void matmul_at_b_gpu(const std::vector<float> &a, const std::vector<float> &b,
+                     std::vector<float> &dw, size_t m, size_t k, size_t n) {
+  need(a, m * k, "a");
+  need(b, m * n, "b");
+  need(dw, k * n, "dw");
+  lib_ok(prichs_matmul_at_b_gpu(a.data(), b.data(), dw.data(), m, k, n), "matmul_at_b_gpu");
+}
+
+void matmul_a_bt_gpu(const std::vector<float> &dy, const std::vector<float> &w,
+                     std::vector<float> &dx, size_t m, size_t k, size_t n) {
+  need(dy, m * k, "dy");
+  need(w, n * k, "w");
+  need(dx, m * n, "dx");
+  lib_ok(prichs_matmul_a_bt_gpu(dy.data(), w.data(), dx.data(), m, k, n), "matmul_a_bt_gpu");
 }
 
 }  // namespace prichs_host

@@ -23,6 +23,7 @@
 #include <vector>
 
 struct prichs_moe_engine;
+struct prichs_gpu_workspace;
 
 namespace prichs_host {
 
@@ -173,5 +174,49 @@ class GpuModelEngine {
   std::vector<PackedGemm *> packed_;
   std::vector<MoeLayer> layers_;
 };
+
+// GpuWorkspace (crates/prichs-cuda/src/cublas.rs:46-268) over
+// prichs_gpu_workspace_*: device slabs for A, B and C (sizes in bytes; 0 = the
+// reference's 16 MB / 32 MB / 16 MB) and the three host-slice GEMMs, each
+// H2D, GEMM, D2H and a device synchronisation.  Slices must hold at least the
+// elements (m, k, n) name; an operand larger than its slab throws the
+// reference's "exceed preallocated GPU workspace slabs" error.  dw / dx are
+// overwritten, like the reference's GPU path.
+class GpuWorkspace {
+ public:
+  explicit GpuWorkspace(size_t a_bytes = 0, size_t b_bytes = 0, size_t c_bytes = 0);
+  ~GpuWorkspace();
+  GpuWorkspace(const GpuWorkspace &) = delete;
+  GpuWorkspace &operator=(const GpuWorkspace &) = delete;
+
+  // cublas.rs:117-166: c [m, n] = a [m, k] b [k, n].
+  void matmul(const std::vector<float> &a, const std::vector<float> &b, std::vector<float> &c,
+              size_t m, size_t k, size_t n) const;
+  // cublas.rs:170-219: dw [k, n] = a [m, k]^T b [m, n].
+  void matmul_at_b(const std::vector<float> &a, const std::vector<float> &b,
+                   std::vector<float> &dw, size_t m, size_t k, size_t n) const;
+  // cublas.rs:221-268: dx [m, n] = dy [m, k] w [n, k]^T.
+  void matmul_a_bt(const std::vector<float> &dy, const std::vector<float> &w,
+                   std::vector<float> &dx, size_t m, size_t k, size_t n) const;
+
+ private:
+  friend GpuWorkspace *get_gpu_workspace();
+  explicit GpuWorkspace(prichs_gpu_workspace *borrowed);  // the process-wide one
+  prichs_gpu_workspace *ws_ = nullptr;
+  bool owned_ = true;
+};
+
+// get_gpu_workspace (cublas.rs:283-300): the process-wide workspace, or null
+// when it could not be created (no device).
+GpuWorkspace *get_gpu_workspace();
+// matmul_gpu / matmul_at_b_gpu / matmul_a_bt_gpu (cublas.rs:302-327): the
+// methods above on the process-wide workspace, serialised by one mutex;
+// without a workspace they throw "GPU workspace unavailable".
+void matmul_gpu(const std::vector<float> &a, const std::vector<float> &b, std::vector<float> &c,
+                size_t m, size_t k, size_t n);
+void matmul_at_b_gpu(const std::vector<float> &a, const std::vector<float> &b,
+                     std::vector<float> &dw, size_t m, size_t k, size_t n);
+void matmul_a_bt_gpu(const std::vector<float> &dy, const std::vector<float> &w,
+                     std::vector<float> &dx, size_t m, size_t k, size_t n);
 
 }  // namespace prichs_host

@@ -104,6 +104,50 @@ void test_persistent_vram_gemm_correctness() {
   CHECK(back[0] == w_host, "download_weights returned different weights");
 }
 
+// engine.rs:2877-2936 through prichs-core's GPU dispatch target: forward
+// x W with matmul_gpu, backward-data dY W^T with matmul_a_bt_gpu and
+// backward-weight x^T dY with matmul_at_b_gpu (cublas.rs:302-327), against
+// the CPU triple loops within 1e-4; the workspace has the reference's slabs
+// and refuses an operand larger than its slab.
+void test_matmul_gpu_family() {
+  const std::vector<float> w{1.0f, 2.0f, 3.0f, 4.0f, 5.0f, 6.0f,
+                             7.0f, 8.0f, 9.0f, 10.0f, 11.0f, 12.0f};
+  const std::vector<float> x{1.0f, 0.5f, 0.2f, 0.1f, 2.0f, 1.0f, 0.0f, -1.0f};
+  const std::vector<float> dy{0.5f, -0.5f, 1.0f, 1.0f, 2.0f, -1.0f};
+  std::vector<float> out(6), dx(8), dw(12, 7.0f);
+  prichs_host::matmul_gpu(x, w, out, 2, 4, 3);
+  prichs_host::matmul_a_bt_gpu(dy, w, dx, 2, 3, 4);
+  prichs_host::matmul_at_b_gpu(x, dy, dw, 2, 4, 3);
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 3; ++j) {
+      float sum = 0.0f;
+      for (int k = 0; k < 4; ++k) sum += x[i * 4 + k] * w[k * 3 + j];
+      CHECK(std::fabs(out[i * 3 + j] - sum) < 1e-4f, "matmul_gpu mismatch at %d", i * 3 + j);
+    }
+  for (int i = 0; i < 2; ++i)
+    for (int k = 0; k < 4; ++k) {
+      float sum = 0.0f;
+      for (int j = 0; j < 3; ++j) sum += dy[i * 3 + j] * w[k * 3 + j];
+      CHECK(std::fabs(dx[i * 4 + k] - sum) < 1e-4f, "matmul_a_bt_gpu mismatch at %d", i * 4 + k);
+    }
+  for (int k = 0; k < 4; ++k)
+    for (int j = 0; j < 3; ++j) {
+      float sum = 0.0f;
+      for (int i = 0; i < 2; ++i) sum += x[i * 4 + k] * dy[i * 3 + j];
+      CHECK(std::fabs(dw[k * 3 + j] - sum) < 1e-4f, "matmul_at_b_gpu mismatch at %d", k * 3 + j);
+    }
+  prichs_host::GpuWorkspace *ws = prichs_host::get_gpu_workspace();
+  CHECK(ws != nullptr, "no process-wide workspace");
+  CHECK(prichs_host::get_gpu_workspace() == ws, "the process-wide workspace changed");
+  // slab A holds 4 Mi floats (16 MB): 4097 x 1024 does not fit
+  std::vector<float> big(4097 * 1024, 1.0f), bb(1024, 1.0f), cc(4097, 0.0f);
+  expect_error([&] { ws->matmul(big, bb, cc, 4097, 1024, 1); }, "exceed preallocated");
+  prichs_host::GpuWorkspace own(4097 * 1024 * 4, 0, 0);
+  own.matmul(big, bb, cc, 4097, 1024, 1);
+  CHECK(cc[0] == 1024.0f && cc[4096] == 1024.0f, "sums of 1024 ones: %g %g", cc[0], cc[4096]);
+  expect_error([&] { own.matmul(bb, bb, cc, 4097, 1024, 1); }, "elements");
+}
+
 // engine.rs:3032-3053 (forward half of test_gpu_rmsnorm_correctness).
 void test_gpu_rmsnorm_correctness() {
   const size_t seq_len = 2, hidden_dim = 4;
@@ -359,9 +403,16 @@ int main(int argc, char **argv) {
     run("engine_creation_without_device_raises", [] {
       expect_error([] { GpuModelEngine e({{4, 3, true}}); }, "hipMalloc");
     });
+    // cublas.rs:285-309: no workspace without a device, and matmul_gpu errs.
+    run("matmul_gpu_without_device_raises", [] {
+      CHECK(prichs_host::get_gpu_workspace() == nullptr, "a workspace without a device");
+      std::vector<float> a(8, 1.0f), b(12, 1.0f), c(6, 0.0f);
+      expect_error([&] { prichs_host::matmul_gpu(a, b, c, 2, 4, 3); }, "unavailable");
+    });
     return g_failed == 0 ? 0 : 1;
   }
   run("persistent_vram_gemm_correctness", test_persistent_vram_gemm_correctness);
+  run("matmul_gpu_family", test_matmul_gpu_family);
   run("gpu_rmsnorm_correctness", test_gpu_rmsnorm_correctness);
   run("gpu_moe_forward", test_gpu_moe_forward);
   run("error_paths", test_error_paths);
