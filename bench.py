@@ -41,6 +41,100 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+FLUSH_BYTES = 512 << 20  # twice the 256 MB MALL: overwriting it evicts L2 and MALL
+
+
+class Flusher:
+    """Overwrites a 512 MiB device buffer (a fill kernel) so that the next
+    kernel finds its inputs in HBM, not in L2 or the 256 MB MALL.  Run between
+    event-timed repetitions, outside the timed intervals."""
+
+    def __init__(self):
+        import torch
+
+        self.buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda")
+
+    def __call__(self):
+        self.buf.zero_()
+
+
+def device_caps():
+    """CU count and peak clocks of the device (prichs_device_caps) and the bf16
+    dense MFMA peak they imply (CUs x clock x 4096 FLOP/clk/CU: 4 SIMDs x one
+    16x16x32 MFMA = 16384 FLOP per 16 cycles each)."""
+    import ctypes as C
+
+    from prichs_amd import _lib as L
+
+    v = [C.c_int(0) for _ in range(4)]
+    L.check(L.load().prichs_device_caps(*(C.byref(x) for x in v)))
+    cus, clk, mclk, bus = (x.value for x in v)
+    return {"compute_units": cus, "max_clock_MHz": clk / 1e3, "mem_clock_MHz": mclk / 1e3,
+            "mem_bus_bits": bus,
+            "bf16_dense_peak_TFLOPs_from_caps": cus * clk * 1e3 * 4096 / 1e12}
+
+
+def copy_bandwidth(reps: int = 10):
+    """Device-to-device copy of 2 GiB (torch's copy kernel) timed with HIP
+    events: read + write bytes per second, a measured practical HBM peak."""
+    import torch
+
+    n = (2 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    del src, dst
+    return {"GB/s": 2 * n * 4 / (ms * 1e-3) / 1e9, "bytes_per_copy": 2 * n * 4, "ms": ms,
+            "kernel": "torch copy_ of 2 GiB (read + write counted), HIP events, mean of "
+                      f"{reps}"}
+
+
+def copy_same_bytes_flushed(moved_bytes: int, flush, reps: int = 10):
+    """The practical cold roof of a memory-bound kernel that moves moved_bytes
+    (reads + writes): a device copy of moved_bytes / 2 (torch's copy kernel),
+    L2 and MALL flushed before each repetition, event-timed like the kernels.
+    At tens of MB the ramp of a cold launch, not the 8 TB/s HBM peak, bounds
+    any streaming kernel."""
+    import torch
+
+    n = max(1, moved_bytes // 2 // 4)
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for a, b in evs:
+        flush()
+        a.record()
+        dst.copy_(src)
+        b.record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in evs) / reps
+    del src, dst
+    return {"ms": ms, "GB/s": 2 * n * 4 / (ms * 1e-3) / 1e9}
+
+
+def committed_digest(name: str):
+    try:
+        with open(os.path.join(ROOT, "tests", "golden", "input_sha256.json")) as fh:
+            return json.load(fh).get(name)
+    except OSError:
+        return None
+
+
+def inputs_record(name: str, digest: str):
+    want = committed_digest(name)
+    return {"sha256": digest, "committed_sha256": want, "matches_committed": digest == want}
+
+
 def cpu_model() -> str:
     """The host CPU's model name (Linux /proc/cpuinfo), or "unknown"."""
     try:
@@ -160,8 +254,25 @@ def main():
         eng.forward(x, out=out)
     torch.cuda.synchronize()
     ms = eng.stage_ms()
+    # The same forwards with L2 and the MALL flushed before each one (the
+    # flush sits between forwards, outside every stage interval): the
+    # router reads x from HBM as a layer does after the attention sub-layer.
+    flush = Flusher()
+    eng.set_timing(args.steps)
+    for _ in range(args.steps):
+        flush()
+        eng.forward(x, out=out)
+    torch.cuda.synchronize()
+    ms_cold = eng.stage_ms()
     eng.set_timing(0)
+    es_ = 2 if inp.dtype == "bf16" else 4
+    copy_ref = {"router": copy_same_bytes_flushed(T * d * es_ + d * E * 4 + T * E * 4 + T * k * 8,
+                                                  flush),
+                "combine": copy_same_bytes_flushed((T * k + S * T) * d * es_ + T * k * 12
+                                                   + T * d * es_, flush)}
+    del flush
     log("bench: stage ms", json.dumps({kk: round(v, 4) for kk, v in ms.items()}))
+    log("bench: stage ms (flushed)", json.dumps({kk: round(v, 4) for kk, v in ms_cold.items()}))
 
     es = 2 if inp.dtype == "bf16" else 4
     rows = T * k + S * T
@@ -176,8 +287,8 @@ def main():
     permute_bytes = T * k * 8 + (T * k + T) * 4 + T * k * 8
     combine_bytes = rows * d * es + T * k * 12 + T * d * es
 
-    def gbps(b, stage):
-        return b / (ms[stage] / 1e3) / 1e9 if ms[stage] > 0 else None
+    def gbps(b, stage, m=ms):
+        return b / (m[stage] / 1e3) / 1e9 if m[stage] > 0 else None
 
     kernel = "grouped gate/up GEMM + fused SwiGLU (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, Bf16Cfg<256,256,2,4>, true>)"
     if T * k < 64 * E:  # fewer than 64 rows per routed expert on average
@@ -191,7 +302,7 @@ def main():
         tfile = "pmc_config4_skinny_traffic.txt"
         roofline = {"kernel": kernel, "bound": "hbm", "achieved": bw, "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": bw / PEAK_HBM_GBPS,
-                    "traffic": measured_traffic(tfile) if args.config == 4 else None,
+                    "traffic": measured_traffic(tfile, "gate_up") if args.config == 4 else None,
                     "traffic_source": f"profiles/{tfile} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE, "
                                       "copy-calibrated)" if args.config == 4 else None,
                     "algorithmic_bytes_per_launch": gu_bytes, "experts_touched": touched,
@@ -202,9 +313,11 @@ def main():
         roofline = {
             "kernel": kernel, "bound": "mfma", "achieved": gu_tflops, "peak": peak,
             "unit": "TFLOP/s", "frac": gu_tflops / peak,
-            "traffic": measured_traffic("pmc_config2_gate_up_traffic.txt") if args.config == 2 else None,
-            "traffic_source": "profiles/pmc_config2_gate_up_traffic.txt (rocprofv3 --pmc "
-                              "FETCH_SIZE, WRITE_SIZE, copy-calibrated)" if args.config == 2 else None,
+            "traffic": measured_traffic("pmc_config2_traffic.txt", "gate_up") if args.config == 2 else None,
+            "traffic_source": "profiles/pmc_config2_traffic.txt (rocprofv3 --pmc FETCH_SIZE, "
+                              "WRITE_SIZE, copy-calibrated)" if args.config == 2 else None,
+            "mfma_busy_source": "profiles/pmc_config2_mfma.txt (SQ_VALU_MFMA_BUSY_CYCLES)"
+                                if args.config == 2 else None,
             "algorithmic_flops_per_launch": flops_gate_up,
             "avg_launch_ms": ms["gate_up"],
             "timed_over": "HIP events on the engine's launch stream between the stages, over a "
@@ -231,13 +344,29 @@ def main():
                         "gate_up_ms": ms["gate_up"], "down_ms": ms["down"],
                         "down_tflops": flops_down / t_dn / 1e12},
         "memory_bound_stages": {
-            "router": {"ms": ms["router"], "GB/s": gbps(router_bytes, "router"), "bytes": router_bytes},
-            "permute": {"ms": ms["permute"], "GB/s": gbps(permute_bytes, "permute"), "bytes": permute_bytes},
-            "combine": {"ms": ms["combine"], "GB/s": gbps(combine_bytes, "combine"), "bytes": combine_bytes},
+            "router": {"ms": ms["router"], "GB/s": gbps(router_bytes, "router"),
+                       "ms_flushed": ms_cold["router"],
+                       "GB/s_flushed": gbps(router_bytes, "router", ms_cold), "bytes": router_bytes,
+                       "copy_same_bytes_flushed": copy_ref["router"]},
+            "permute": {"ms": ms["permute"], "GB/s": gbps(permute_bytes, "permute"),
+                        "ms_flushed": ms_cold["permute"],
+                        "GB/s_flushed": gbps(permute_bytes, "permute", ms_cold),
+                        "bytes": permute_bytes},
+            "combine": {"ms": ms["combine"], "GB/s": gbps(combine_bytes, "combine"),
+                        "ms_flushed": ms_cold["combine"],
+                        "GB/s_flushed": gbps(combine_bytes, "combine", ms_cold),
+                        "bytes": combine_bytes,
+                        "copy_same_bytes_flushed": copy_ref["combine"]},
             "peak_GB/s": PEAK_HBM_GBPS,
+            "note": "flushed = L2 and MALL overwritten (512 MiB) before each forward, outside the "
+                    "stage intervals; the combine reads y right after the down GEMM wrote it",
         },
         "stage_ms": {kk: v for kk, v in ms.items() if kk != "n"},
+        "stage_ms_flushed": {kk: v for kk, v in ms_cold.items() if kk != "n"},
+        "inputs": inputs_record(f"config{args.config}", inp.digest()),
         "device": torch.cuda.get_device_name(0),
+        "device_caps": device_caps(),
+        "copy_bandwidth": copy_bandwidth(),
     }
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
@@ -402,7 +531,9 @@ def bench_backward(args):
         "forward_ms": fms["total"],
         "backward_ms": bms["total"],
         "backward_stage_ms": {kk: v for kk, v in bms.items() if kk != "n"},
+        "inputs": inputs_record(f"config{cfg}", inp.digest()),
         "device": torch.cuda.get_device_name(0),
+        "device_caps": device_caps(),
     }
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle forward + backward)")
@@ -431,14 +562,16 @@ def copy_calibration():
     del src, dst
 
 
-def measured_traffic(name):
-    """HBM bytes per gate/up launch from a committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration), or None."""
+def measured_traffic(name, kernel):
+    """HBM-side bytes per launch of `kernel` from a committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration:
+    the line traffic_bytes_per_launch[kernel] = ...), or None."""
     path = os.path.join(ROOT, "profiles", name)
+    key = f"traffic_bytes_per_launch[{kernel}]"
     try:
         with open(path) as fh:
             for line in fh:
-                if line.startswith("traffic_bytes_per_launch"):
+                if line.startswith(key):
                     return float(line.split("=")[1].split()[0])
     except OSError:
         return None
@@ -495,17 +628,41 @@ def bench_block(args):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / reps
 
+    flush = Flusher()
+
+    def event_ms_flushed(fn, reps=args.steps):
+        # One event pair per repetition with L2 and the MALL flushed before
+        # it, outside the pair: the kernel reads its inputs from HBM.
+        for _ in range(3):
+            fn()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps)]
+        for a, b in evs:
+            flush()
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in evs) / reps
+
     # HBM-bound sub-layers alone at the block's shapes: RMSNorm of x [T, d]
     # (bf16 in/out, f32 weight) and RoPE in place on Q [T, 12, 128] and K [T, 3, 128].
     w_norm = torch.from_numpy(np.ascontiguousarray(inp.input_norm, np.float32)).to("cuda")
-    rn_ms = event_ms(lambda: ops.rmsnorm(x, w_norm, want_rstd=False))
+    rn_out = torch.empty_like(x)
+    rn_ms = event_ms(lambda: ops.rmsnorm(x, w_norm, want_rstd=False, out=rn_out))
+    rn_ms_cold = event_ms_flushed(lambda: ops.rmsnorm(x, w_norm, want_rstd=False, out=rn_out))
     cos, sin = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to("cuda")
                 for a in synth.rope_cache(S, hd, inp.rope_theta))
     qr = q.contiguous().view(B, S, Hq, hd)
     kr = k.contiguous().view(B, S, Hkv, hd)
-    rope_ms = event_ms(lambda: (ops.rope_(qr, cos, sin, S, B, S), ops.rope_(kr, cos, sin, S, B, S)))
+    rope_fn = lambda: (ops.rope_(qr, cos, sin, S, B, S), ops.rope_(kr, cos, sin, S, B, S))  # noqa: E731
+    rope_ms = event_ms(rope_fn)
+    rope_ms_cold = event_ms_flushed(rope_fn)
     rn_bytes = 2 * T * d * 2 + d * 4
     rope_bytes = 2 * T * (Hq + Hkv) * hd * 2 + 2 * S * (hd // 2) * 4
+    rn_copy = copy_same_bytes_flushed(rn_bytes, flush)
+    rope_copy = copy_same_bytes_flushed(rope_bytes, flush)
+    del flush
     att_flops = B * Hq * 4.0 * hd * S * (S + 1) / 2  # causal QK^T + PV
     moe_flops = 6.0 * d * inp.moe.f * T * (inp.moe.k + 1)
     proj_flops = 2.0 * T * d * (d + 2 * Hkv * hd) + 2.0 * T * d * d
@@ -524,12 +681,24 @@ def bench_block(args):
                      "avg_launch_ms": att_ms},
         "block_tflops": (att_flops + moe_flops + proj_flops) / (ms * 1e-3) / 1e12,
         "memory_bound_stages": {
-            "rmsnorm": {"ms": rn_ms, "GB/s": rn_bytes / (rn_ms * 1e-3) / 1e9, "bytes": rn_bytes},
+            "rmsnorm": {"ms": rn_ms, "GB/s": rn_bytes / (rn_ms * 1e-3) / 1e9,
+                        "ms_flushed": rn_ms_cold,
+                        "GB/s_flushed": rn_bytes / (rn_ms_cold * 1e-3) / 1e9, "bytes": rn_bytes,
+                        "copy_same_bytes_flushed": rn_copy},
             "rope_q_and_k": {"ms": rope_ms, "GB/s": rope_bytes / (rope_ms * 1e-3) / 1e9,
-                             "bytes": rope_bytes},
+                             "ms_flushed": rope_ms_cold,
+                             "GB/s_flushed": rope_bytes / (rope_ms_cold * 1e-3) / 1e9,
+                             "bytes": rope_bytes,
+                             "copy_same_bytes_flushed": rope_copy,
+                             "note": "two launches (Q 12 heads, K 3 heads); the copy is one"},
             "peak_GB/s": PEAK_HBM_GBPS,
+            "note": "flushed = L2 and MALL overwritten (512 MiB) before each repetition, outside "
+                    "its event pair",
         },
+        "inputs": inputs_record("config5", inp.digest()),
         "device": torch.cuda.get_device_name(0),
+        "device_caps": device_caps(),
+        "copy_bandwidth": copy_bandwidth(),
     }
     eng.close()
     if not args.no_cpu_baseline:

@@ -78,6 +78,10 @@ const char *prichs_last_error(void);
 void prichs_clear_error(void);
 /* ABI version of this header (major * 10000 + minor * 100 + patch). */
 int prichs_abi_version(void);
+/* The current device's compute units, peak engine and memory clocks (kHz)
+ * and memory bus width (bits), for rooflines (any output may be NULL). */
+int prichs_device_caps(int *cus, int *clock_khz, int *mem_clock_khz,
+                       int *mem_bus_bits);
 
 /* ---------------------------------------------------------------------- */
 /* 1. Legacy launchers (identical signatures to the reference)             */

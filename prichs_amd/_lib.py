@@ -88,6 +88,7 @@ SIGNATURES = {
     "prichs_last_error": (C.c_char_p, []),
     "prichs_clear_error": (None, []),
     "prichs_abi_version": (_i, []),
+    "prichs_device_caps": (_i, [C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),
     "launch_rmsnorm_forward": (None, [_vp, _vp, _vp, _vp, _sz, _sz, _f, _vp]),
     "launch_swiglu_forward": (None, [_vp, _vp, _vp, _sz, _vp]),
     "launch_rope": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _i, _vp]),

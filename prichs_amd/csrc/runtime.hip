@@ -47,3 +47,22 @@ extern "C" const char *prichs_last_error(void) { return prichs::g_last_error; }
 extern "C" void prichs_clear_error(void) { prichs::g_last_error[0] = 0; }
 
 extern "C" int prichs_abi_version(void) { return 100; }
+
+// Capabilities of the current device for the roofline (all outputs may be
+// NULL): compute units, peak engine clock and memory clock in kHz, memory
+// bus width in bits.
+extern "C" int prichs_device_caps(int *cus, int *clock_khz, int *mem_clock_khz,
+                                  int *mem_bus_bits) {
+  int dev = 0;
+  PRICHS_HIP_TRY(hipGetDevice(&dev), "device_caps: no HIP device");
+  struct Q {
+    int *out;
+    hipDeviceAttribute_t attr;
+  } qs[] = {{cus, hipDeviceAttributeMultiprocessorCount},
+            {clock_khz, hipDeviceAttributeClockRate},
+            {mem_clock_khz, hipDeviceAttributeMemoryClockRate},
+            {mem_bus_bits, hipDeviceAttributeMemoryBusWidth}};
+  for (const Q &q : qs)
+    if (q.out) PRICHS_HIP_TRY(hipDeviceGetAttribute(q.out, q.attr, dev), "device_caps");
+  return PRICHS_OK;
+}

@@ -170,13 +170,14 @@ def moe_combine(y, idx, w, token_row, has_shared=True, out_dtype=torch.float32, 
 
 
 # ------------------------------------------------------- memory-bound ops --
-def rmsnorm(x, w, eps=1e-5, out_dtype=None, want_rstd=True, stream=None):
+def rmsnorm(x, w, eps=1e-5, out_dtype=None, want_rstd=True, stream=None, out=None):
     """prichs_rmsnorm_forward -> (out, rstd)."""
     lib = L.load()
     x = _dev(x)
     d = x.shape[-1]
     T = x.numel() // d
-    out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
     rstd = torch.empty((T,), dtype=torch.float32, device=x.device) if want_rstd else None
     L.check(lib.prichs_rmsnorm_forward(_p(x), dtype_code(x), _p(_dev(w)), _p(out), dtype_code(out),
                                        _p(rstd), T, d, eps, _stream(stream)))

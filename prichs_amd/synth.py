@@ -216,6 +216,17 @@ class BlockInputs:
     sin: np.ndarray
     moe: MoEInputs
 
+    def digest(self) -> str:
+        """SHA-256 of every input tensor as little-endian f32 bytes, in a fixed
+        order: x, the norms, the projections, then the MoE's router, bias and
+        expert weights (shared first)."""
+        h = hashlib.sha256()
+        m = self.moe
+        for a in [self.x, self.input_norm, self.post_norm, self.wq, self.wk, self.wv, self.wo,
+                  m.w_router, m.router_bias, *m.gate, *m.up, *m.down]:
+            h.update(np.ascontiguousarray(a, dtype=np.float32).tobytes())
+        return h.hexdigest()
+
 
 def rope_cache(max_seq_len: int, head_dim: int, theta: float):
     """(cos, sin) RoPE tables [max_seq_len * head_dim/2] from the library's host

@@ -309,6 +309,22 @@ def test_config1_golden_fixture(orc):
     assert float(np.abs(r["out"]).astype(np.float64).sum()) == float(g["out_abs_sum"])
 
 
+def test_input_digests_of_every_configuration():
+    # The committed SHA-256s of the seeded inputs of configurations 1-5
+    # (tests/golden/make_input_digests.py): generator drift is reported here,
+    # apart from any kernel error.  The config-1 digest is also in the oracle
+    # fixture above.
+    import json
+
+    with open(os.path.join(GOLDEN, "input_sha256.json")) as fh:
+        want = json.load(fh)
+    g = np.load(os.path.join(GOLDEN, "config1_oracle.npz"), allow_pickle=False)
+    assert want["config1"] == str(g["input_sha256"])
+    for c in (2, 3, 4):
+        assert synth.config_inputs(c).digest() == want[f"config{c}"], c
+    assert synth.make_block_inputs().digest() == want["config5"]
+
+
 # ------------------------------------------------------------ attention --
 def _attention_f64(x, Hq, Hkv, wq, wk, wv, wo, cos, sin, pos_offset=0):
     """Causal GQA softmax attention in float64 (attention.rs:56-176 semantics)."""
