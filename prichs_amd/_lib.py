@@ -9,7 +9,9 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libprichs_hip.so")
+# PRICHS_HIP_LIB selects another build of the same library (the sanitizer
+# tests load prichs_amd/_build_asan/libprichs_hip.so this way).
+LIB_PATH = os.environ.get("PRICHS_HIP_LIB") or os.path.join(HERE, "libprichs_hip.so")
 
 PRICHS_OK = 0
 PRICHS_ERR_INVALID_ARGUMENT = -1
@@ -120,6 +122,7 @@ SIGNATURES = {
     "prichs_gemm": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _i, _vp]),
     "prichs_attention_forward": (_i, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
                                       _sz, _i, _vp]),
+    "prichs_attention_probs_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     "prichs_checkpoint_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
     "prichs_checkpoint_close": (_i, [_vp]),
     "prichs_checkpoint_info": (_i, [_vp, C.POINTER(C.c_uint64), C.POINTER(_f), C.POINTER(_sz),

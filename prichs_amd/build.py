@@ -92,6 +92,76 @@ def build_host(verbose: bool = False) -> str:
     return HOST_LIB
 
 
+# ---- AddressSanitizer + UBSan build of the host code (CPU tests only) -----
+# The library's host code (argument checks, packing, the checkpoint reader,
+# the workspace) and the C++ host mirror are compiled with clang's
+# -fsanitize=address,undefined into prichs_amd/_build_asan/; device code is
+# unchanged.  tests/test_sanitizers.py runs the CPU tests against these
+# builds with the clang ASan runtime preloaded.
+ASAN_DIR = os.path.join(HERE, "_build_asan")
+ASAN_LIB = os.path.join(ASAN_DIR, "libprichs_hip.so")
+ASAN_HOST_LIB = os.path.join(ASAN_DIR, "libprichs_host.so")
+ASAN_HOST_TEST_BIN = os.path.join(ASAN_DIR, "test_gpu_model_engine")
+LLVM = os.path.join(ROCM, "llvm", "bin")
+# Each -fsanitize= follows -Xarch_host: host code only.
+SAN_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=all"]
+
+
+def asan_runtime() -> str:
+    """The clang ASan runtime that the sanitized builds link against."""
+    import glob
+
+    hits = sorted(glob.glob(os.path.join(ROCM, "llvm", "lib", "clang", "*", "lib", "linux",
+                                         "libclang_rt.asan-x86_64.so")))
+    if not hits:
+        raise RuntimeError("libclang_rt.asan-x86_64.so not found under ROCm's LLVM")
+    return hits[-1]
+
+
+def _compile_asan(src: str) -> str:
+    obj = os.path.join(ASAN_DIR, os.path.basename(src) + ".o")
+    flags = [f if f != "-O3" else "-O1" for f in COMMON_FLAGS]
+    cmd = [hipcc(), *flags, "-g", *SAN_HOST, "-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc (sanitized) failed for {src}:\n{r.stderr}")
+    return obj
+
+
+def build_sanitized(verbose: bool = False) -> str:
+    os.makedirs(ASAN_DIR, exist_ok=True)
+    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(_compile_asan, srcs))
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *SAN_HOST, *objs, "-o", ASAN_LIB]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{r.stderr}")
+    cxx = os.path.join(LLVM, "clang++")
+    san = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-fno-sanitize-recover=all",
+           "-g", "-O1"]
+    flags = ["-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
+             "-I", os.path.join(ROOT, "include"), "-I", HOST]
+    rocm_lib = ["-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+                f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"]
+    for args, what in (
+        ([*flags, *san, "-fPIC", "-shared", os.path.join(HOST, "gpu_model_engine.cpp"), "-L",
+          ASAN_DIR, "-lprichs_hip", *rocm_lib, "-Wl,-rpath,$ORIGIN", "-o", ASAN_HOST_LIB],
+         "sanitized libprichs_host.so"),
+        ([*flags, *san, HOST_TEST_SRC, "-L", ASAN_DIR, "-lprichs_host", "-lprichs_hip", *rocm_lib,
+          "-Wl,-rpath,$ORIGIN", "-o", ASAN_HOST_TEST_BIN], "sanitized test_gpu_model_engine")):
+        r = subprocess.run([cxx, *args], capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"{what} failed:\n{r.stderr}")
+    if verbose:
+        print(f"built {ASAN_LIB}, {ASAN_HOST_LIB} and {ASAN_HOST_TEST_BIN}")
+    return ASAN_LIB
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if len(sys.argv) > 1 and sys.argv[1] == "--sanitized":
+        build_sanitized(verbose=True)
+    else:
+        build(verbose=True)
     sys.exit(0)
