@@ -102,7 +102,8 @@ void launch_swiglu_forward(const float *dev_gate, const float *dev_up,
 
 /* Replaces launch_rope (kernels.cu:554-572, kernel 520-552).  In-place
  * rotation of interleaved pairs of [seq_len, num_heads, head_dim] by
- * cos/sin[t * head_dim/2 + i]; backward_sign (+1/-1) multiplies sin.  Like the
+ * cos/sin[t * head_dim/2 + i]; sin is multiplied by (float)backward_sign,
+ * whatever its value (+1 forward, -1 inverse), as in the original.  Like the
  * original it has no position offset; prichs_rope_forward has one. */
 void launch_rope(float *dev_q_or_k, const float *dev_cos_cache,
                  const float *dev_sin_cache, size_t seq_len, size_t num_heads,
@@ -322,6 +323,22 @@ int prichs_attention_forward(const void *q, size_t ldq, const void *k,
                              size_t ldo, size_t batch, size_t seq_len,
                              size_t n_heads, size_t n_kv_heads,
                              size_t head_dim, int dtype, void *stream);
+
+/* f32 causal attention of one sequence with the probabilities kept: the
+ * per-head computation of crates/prichs-model/src/attention.rs:96-149 (scores
+ * (q . k) / sqrt(head_dim), sequential dot products; row max, expf, sum,
+ * times 1 / max(sum, 1e-9); context sum over keys ascending) for the
+ * reference's host-slice gpu_batched_attention_forward
+ * (crates/prichs-cuda/src/engine.rs:1181-1405), which returns these
+ * probabilities.  q [T, n_heads * head_dim], k / v [T, n_kv_heads * head_dim]
+ * (query head h reads kv head h / (n_heads / n_kv_heads)); probs
+ * [n_heads, T, T] (zeros past the diagonal) and ctx [T, n_heads * head_dim]
+ * (the heads concatenated); all f32 device memory, contiguous.  seq_len <=
+ * 16384 (PRICHS_ERR_UNSUPPORTED beyond). */
+int prichs_attention_probs_f32(const float *q, const float *k, const float *v,
+                               float *probs, float *ctx, size_t seq_len,
+                               size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                               void *stream);
 
 /* RoPE cos/sin tables on the host (no GPU needed): replaces
  * precompute_rope_cache (crates/prichs-core/src/backward.rs:136-157).

@@ -478,3 +478,92 @@ extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k
   PRICHS_LAUNCH_CHECK("attention launch");
   return PRICHS_OK;
 }
+
+// ---------------------------------------------------------------------------
+// f32 causal attention with materialised probabilities: the computation of
+// the reference's per-head CPU attention (crates/prichs-model/src/
+// attention.rs:96-149) for one sequence, keeping the [H, T, T] probability
+// matrix that the reference's host-slice GPU method returns
+// (gpu_batched_attention_forward, crates/prichs-cuda/src/engine.rs:1181-1405).
+// One wave per (query row i, head h):
+//   s_j = (sum_c q[i][c] k[j][c]) * scale for j <= i (each a sequential sum
+//   over c, lanes over j), written into the probability row;
+//   m = max_j s_j (exact in any order); e_j = expf(s_j - m);
+//   sum of e_j by a fixed wave-tree order; p_j = e_j * (1 / max(sum, 1e-9));
+//   zeros past the diagonal; ctx[i][h][c] = sum_j p_j v[j][c] with j
+//   ascending (lanes over c).
+// ---------------------------------------------------------------------------
+namespace prichs {
+namespace {
+__global__ __launch_bounds__(64) void attn_probs_f32_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    float *__restrict__ probs, float *__restrict__ ctx, int T, int H, int group, int hd,
+    float scale) {
+#pragma clang fp contract(off)
+  extern __shared__ float srow[];  // the row's scores, then probabilities [T]
+  const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int kvh = h / group;
+  const long long ldq = (long long)H * hd, ldk = (long long)(H / group) * hd;
+  const float *qr = q + (long long)i * ldq + (long long)h * hd;
+  float mx = -INFINITY;
+  for (int j = lane; j <= i; j += 64) {
+    const float *kr = k + (long long)j * ldk + (long long)kvh * hd;
+    float dot = 0.0f;
+    for (int c = 0; c < hd; ++c) {
+      const float p = qr[c] * kr[c];
+      dot = dot + p;
+    }
+    const float s = dot * scale;
+    srow[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  float sum = 0.0f;
+  for (int j = lane; j <= i; j += 64) {
+    const float e = expf(srow[j] - mx);
+    srow[j] = e;
+    sum = sum + e;
+  }
+  for (int m = 1; m < 64; m <<= 1) sum = sum + __shfl_xor(sum, m);
+  const float inv = 1.0f / fmaxf(sum, 1e-9f);
+  float *row = probs + ((long long)h * T + i) * T;
+  for (int j = lane; j < T; j += 64) {
+    const float p = j <= i ? srow[j] * inv : 0.0f;
+    if (j <= i) srow[j] = p;
+    row[j] = p;
+  }
+  __syncthreads();  // every lane's probabilities are in LDS
+  for (int c = lane; c < hd; c += 64) {
+    float acc = 0.0f;
+    for (int j = 0; j <= i; ++j) {
+      const float p = srow[j] * v[(long long)j * ldk + (long long)kvh * hd + c];
+      acc = acc + p;
+    }
+    ctx[(long long)i * ldq + (long long)h * hd + c] = acc;
+  }
+}
+}  // namespace
+}  // namespace prichs
+
+extern "C" int prichs_attention_probs_f32(const float *q, const float *k, const float *v,
+                                          float *probs, float *ctx, size_t seq_len,
+                                          size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                          void *stream) {
+  PRICHS_REQUIRE(n_heads >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0,
+                 "attention_probs: n_heads=%zu must be a positive multiple of n_kv_heads=%zu",
+                 n_heads, n_kv_heads);
+  PRICHS_REQUIRE(head_dim >= 1 && head_dim <= 65536 && n_heads <= 65535,
+                 "attention_probs: shape too large");
+  if (seq_len > 16384)
+    return fail(PRICHS_ERR_UNSUPPORTED, "attention_probs: seq_len=%zu above 16384 (one row of "
+                "scores is kept in LDS)", seq_len);
+  if (seq_len == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(q && k && v && probs && ctx, "attention_probs: null pointer argument");
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  hipLaunchKernelGGL(attn_probs_f32_kernel, dim3((unsigned)seq_len, (unsigned)n_heads), dim3(64),
+                     seq_len * sizeof(float), as_stream(stream), q, k, v, probs, ctx,
+                     (int)seq_len, (int)n_heads,
+                     (int)(n_heads / n_kv_heads), (int)head_dim, scale);
+  PRICHS_LAUNCH_CHECK("attention_probs launch");
+  return PRICHS_OK;
+}

@@ -165,8 +165,10 @@ void GpuModelEngine::release() {
   for (void *p : {(void *)dev_weights_, (void *)dev_act_in_, (void *)dev_act_out_, (void *)dev_x_,
                   (void *)dev_gate_, (void *)dev_up_, (void *)dev_act_, (void *)dev_out_,
                   (void *)dev_moe_out_, (void *)dev_rstd_, (void *)dev_cos_, (void *)dev_sin_,
-                  (void *)dev_idx_, (void *)dev_w_})
+                  (void *)dev_idx_, (void *)dev_w_, (void *)dev_q_, (void *)dev_k_,
+                  (void *)dev_v_, (void *)dev_cat_, (void *)dev_probs_})
     if (p != nullptr) (void)hipFree(p);
+  dev_q_ = dev_k_ = dev_v_ = dev_cat_ = dev_probs_ = nullptr;
   dev_weights_ = dev_act_in_ = dev_act_out_ = dev_x_ = dev_gate_ = dev_up_ = dev_act_ = nullptr;
   dev_out_ = dev_moe_out_ = dev_rstd_ = dev_cos_ = dev_sin_ = dev_w_ = nullptr;
   dev_idx_ = nullptr;
@@ -306,6 +308,73 @@ void GpuModelEngine::upload_rope_cache(const std::vector<float> &cos_cache,
   const size_t bytes = cos_cache.size() * sizeof(float);
   hip_ok(hipMemcpy(dev_cos_, cos_cache.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy cos");
   hip_ok(hipMemcpy(dev_sin_, sin_cache.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy sin");
+  rope_len_ = cos_cache.size();
+}
+
+// engine.rs:1181-1405.
+AttentionOut GpuModelEngine::gpu_batched_attention_forward(
+    const std::vector<float> &normed1, size_t q_id, size_t k_id, size_t v_id, size_t out_id,
+    std::vector<float> &attn_out, size_t seq_len, size_t num_heads, size_t num_kv_heads,
+    size_t head_dim) {
+  const size_t hidden = num_heads * head_dim, kv = num_kv_heads * head_dim;
+  // The reference's checks (engine.rs:1197-1208), then the weight shapes.
+  if (normed1.size() != seq_len * hidden)
+    bail(fmt("normed1 length mismatch: %zu != %zu", normed1.size(), seq_len * hidden));
+  if (attn_out.size() != seq_len * hidden)
+    bail(fmt("attn_out length mismatch: %zu != %zu", attn_out.size(), seq_len * hidden));
+  if (seq_len * hidden > cap_.attn_vec) bail("Attention dimensions exceed attn_vec_capacity");
+  if (num_heads * seq_len * seq_len > cap_.attn_scores)
+    bail("Attention scores dimensions exceed attn_scores_capacity");
+  if (num_kv_heads == 0 || num_heads % num_kv_heads != 0)
+    bail(fmt("num_heads=%zu is not a multiple of num_kv_heads=%zu", num_heads, num_kv_heads));
+  for (size_t id : {q_id, k_id, v_id, out_id}) check_param(id, "gpu_batched_attention_forward");
+  const ParamMetadata &mq = meta_[q_id], &mk = meta_[k_id], &mv = meta_[v_id],
+                      &mo = meta_[out_id];
+  if (mq.rows != hidden || mq.cols != hidden || mk.rows != hidden || mk.cols != kv ||
+      mv.rows != hidden || mv.cols != kv || mo.rows != hidden || mo.cols != hidden)
+    bail("attention weight shapes do not match the head layout");
+  if (head_dim % 2 != 0) bail(fmt("head_dim %zu must be even for RoPE", head_dim));
+  if (seq_len * (head_dim / 2) > rope_len_)
+    bail(fmt("seq_len %zu needs %zu RoPE cache entries; %zu uploaded", seq_len,
+             seq_len * (head_dim / 2), rope_len_));
+  if (dev_q_ == nullptr) {
+    dev_q_ = dev_alloc<float>(cap_.attn_vec, "hipMalloc(q)");
+    dev_k_ = dev_alloc<float>(cap_.attn_vec, "hipMalloc(k)");
+    dev_v_ = dev_alloc<float>(cap_.attn_vec, "hipMalloc(v)");
+    dev_cat_ = dev_alloc<float>(cap_.attn_vec, "hipMalloc(concat)");
+    dev_probs_ = dev_alloc<float>(cap_.attn_scores, "hipMalloc(scores)");
+  }
+  if (seq_len * hidden > cap_.act_in || seq_len * hidden > cap_.act_out)
+    bail("Attention dimensions exceed the activation capacity");
+  const size_t q_bytes = seq_len * hidden * sizeof(float), kv_bytes = seq_len * kv * sizeof(float);
+  hip_ok(hipMemcpy(dev_act_in_, normed1.data(), q_bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  lib_ok(prichs_matmul_f32(PRICHS_MATMUL_AB, dev_act_in_, dev_weights_ + mq.offset, dev_q_,
+                           seq_len, hidden, hidden, nullptr), "Q projection");
+  lib_ok(prichs_matmul_f32(PRICHS_MATMUL_AB, dev_act_in_, dev_weights_ + mk.offset, dev_k_,
+                           seq_len, hidden, kv, nullptr), "K projection");
+  lib_ok(prichs_matmul_f32(PRICHS_MATMUL_AB, dev_act_in_, dev_weights_ + mv.offset, dev_v_,
+                           seq_len, hidden, kv, nullptr), "V projection");
+  // RoPE like the reference's launch_rope (positions 0.., sign +1).
+  lib_ok(prichs_rope_forward(dev_q_, PRICHS_DTYPE_F32, dev_cos_, dev_sin_, seq_len, 1, seq_len,
+                             num_heads, head_dim, 0, 1, nullptr), "RoPE Q");
+  lib_ok(prichs_rope_forward(dev_k_, PRICHS_DTYPE_F32, dev_cos_, dev_sin_, seq_len, 1, seq_len,
+                             num_kv_heads, head_dim, 0, 1, nullptr), "RoPE K");
+  lib_ok(prichs_attention_probs_f32(dev_q_, dev_k_, dev_v_, dev_probs_, dev_cat_, seq_len,
+                                    num_heads, num_kv_heads, head_dim, nullptr), "attention");
+  lib_ok(prichs_matmul_f32(PRICHS_MATMUL_AB, dev_cat_, dev_weights_ + mo.offset, dev_act_out_,
+                           seq_len, hidden, hidden, nullptr), "out projection");
+  std::vector<float> q_rope(seq_len * hidden), k_rope(seq_len * kv), v(seq_len * kv),
+      probs(num_heads * seq_len * seq_len), concat(seq_len * hidden);
+  hip_ok(hipMemcpy(attn_out.data(), dev_act_out_, q_bytes, hipMemcpyDeviceToHost), "D2H out");
+  hip_ok(hipMemcpy(q_rope.data(), dev_q_, q_bytes, hipMemcpyDeviceToHost), "D2H q");
+  hip_ok(hipMemcpy(k_rope.data(), dev_k_, kv_bytes, hipMemcpyDeviceToHost), "D2H k");
+  hip_ok(hipMemcpy(v.data(), dev_v_, kv_bytes, hipMemcpyDeviceToHost), "D2H v");
+  hip_ok(hipMemcpy(probs.data(), dev_probs_, probs.size() * sizeof(float), hipMemcpyDeviceToHost),
+         "D2H probs");
+  hip_ok(hipMemcpy(concat.data(), dev_cat_, q_bytes, hipMemcpyDeviceToHost), "D2H concat");
+  hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  return AttentionOut{std::move(q_rope), std::move(k_rope), std::move(v), std::move(probs),
+                      std::move(concat)};
 }
 
 // engine.rs:1917-2051.

@@ -52,6 +52,10 @@ struct Capacity {
   size_t moe_dim = 16384 * 1280;  // [rows, f] intermediates
   size_t rope_cache = 4096 * 64;  // cos / sin entries
   size_t max_rows = 16384;        // RMSNorm rows (rstd)
+  // Attention (engine.rs:421-424): [T, H * hd] vectors and the [H, T, T]
+  // scores; allocated on the first gpu_batched_attention_forward.
+  size_t attn_vec = 4 * 1024 * 1024;
+  size_t attn_scores = 32 * 1024 * 1024;
 };
 
 // (x, gate, up, act, out) of gpu_moe_forward_expert; the shared form has no x.
@@ -59,6 +63,10 @@ using SharedOut = std::tuple<std::vector<float>, std::vector<float>, std::vector
                              std::vector<float>>;
 using ExpertOut = std::tuple<std::vector<float>, std::vector<float>, std::vector<float>,
                              std::vector<float>, std::vector<float>>;
+// (q after RoPE, k after RoPE, v, probabilities [H, T, T], heads concatenated)
+// of gpu_batched_attention_forward.
+using AttentionOut = std::tuple<std::vector<float>, std::vector<float>, std::vector<float>,
+                                std::vector<float>, std::vector<float>>;
 
 // Model::load_checkpoint (crates/prichs-model/src/model.rs:1673-1736) for a
 // PRICHS02 file, through the library's reader: every parameter in the order
@@ -100,6 +108,17 @@ class GpuModelEngine {
 
   // engine.rs:1162-1179.
   void upload_rope_cache(const std::vector<float> &cos_cache, const std::vector<float> &sin_cache);
+
+  // engine.rs:1181-1405 (called at model.rs:1101): one sequence's attention
+  // sub-layer on host slices.  q/k/v = normed1 [T, d] @ W (f32 MFMA GEMMs),
+  // RoPE from the uploaded cache at positions 0..T-1, causal GQA attention with
+  // the probabilities kept (prichs_attention_probs_f32), attn_out = concat @ Wo.
+  // Returns (q_rope, k_rope, v, probs [H, T, T], concat) like the reference.
+  AttentionOut gpu_batched_attention_forward(const std::vector<float> &normed1, size_t q_id,
+                                             size_t k_id, size_t v_id, size_t out_id,
+                                             std::vector<float> &attn_out, size_t seq_len,
+                                             size_t num_heads, size_t num_kv_heads,
+                                             size_t head_dim);
 
   // engine.rs:1917-2051: the shared expert on all rows of normed2, which stays
   // resident for the routed experts; its output starts the MoE accumulator.
@@ -167,6 +186,10 @@ class GpuModelEngine {
   float *dev_moe_out_ = nullptr;  // MoE accumulator
   float *dev_rstd_ = nullptr;
   float *dev_cos_ = nullptr, *dev_sin_ = nullptr;
+  size_t rope_len_ = 0;  // entries of the last uploaded cos / sin cache
+  // attention scratch (q, k, v, concat, probabilities), allocated on first use
+  float *dev_q_ = nullptr, *dev_k_ = nullptr, *dev_v_ = nullptr, *dev_cat_ = nullptr;
+  float *dev_probs_ = nullptr;
   int32_t *dev_idx_ = nullptr;
   float *dev_w_ = nullptr;
   size_t moe_rows_ = 0, moe_ld_ = 0, moe_d_ = 0;  // layout of the accumulator

@@ -148,6 +148,143 @@ void test_matmul_gpu_family() {
   expect_error([&] { own.matmul(bb, bb, cc, 4097, 1024, 1); }, "elements");
 }
 
+// engine.rs:2948-3005 (test_gpu_batched_attention_execution): the reference's
+// data, its length / row-sum / causal checks, plus the closed form that data
+// has (every projection 0.4, uniform causal rows, attn_out 8 * 0.4 * 0.1).
+void test_gpu_batched_attention_execution() {
+  const size_t T = 4, H = 2, KV = 1, hd = 4, hidden = H * hd, kvd = KV * hd;
+  GpuModelEngine eng({{hidden, hidden, true}, {hidden, kvd, true}, {hidden, kvd, true},
+                      {hidden, hidden, true}});
+  eng.upload_weights({std::vector<float>(hidden * hidden, 0.1f),
+                      std::vector<float>(hidden * kvd, 0.1f),
+                      std::vector<float>(hidden * kvd, 0.1f),
+                      std::vector<float>(hidden * hidden, 0.1f)});
+  eng.upload_rope_cache(std::vector<float>(T * (hd / 2), 1.0f),
+                        std::vector<float>(T * (hd / 2), 0.0f));
+  const std::vector<float> normed1(T * hidden, 0.5f);
+  std::vector<float> attn_out(T * hidden, 0.0f);
+  auto [q, k, v, probs, concat] =
+      eng.gpu_batched_attention_forward(normed1, 0, 1, 2, 3, attn_out, T, H, KV, hd);
+  CHECK(q.size() == T * hidden && k.size() == T * kvd && v.size() == T * kvd, "lengths");
+  CHECK(probs.size() == H * T * T && concat.size() == T * hidden, "lengths");
+  for (size_t h = 0; h < H; ++h)
+    for (size_t i = 0; i < T; ++i) {
+      const float *row = &probs[h * T * T + i * T];
+      float sum = 0.0f;
+      for (size_t j = 0; j < T; ++j) sum += row[j];
+      CHECK(std::fabs(sum - 1.0f) < 1e-4f, "softmax sum %g at h=%zu i=%zu", sum, h, i);
+      for (size_t j = i + 1; j < T; ++j) CHECK(row[j] == 0.0f, "causal violation %zu %zu", i, j);
+      for (size_t j = 0; j <= i; ++j)
+        CHECK(std::fabs(row[j] - 1.0f / (i + 1)) < 1e-5f, "uniform row %zu: %g", i, row[j]);
+    }
+  for (float x : q) CHECK(std::fabs(x - 0.4f) < 1e-5f, "q %g", x);
+  for (float x : k) CHECK(std::fabs(x - 0.4f) < 1e-5f, "k %g", x);
+  for (float x : v) CHECK(std::fabs(x - 0.4f) < 1e-5f, "v %g", x);
+  for (float x : concat) CHECK(std::fabs(x - 0.4f) < 1e-5f, "concat %g", x);
+  for (float x : attn_out) CHECK(std::fabs(x - 0.32f) < 1e-5f, "attn_out %g", x);
+}
+
+// The same method on random weights and a real RoPE cache against a
+// double-precision host computation of the textbook causal GQA attention.
+void test_gpu_batched_attention_random() {
+  const size_t T = 37, H = 4, KV = 2, hd = 16, hidden = H * hd, kvd = KV * hd, half = hd / 2;
+  unsigned seed = 12345;
+  auto rnd = [&] {
+    seed = seed * 1664525u + 1013904223u;
+    return ((seed >> 8) * (1.0f / 16777216.0f)) - 0.5f;
+  };
+  auto fill = [&](size_t n, float scale) {
+    std::vector<float> w(n);
+    for (auto &x : w) x = scale * rnd();
+    return w;
+  };
+  std::vector<std::vector<float>> w{fill(hidden * hidden, 0.3f), fill(hidden * kvd, 0.3f),
+                                    fill(hidden * kvd, 0.3f), fill(hidden * hidden, 0.3f)};
+  GpuModelEngine eng({{hidden, hidden, true}, {hidden, kvd, true}, {hidden, kvd, true},
+                      {hidden, hidden, true}});
+  eng.upload_weights(w);
+  std::vector<float> cosc(T * half), sinc(T * half);
+  for (size_t t = 0; t < T; ++t)
+    for (size_t i = 0; i < half; ++i) {
+      const double ang = t * std::pow(10000.0, -2.0 * i / hd);
+      cosc[t * half + i] = (float)std::cos(ang);
+      sinc[t * half + i] = (float)std::sin(ang);
+    }
+  std::vector<float> normed1 = fill(T * hidden, 2.0f), attn_out(T * hidden, 0.0f);
+  // A cache shorter than seq_len is refused before any launch.
+  eng.upload_rope_cache(std::vector<float>(half), std::vector<float>(half));
+  expect_error([&] {
+    eng.gpu_batched_attention_forward(normed1, 0, 1, 2, 3, attn_out, T, H, KV, hd);
+  }, "RoPE cache");
+  expect_error([&] {
+    std::vector<float> short_out(5);
+    eng.gpu_batched_attention_forward(normed1, 0, 1, 2, 3, short_out, T, H, KV, hd);
+  }, "attn_out length mismatch");
+  eng.upload_rope_cache(cosc, sinc);
+  auto [q, k, v, probs, concat] =
+      eng.gpu_batched_attention_forward(normed1, 0, 1, 2, 3, attn_out, T, H, KV, hd);
+  auto proj = [&](const std::vector<float> &x, const std::vector<float> &wm, size_t n) {
+    std::vector<double> y(T * n, 0.0);
+    for (size_t t = 0; t < T; ++t)
+      for (size_t c = 0; c < hidden; ++c)
+        for (size_t j = 0; j < n; ++j) y[t * n + j] += (double)x[t * hidden + c] * wm[c * n + j];
+    return y;
+  };
+  auto rope = [&](std::vector<double> &y, size_t heads) {
+    for (size_t t = 0; t < T; ++t)
+      for (size_t h = 0; h < heads; ++h)
+        for (size_t i = 0; i < half; ++i) {
+          double *p = &y[t * heads * hd + h * hd + 2 * i];
+          const double c = cosc[t * half + i], s = sinc[t * half + i];
+          const double a = p[0], b = p[1];
+          p[0] = a * c - b * s;
+          p[1] = a * s + b * c;
+        }
+  };
+  std::vector<double> rq = proj(normed1, w[0], hidden), rk = proj(normed1, w[1], kvd),
+                      rv = proj(normed1, w[2], kvd);
+  rope(rq, H);
+  rope(rk, KV);
+  std::vector<double> rp(H * T * T, 0.0), rc(T * hidden, 0.0);
+  for (size_t h = 0; h < H; ++h) {
+    const size_t g = h / (H / KV);
+    for (size_t i = 0; i < T; ++i) {
+      double m = -1e300, sum = 0.0;
+      std::vector<double> s(i + 1);
+      for (size_t j = 0; j <= i; ++j) {
+        double d = 0.0;
+        for (size_t c = 0; c < hd; ++c) d += rq[i * hidden + h * hd + c] * rk[j * kvd + g * hd + c];
+        s[j] = d / std::sqrt((double)hd);
+        m = std::max(m, s[j]);
+      }
+      for (size_t j = 0; j <= i; ++j) sum += (s[j] = std::exp(s[j] - m));
+      for (size_t j = 0; j <= i; ++j) {
+        rp[h * T * T + i * T + j] = s[j] / sum;
+        for (size_t c = 0; c < hd; ++c)
+          rc[i * hidden + h * hd + c] += s[j] / sum * rv[j * kvd + g * hd + c];
+      }
+    }
+  }
+  std::vector<double> ro(T * hidden, 0.0);
+  for (size_t t = 0; t < T; ++t)
+    for (size_t c = 0; c < hidden; ++c)
+      for (size_t j = 0; j < hidden; ++j) ro[t * hidden + j] += rc[t * hidden + c] * w[3][c * hidden + j];
+  auto close = [&](const std::vector<float> &got, const std::vector<double> &want, const char *what) {
+    double err = 0.0, mag = 0.0;
+    for (size_t i = 0; i < want.size(); ++i) {
+      err = std::max(err, std::fabs(got[i] - want[i]));
+      mag = std::max(mag, std::fabs(want[i]));
+    }
+    CHECK(err <= 1e-4 * std::max(mag, 1.0), "%s: max error %g (magnitude %g)", what, err, mag);
+  };
+  close(q, rq, "q_rope");
+  close(k, rk, "k_rope");
+  close(v, rv, "v");
+  close(probs, rp, "probs");
+  close(concat, rc, "concat");
+  close(attn_out, ro, "attn_out");
+}
+
 // engine.rs:3032-3053 (forward half of test_gpu_rmsnorm_correctness).
 void test_gpu_rmsnorm_correctness() {
   const size_t seq_len = 2, hidden_dim = 4;
@@ -414,6 +551,8 @@ int main(int argc, char **argv) {
   run("persistent_vram_gemm_correctness", test_persistent_vram_gemm_correctness);
   run("matmul_gpu_family", test_matmul_gpu_family);
   run("gpu_rmsnorm_correctness", test_gpu_rmsnorm_correctness);
+  run("gpu_batched_attention_execution", test_gpu_batched_attention_execution);
+  run("gpu_batched_attention_random", test_gpu_batched_attention_random);
   run("gpu_moe_forward", test_gpu_moe_forward);
   run("error_paths", test_error_paths);
   if (argc > 1) run("moe_config1_parity", [&] { test_moe_config1_parity(argv[1]); });
