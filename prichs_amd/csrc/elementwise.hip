@@ -546,15 +546,16 @@ extern "C" int prichs_rmsnorm_forward(const void *x, int x_dtype, const float *w
   return PRICHS_OK;
 }
 
-extern "C" int prichs_rope_forward_ld(void *qk, size_t row_stride, int dtype,
-                                      const float *cos_cache, const float *sin_cache,
-                                      size_t cache_rows, size_t batch, size_t seq_len,
-                                      size_t n_heads, size_t head_dim, size_t pos_offset, int sign,
-                                      void *stream) {
+// RoPE with the sine multiplied by sin_scale (+1 forward, -1 inverse; the
+// legacy launcher passes its int backward_sign through, as kernels.cu:543
+// does).
+static int rope_impl(void *qk, size_t row_stride, int dtype, const float *cos_cache,
+                     const float *sin_cache, size_t cache_rows, size_t batch, size_t seq_len,
+                     size_t n_heads, size_t head_dim, size_t pos_offset, float sin_scale,
+                     void *stream) {
   PRICHS_REQUIRE(dtype_ok(dtype), "rope: bad dtype %d", dtype);
   PRICHS_REQUIRE(head_dim >= 2 && head_dim % 2 == 0, "rope: head_dim=%zu must be even",
                  head_dim);
-  PRICHS_REQUIRE(sign == 1 || sign == -1, "rope: sign must be +1 or -1");
   PRICHS_REQUIRE(seq_len + pos_offset <= cache_rows,
                  "rope: positions up to %zu exceed the cache (%zu rows)", seq_len + pos_offset,
                  cache_rows);
@@ -567,12 +568,22 @@ extern "C" int prichs_rope_forward_ld(void *qk, size_t row_stride, int dtype,
   hipStream_t s = as_stream(stream);
   if (dtype == PRICHS_DTYPE_BF16)
     launch_rope_t<bf16_t>(qk, row_stride, cos_cache, sin_cache, batch, seq_len, n_heads,
-                          head_dim, pos_offset, (float)sign, s);
+                          head_dim, pos_offset, sin_scale, s);
   else
     launch_rope_t<float>(qk, row_stride, cos_cache, sin_cache, batch, seq_len, n_heads, head_dim,
-                         pos_offset, (float)sign, s);
+                         pos_offset, sin_scale, s);
   PRICHS_LAUNCH_CHECK("rope launch");
   return PRICHS_OK;
+}
+
+extern "C" int prichs_rope_forward_ld(void *qk, size_t row_stride, int dtype,
+                                      const float *cos_cache, const float *sin_cache,
+                                      size_t cache_rows, size_t batch, size_t seq_len,
+                                      size_t n_heads, size_t head_dim, size_t pos_offset, int sign,
+                                      void *stream) {
+  PRICHS_REQUIRE(sign == 1 || sign == -1, "rope: sign must be +1 or -1");
+  return rope_impl(qk, row_stride, dtype, cos_cache, sin_cache, cache_rows, batch, seq_len,
+                   n_heads, head_dim, pos_offset, (float)sign, stream);
 }
 
 extern "C" int prichs_rope_forward(void *qk, int dtype, const float *cos_cache,
@@ -760,9 +771,10 @@ extern "C" void launch_swiglu_forward(const float *dev_gate, const float *dev_up
 extern "C" void launch_rope(float *dev_q_or_k, const float *dev_cos_cache,
                             const float *dev_sin_cache, size_t seq_len, size_t num_heads,
                             size_t head_dim, int backward_sign, void *stream) {
-  (void)prichs_rope_forward(dev_q_or_k, PRICHS_DTYPE_F32, dev_cos_cache, dev_sin_cache, seq_len,
-                            1, seq_len, num_heads, head_dim, 0, backward_sign >= 0 ? 1 : -1,
-                            stream);
+  // sin * (float)backward_sign, whatever the int (kernels.cu:543).
+  (void)rope_impl(dev_q_or_k, num_heads * head_dim, PRICHS_DTYPE_F32, dev_cos_cache,
+                  dev_sin_cache, seq_len, 1, seq_len, num_heads, head_dim, 0,
+                  (float)backward_sign, stream);
 }
 
 extern "C" void launch_moe_gather(const float *dev_in, const int *dev_token_indices,

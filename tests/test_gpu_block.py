@@ -204,6 +204,17 @@ def test_block_small(cuda, orc):
     _check_block(orc, inp)
 
 
+@pytest.mark.parametrize("k", [1, 4])
+def test_block_other_top_k(cuda, orc, k):
+    # The block's final residual add rides in the combine, whose top-k is a
+    # compile-time constant for k = 2 and a run-time loop otherwise: out ==
+    # x1 + moe_out bit for bit (f32 and bf16) and the sub-layers against the
+    # oracle, at k = 1 and k = 4.
+    inp = synth.make_block_inputs(batch=1, seq_len=64, k=k, name=f"block-1x64-k{k}")
+    say("block top-k", k)
+    _check_block(orc, inp)
+
+
 def test_block_config5_full(cuda, orc):
     inp = synth.make_block_inputs()  # config 5: 4 x 2048, theta 500000
     say("block config5", inp.batch, inp.seq_len)

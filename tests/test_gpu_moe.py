@@ -253,6 +253,33 @@ def test_aux_free_bias_update_on_device(cuda, orc):
     layer.engine.close()
 
 
+@pytest.mark.parametrize("E,k", [(6, 1), (5, 3), (7, 2)])
+def test_decode_fused_permutation_other_experts(cuda, orc, E, k):
+    # The quad router (5-8 experts) writes the permutation itself when one
+    # workgroup covers the batch; with fewer than 8 experts and k != 2 its
+    # outputs equal the separate permute kernel's, and the layer matches the
+    # oracle (routing bit-exact, outputs within 2e-2).
+    inp = synth.make_moe_inputs(T=17, d=256, f=128, E=E, k=k, dtype="bf16", seed=E * 10 + k,
+                                name=f"decode-E{E}-k{k}")
+    say("fused permutation", E, k)
+    assert ops.router_num_blocks(inp.T, E) == 1
+    layer = moe.MoELayer.from_inputs(inp)
+    out, stash = layer.forward_train(inp.x)
+    r = orc.moe_forward(inp)
+    np.testing.assert_array_equal(stash.selected_experts, r["sel"])
+    np.testing.assert_array_equal(stash.row_token, r["row_token"])
+    assert rel_err(out, r["out"]) <= TOL["bf16"]
+    _, idx, w, bc = ops.router_topk(dev(inp.x, inp.dtype), dev(inp.w_router),
+                                    dev(inp.router_bias), inp.k)
+    off, rt, rw, tr = ops.permute(idx, w, bc, inp.E)
+    h = layer.engine.stash()
+    np.testing.assert_array_equal(host(h["offsets"]), host(off))
+    np.testing.assert_array_equal(host(h["row_token"]), host(rt))
+    np.testing.assert_array_equal(host(h["row_weight"]).view(np.uint32), host(rw).view(np.uint32))
+    np.testing.assert_array_equal(host(h["token_row"]), host(tr))
+    layer.engine.close()
+
+
 # ------------------------------------------------------------- full layer --
 @pytest.mark.parametrize("cfg", [1, 2, 4])
 def test_moe_layer_full_against_oracle(cuda, orc, cfg):

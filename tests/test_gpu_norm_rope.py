@@ -100,6 +100,14 @@ def test_legacy_rope_identity_and_sign(cuda, orc):
     cos_d, sin_d = dev(cos), dev(sin)
     lib.launch_rope(ptr(qd), ptr(cos_d), ptr(sin_d), S, H, hd, 1, None)
     np.testing.assert_array_equal(host(qd), orc.rope_forward(q, cos, sin))
+    # kernels.cu:543 multiplies sin by (float)backward_sign for any int: -1 is
+    # the inverse rotation (the oracle's rotation with -sin), 0 scales both
+    # elements of each pair by cos, 2 doubles the sine term.
+    for sign in (-1, 0, 2):
+        qd = dev(q)
+        lib.launch_rope(ptr(qd), ptr(cos_d), ptr(sin_d), S, H, hd, sign, None)
+        s2 = (np.float32(sign) * sin).astype(np.float32)
+        np.testing.assert_array_equal(host(qd), orc.rope_forward(q, cos, s2))
 
 
 def test_legacy_swiglu_gather_scatter(cuda, orc):
