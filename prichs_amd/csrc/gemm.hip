@@ -366,19 +366,42 @@ __device__ __forceinline__ void bf16_tile(
   wait_vmcnt(min(2, KT - 1) * kInstPerStage);  // own share of stage 0
   pp_barrier();
   if (grp == 1) pp_barrier();  // group 1 runs one phase behind
-  for (int kt = 0; kt < KT; ++kt) {
+  // One K-step.  `ahead` = own stages still allowed in flight after the wait
+  // (stages kt + 2 .. min(kt + 3, KT - 1)) is a compile-time count, so the
+  // wait is one instruction: a count computed at run time compiled into a
+  // branch tree of ~20 scalar instructions per step, which cost 10% of the
+  // kernel.  kFirst: the MFMAs start from an inline zero, not from acc.
+  auto kstep = [&](int kt, auto ahead_c, auto first_c) {
+    constexpr int kAhead = decltype(ahead_c)::value;
+    constexpr bool kFirst = decltype(first_c)::value;
     read_frags(kt);
-    if (kt + 3 < KT) issue_stage(kt + 3);
-    // Own shares still allowed in flight: stages kt + 2 .. min(kt + 3, KT - 1).
-    wait_vmcnt(max(0, min(kt + 3, KT - 1) - kt - 1) * kInstPerStage);
+    if constexpr (kAhead == 2) issue_stage(kt + 3);
+    PRICHS_WAIT_VMCNT(kAhead * kInstPerStage);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS reads done
     pp_barrier();
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(F.w[j], F.a[i], acc[i][j]);
+      for (int j = 0; j < NJ; ++j)
+        acc[i][j] = mfma_bf16(F.w[j], F.a[i], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
     pp_barrier();
-  }
+  };
+  using A2 = std::integral_constant<int, 2>;
+  using A1 = std::integral_constant<int, 1>;
+  using A0 = std::integral_constant<int, 0>;
+  // K-step 0, the steady state that issues stage kt + 3, then the last
+  // (up to three) steps.
+  if (KT > 3)
+    kstep(0, A2{}, bool_c<true>{});
+  else if (KT == 3)
+    kstep(0, A1{}, bool_c<true>{});
+  else
+    kstep(0, A0{}, bool_c<true>{});
+  int kt = 1;
+  for (; kt + 3 < KT; ++kt) kstep(kt, A2{}, bool_c<false>{});
+  if (kt + 2 < KT) kstep(kt++, A1{}, bool_c<false>{});
+  if (kt + 1 < KT) kstep(kt++, A0{}, bool_c<false>{});
+  if (kt < KT) kstep(kt++, A0{}, bool_c<false>{});
   if (grp == 0) pp_barrier();  // both groups leave after the same barrier count
 #else
   // Prologue: stages 0..3 in flight; stage 0 lands and is read.
