@@ -26,6 +26,7 @@
 // f32 kernel: 128x128x16 tiles on v_mfma_f32_16x16x4_f32 (the fp32-checked
 // mode; accumulates in fp32 like the reference CPU path).
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 #include <cstring>
 #include <vector>
@@ -1078,6 +1079,18 @@ template <typename T> void pack_down_impl(const float *down, size_t d, size_t f,
       put<T>(out, packed_index(n, k, f, sizeof(T) == 2), n < d ? down[k * d + n] : 0.0f);
 }
 
+// Workgroups of the persistent bf16 launches: one per CU, or at most
+// PRICHS_GEMM_MAX_CUS (read once) -- a cap that leaves CUs to other work
+// and measures how the kernels scale with the number of CUs in use.
+int gemm_cu_limit(int cus) {
+  static const int cap = [] {
+    const char *v = std::getenv("PRICHS_GEMM_MAX_CUS");
+    const int n = v ? std::atoi(v) : 0;
+    return n > 0 ? n : 0;
+  }();
+  return cap > 0 && cap < cus ? cap : cus;
+}
+
 // Half-width configuration of the last partial round (down / dense only).
 template <class Cf, bool GATEUP>
 using TailCfg = typename std::conditional<GATEUP, Cf,
@@ -1092,7 +1105,7 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
   // be split into halves).
   using CfT = TailCfg<Cf, GATEUP>;
   const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN) * (GATEUP ? 1 : 2);
-  const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)cus));
+  const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)gemm_cu_limit(cus)));
   static bool attr_set = false;
   if (!attr_set) {
     PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&bf16_gemm_kernel<Cf, CfT, GATEUP>),
