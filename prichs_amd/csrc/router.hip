@@ -709,6 +709,15 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __shared__ int base_s[PRICHS_MAX_EXPERTS];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  // This block's first 64 (token, slot) entries and its shared rows do not
+  // depend on the histograms: their loads and stores go out first, so their
+  // latency overlaps the histogram reads instead of following them.
+  const int t0 = b * tpb, t1 = min(T, (b + 1) * tpb);
+  const size_t s0 = (size_t)t0 * k, s1 = (size_t)t1 * k;
+  const bool live0 = tid < 64 && s0 + tid < s1;
+  const int e0 = live0 ? topk_idx[s0 + tid] : -1;
+  const float w0 = live0 ? topk_w[s0 + tid] : 0.0f;
+  for (int t = t0 + tid; t < t1; t += blockDim.x) row_token[(size_t)T * k + t] = t;
   if (tid < E) {
     tot_s[tid] = 0;
     pre_s[tid] = 0;
@@ -757,8 +766,31 @@ __global__ __launch_bounds__(256) void permute_kernel(
     }
   }
   __syncthreads();
-  place_entries(topk_idx, topk_w, b * tpb, min(T, (b + 1) * tpb), T, E, k, base_s, row_token,
-                row_weight, token_row);
+  // Stable placement (place_entries' order), the first window from the
+  // registers loaded above.
+  if (tid < 64) {
+    const int lane = tid;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int base = lane < E ? base_s[lane] : 0;  // running base of expert `lane`
+    for (size_t ws = s0; ws < s1; ws += 64) {
+      const size_t ts = ws + lane;
+      const bool live = ts < s1;
+      const int e_me = ws == s0 ? e0 : (live ? topk_idx[ts] : -1);
+      const float wt = ws == s0 ? w0 : (live ? topk_w[ts] : 0.0f);
+      int r = -1;
+      for (int e = 0; e < E; ++e) {
+        const uint64_t m = __ballot(e_me == e);
+        const int be = __shfl(base, e);
+        if (e_me == e) r = be + __popcll(m & lt);
+        if (lane == e) base += __popcll(m);
+      }
+      if (live && r >= 0) {
+        row_token[r] = (int32_t)(ts / k);
+        row_weight[r] = wt;
+        token_row[ts] = r;
+      }
+    }
+  }
 }
 
 template <typename XT, int LPT, int KC>
