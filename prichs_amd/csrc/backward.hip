@@ -400,22 +400,20 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
   issue(0);
   if (KT > 1) issue(1);
   if (KT > 2) issue(2);
-  for (int kt = 0; kt < KT; ++kt) {
-    // This wave's DMAs of stage kt have landed once at most the later
-    // stages' (4 instructions each) are outstanding.
-    const int ahead = min(2, KT - 1 - kt);
-    if (ahead == 2)
-      PRICHS_WG_VMCNT(8);
-    else if (ahead == 1)
-      PRICHS_WG_VMCNT(4);
-    else
-      PRICHS_WG_VMCNT(0);
+  // One K-step.  kAhead = this wave's later stages (4 instructions each)
+  // still allowed in flight when stage kt has landed: a compile-time count,
+  // so the wait is one instruction and the steady state carries no branch.
+  auto kstep = [&](int kt, auto ahead_c) {
+    constexpr int kAhead = decltype(ahead_c)::value;
+    PRICHS_WG_VMCNT(4 * kAhead);
     // Every wave's DMAs of stage kt landed, and every wave is done reading
     // stage kt - 1, whose slot the next issue refills.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + 3 < KT) issue(kt + 3);
+    if constexpr (kAhead == 2) {
+      if (kt + 3 < KT) issue(kt + 3);
+    }
     const uint32_t st = (uint32_t)(kt & (kStages - 1)) * kStageBytes;
     u32x2 alo[8], ahi[8], bt[8];  // bt: B lo (0..3) and hi (4..7)
 #pragma unroll
@@ -442,7 +440,13 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
         acc[jb][ib] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, af, acc[jb][ib], 0, 0, 0);
       }
     }
-  }
+  };
+  // Steps with two later stages in flight (issuing stage kt + 3 when it
+  // exists), then the last two.
+  int kt = 0;
+  for (; kt + 2 < KT; ++kt) kstep(kt, std::integral_constant<int, 2>{});
+  if (kt + 1 < KT) kstep(kt++, std::integral_constant<int, 1>{});
+  if (kt < KT) kstep(kt++, std::integral_constant<int, 0>{});
 
   // acc[jb][ib] lane l holds out[i = 16 ib + l % 16][j = 16 jb + 4 (l / 16) + r]
   // of the wave's 128 x 64 block.
