@@ -155,6 +155,46 @@ def copy_same_bytes_flushed(moved_bytes: int, flush, reps: int = 10):
     return {"ms": ms, "GB/s": 2 * n * 4 / (ms * 1e-3) / 1e9}
 
 
+def library_dense_equivalent(rows: int, d: int, f: int, reps: int = 50, rounds: int = 3):
+    """Vendor-library yardstick for the expert GEMMs: torch.matmul (hipBLASLt)
+    on one dense bf16 GEMM per expert GEMM with the same total rows and
+    FLOPs -- [rows, d] x [d, 2f] for gate/up and [rows, f] x [f, d] for down,
+    weights stored [N, K] as the packed expert weights are -- with no row
+    gather, no ragged groups and no fused SwiGLU.  Event-timed: after 20
+    warmup calls, `rounds` means of `reps` back-to-back calls; the best mean
+    is reported (the library's run-to-run spread is large).  A measurement
+    beside the product, never part of it."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    out = {}
+    for name, (m, n, kk) in (("gate_up", (rows, 2 * f, d)), ("down", (rows, d, f))):
+        a = torch.randn(m, kk, device="cuda", dtype=torch.bfloat16, generator=g)
+        w = torch.randn(n, kk, device="cuda", dtype=torch.bfloat16, generator=g)
+        c = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+        for _ in range(20):
+            torch.matmul(a, w.t(), out=c)
+        means = []
+        for _ in range(rounds):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                torch.matmul(a, w.t(), out=c)
+            e1.record()
+            torch.cuda.synchronize()
+            means.append(e0.elapsed_time(e1) / reps)
+        ms = min(means)
+        tf = 2.0 * m * n * kk / (ms * 1e-3) / 1e12
+        out[name] = {"shape_MNK": [m, n, kk], "ms": ms, "TFLOP/s": tf,
+                     "frac_of_peak": tf / PEAK_BF16_TFLOPS, "ms_round_means": means}
+        del a, w, c
+    tot = out["gate_up"]["ms"] + out["down"]["ms"]
+    out["both"] = {"ms": tot, "TFLOP/s": 6.0 * rows * d * f / (tot * 1e-3) / 1e12,
+                   "frac_of_peak": 6.0 * rows * d * f / (tot * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+    out["library"] = f"torch {torch.__version__} matmul (hipBLASLt), bf16 in/out, fp32 accumulate"
+    return out
+
+
 def committed_digest(name: str):
     try:
         with open(os.path.join(ROOT, "tests", "golden", "input_sha256.json")) as fh:
@@ -298,6 +338,10 @@ def main():
                 "combine": copy_same_bytes_flushed((T * k + S * T) * d * es_ + T * k * 12
                                                    + T * d * es_, flush)}
     del flush
+    # Library yardstick (prefill bf16 shapes only; decode is HBM-bound).
+    rows_ = T * k + S * T
+    lib = (library_dense_equivalent(rows_, d, f)
+           if inp.dtype == "bf16" and T * k >= 64 * E else None)
     log(f"bench: timing pass, {args.warmup} warmup + {args.steps} timed steps")
     elapsed = timed_pass(fwd, args.steps, args.warmup)
     log("bench: stage ms", json.dumps({kk: round(v, 4) for kk, v in ms.items()}))
@@ -373,7 +417,8 @@ def main():
         "roofline": roofline,
         "expert_gemm": {"tflops": gemm_tflops, "frac_of_peak": gemm_tflops / peak,
                         "gate_up_ms": ms["gate_up"], "down_ms": ms["down"],
-                        "down_tflops": flops_down / t_dn / 1e12},
+                        "down_tflops": flops_down / t_dn / 1e12,
+                        "library_dense_same_flops": lib},
         "memory_bound_stages": {
             "router": {"ms": ms["router"], "GB/s": gbps(router_bytes, "router"),
                        "ms_flushed": ms_cold["router"],

@@ -219,6 +219,12 @@ using Bf16 = Bf16Cfg<256, 256, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
 using Bf16Down = Bf16Cfg<PRICHS_DOWN_BM, PRICHS_DOWN_BN, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
 static_assert(Bf16::BN % Bf16Down::BN == 0,
               "packed weights are padded to Bf16::BN rows, a whole number of down N tiles");
+// Dense (single-group) launches whose padded N is a multiple of 384 may use
+// 128 x 384 tiles instead: three quarters of a 256 x 256 tile's work, and a
+// tile count that can fill the CUs where 256 x 256 tiles leave a round part
+// empty (8192 x 1536 outputs: 256 such tiles against 192).  Each output
+// element is the same MFMA chain over K either way, so the bits are the same.
+using Bf16Wide = Bf16Cfg<128, 384, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
 
 // C[m, n] = sum_k A[row(m), k] * B[n, k] for the rows of each group, with
 // B = packed weights [Np, K] of group g.  The MFMA takes the weight fragment
@@ -1091,21 +1097,29 @@ int gemm_cu_limit(int cus) {
   return cap > 0 && cap < cus ? cap : cus;
 }
 
-// Half-width configuration of the last partial round (down / dense only).
+// Half-width configuration of the last partial round (down / dense only,
+// and only where half a tile is still a whole number of B loads per wave).
 template <class Cf, bool GATEUP>
-using TailCfg = typename std::conditional<GATEUP, Cf,
-                                          Bf16Cfg<Cf::BM, Cf::BN / 2, Cf::WGM, Cf::WGN>>::type;
+using TailCfg = typename std::conditional<
+    GATEUP || (Cf::BN / 2) % (Cf::kRowsPerInst * Cf::kWaves) != 0, Cf,
+    Bf16Cfg<Cf::BM, Cf::BN / 2, Cf::WGM, Cf::WGN>>::type;
+
+// Persistent grid of a bf16 launch: one workgroup per CU (the LDS ring allows
+// one), fewer when the launch has fewer tiles (twice the tiles when the last
+// round may be split into halves).
+template <class Cf, bool GATEUP>
+size_t bf16_grid(size_t max_rows, int G, int Np, int cus) {
+  const bool halves = !std::is_same<Cf, TailCfg<Cf, GATEUP>>::value;
+  const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN) * (halves ? 2 : 1);
+  return std::max<size_t>(1, std::min<size_t>(ub, (size_t)gemm_cu_limit(cus)));
+}
 
 template <class Cf, bool GATEUP>
 int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                 int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
                 int dense_m, size_t max_rows, int cus, hipStream_t s, void *pre) {
-  // Persistent grid: one workgroup per CU (the LDS ring allows one), fewer
-  // when the launch has fewer tiles (twice the tiles when the last round may
-  // be split into halves).
   using CfT = TailCfg<Cf, GATEUP>;
-  const size_t ub = (max_rows / Cf::BM + G) * (size_t)(Np / Cf::BN) * (GATEUP ? 1 : 2);
-  const int grid = (int)std::max<size_t>(1, std::min<size_t>(ub, (size_t)gemm_cu_limit(cus)));
+  const int grid = (int)bf16_grid<Cf, GATEUP>(max_rows, G, Np, cus);
   static bool attr_set = false;
   if (!attr_set) {
     PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&bf16_gemm_kernel<Cf, CfT, GATEUP>),
@@ -1126,6 +1140,37 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
                      stage_c, static_cast<bf16_t *>(pre));
   PRICHS_LAUNCH_CHECK("grouped gemm launch");
   return PRICHS_OK;
+}
+
+// Tile-times (in units of the configuration's own tile) of a persistent
+// launch of `tiles` tiles on `grid` workgroups: whole rounds, plus the last
+// partial round -- 0.6 of a tile-time when its tiles are split into
+// half-width tiles (split allowed and twice the tail fits the grid; measured
+// on MI355X: 8192 x 2304 x 1536 takes 1.59 tile-times of a full round), else
+// a full one.
+double launch_tile_times(size_t tiles, size_t grid, bool split) {
+  const size_t full = tiles / grid, tail = tiles % grid;
+  if (tail == 0) return (double)full;
+  return (double)full + (split && 2 * tail <= grid ? 0.6 : 1.0);
+}
+
+// Work of one 128 x 384 tile against a 256 x 256 one, and the rate of the
+// narrower tile (fewer MFMAs per barrier and per byte staged) against the
+// square one's, measured on MI355X in whole rounds (32768 x 1536 x 1536:
+// 124.7 us as 1024 wide tiles, 120.2 us as 768 square ones).
+constexpr double kWideWork = 0.75, kWideRate = 0.96;
+
+// Whether a dense launch of M rows and Np packed columns runs faster as
+// 128 x 384 tiles than as 256 x 256 tiles with half-width tails, each on the
+// grid launch_bf16 gives it.
+bool dense_prefers_wide(size_t M, size_t Np, int cus) {
+  if (Np % Bf16Wide::BN != 0) return false;
+  const size_t sq = ((M + Bf16Down::BM - 1) / Bf16Down::BM) * (Np / Bf16Down::BN);
+  const size_t wd = ((M + Bf16Wide::BM - 1) / Bf16Wide::BM) * (Np / Bf16Wide::BN);
+  const double t_sq = launch_tile_times(sq, bf16_grid<Bf16Down, false>(M, 1, Np, cus), true);
+  const double t_wd = launch_tile_times(wd, bf16_grid<Bf16Wide, false>(M, 1, Np, cus), false) *
+                      kWideWork / kWideRate;
+  return t_wd < t_sq;
 }
 
 template <bool GATEUP, int U, int SK>
@@ -1200,6 +1245,9 @@ int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, c
     if (gateup)
       return launch_bf16<Bf16, true>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
                                      offsets, G, dense_m, max_rows, cus, s, pre);
+    if (offsets == nullptr && dense_prefers_wide((size_t)dense_m, (size_t)Np, cus))
+      return launch_bf16<Bf16Wide, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
+                                          offsets, G, dense_m, max_rows, cus, s, nullptr);
     return launch_bf16<Bf16Down, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
                                         offsets, G, dense_m, max_rows, cus, s, nullptr);
   } else {

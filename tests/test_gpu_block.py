@@ -50,39 +50,77 @@ def test_dense_gemm(cuda, orc, M, K, N):
     assert not hw[:, :32].any() and not hw[:, 32 + N:].any()
 
 
-def _tail_split(M, n_tiles, cus, bm=256):
-    """Whether the dense GEMM computes its last partial round as half-width
-    tiles: the launcher's grid is min(2 (M/bm + 1) n_tiles, CUs), and a tail
-    of t tiles is split when 2 t fits the grid."""
-    tiles = -(-M // bm) * n_tiles
-    grid = min(2 * (M // bm + 1) * n_tiles, cus)
-    tail = tiles % grid
-    return 0 < tail and 2 * tail <= grid
+def _tile_times(tiles, grid, split):
+    full, tail = divmod(tiles, grid)
+    if tail == 0:
+        return full
+    return full + (0.6 if split and 2 * tail <= grid else 1.0)
+
+
+def _dense_cfg(M, N, cus):
+    """Mirror of the dense launcher's choice: ("wide" | "square", tail split).
+    Square = 256 x 256 tiles on a grid of min(2 (M/256 + 1) N/256, CUs) whose
+    last partial round of t tiles is split into half-width tiles when 2 t fits
+    the grid; wide = 128 x 384 tiles (N a multiple of 384) on min((M/128 + 1)
+    N/384, CUs), never split, each 0.75 of a square tile's work at 0.96 of its
+    rate.  The faster estimate wins."""
+    sq_tiles = -(-M // 256) * (N // 256)
+    sq_grid = min(2 * (M // 256 + 1) * (N // 256), cus)
+    tail = sq_tiles % sq_grid
+    split = 0 < tail and 2 * tail <= sq_grid
+    if N % 384 == 0:
+        wd_tiles = -(-M // 128) * (N // 384)
+        wd_grid = min((M // 128 + 1) * (N // 384), cus)
+        if _tile_times(wd_tiles, wd_grid, False) * 0.75 / 0.96 < _tile_times(sq_tiles, sq_grid, True):
+            return "wide", False
+    return "square", split
 
 
 def test_gemm_tail_round_halves_bit_identical(cuda):
     """The last partial round of the down / dense GEMM runs as half-width
-    tiles: every output element is the same MFMA chain over K, so rows
-    computed that way are bit-identical to the same rows of a launch that
-    computes them as whole tiles, and within the 1e-2 bar of float64."""
+    tiles, and some dense launches run as 128 x 384 tiles: every output
+    element is the same MFMA chain over K, so rows computed either way are
+    bit-identical to the same rows of a launch that computes them as whole
+    256 x 256 tiles, and within the 1e-2 bar of float64."""
     K = N = 1536
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     rng = np.random.default_rng(11)
     a = synth.round_bf16(rng.standard_normal((20000, K)))
     w = synth.round_bf16(0.05 * rng.standard_normal((K, N)))
     wp = ops.to_device_packed([ops.pack_weight(w, "bf16")], "bf16")
-    assert not _tail_split(20000, N // 256, cus)
+    assert _dense_cfg(20000, N, cus) == ("square", False)
     whole = host(ops.gemm(dev(a), wp, N))
-    split_seen = False
-    for M in (4096, 12000, 12288):
-        split_seen |= _tail_split(M, N // 256, cus)
-        say(f"dense gemm M={M}: tail split {_tail_split(M, N // 256, cus)} on {cus} CUs")
+    seen = set()
+    for M in (4096, 8192, 12000, 12288):
+        cfg = _dense_cfg(M, N, cus)
+        seen.add(cfg)
+        say(f"dense gemm M={M}: tiles {cfg[0]}, tail split {cfg[1]} on {cus} CUs")
         c = host(ops.gemm(dev(a[:M]), wp, N))
         np.testing.assert_array_equal(c, whole[:M])
         lo = max(0, M - 2048)  # the tail tiles hold the last M-tiles
         ref = a[lo:M].astype(np.float64) @ w.astype(np.float64)
         assert rel_err(c[lo:], ref) <= 1e-2
-    assert split_seen or cus > 512, "no shape exercised the half-width tail tiles"
+    if cus == 256:
+        assert ("square", True) in seen and ("wide", False) in seen, seen
+
+
+def test_dense_gemm_wide_tiles_qkv_shape(cuda, orc):
+    """The block's q/k/v projection shape (8192 x 2304, K = 1536) runs as
+    128 x 384 tiles on 256 CUs: against the oracle's matmul_2d on a row slice
+    and bit-identical to the rows of a square-tile launch."""
+    M, K, N = 8192, 1536, 2304
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    say(f"dense gemm {M}x{N}x{K}: tiles {_dense_cfg(M, N, cus)[0]} on {cus} CUs")
+    rng = np.random.default_rng(5)
+    a = synth.round_bf16(rng.standard_normal((M, K)))
+    w = synth.round_bf16(0.05 * rng.standard_normal((K, N)))
+    wp = ops.to_device_packed([ops.pack_weight(w, "bf16")], "bf16")
+    c = host(ops.gemm(dev(a), wp, N))
+    ref = orc.matmul_2d(a[-256:], w)
+    assert rel_err(c[-256:], ref) <= 1e-2
+    M2 = 2048  # square tiles with a half-width tail
+    assert _dense_cfg(M2, N, cus)[0] == "square"
+    np.testing.assert_array_equal(host(ops.gemm(dev(a[:M2]), wp, N)), c[:M2])
 
 
 def test_residual_add_bit_exact(cuda):
