@@ -69,11 +69,6 @@ constexpr int kBf16KMultiple = 64;   // bf16 kernels need d and f to be multiple
 #ifndef PRICHS_BAND_M
 #define PRICHS_BAND_M 4
 #endif
-// K loop of the bf16 tiles: 1 = ping-pong (wave groups alternate MFMA and
-// memory phases), 0 = both groups in step.
-#ifndef PRICHS_PINGPONG
-#define PRICHS_PINGPONG 1
-#endif
 
 // ------------------------------------------------------------------------
 // Tile scheduler shared by the kernels.
@@ -103,6 +98,59 @@ __device__ inline void build_tile_map(TileMap &tm, const int32_t *offsets, int G
     tm.offs[G] = offsets[G];
   }
   __syncthreads();
+}
+
+// The same table held in registers by every wave of a launch (the bf16
+// kernels' LDS is all ring): entry e <= G -- the first global M-tile (prefix)
+// and first row (offs) of group e -- sits in lane e % 64 of word e / 64.
+struct WaveTileMap {
+  int prefix[2], offs[2];
+  int G, m_tiles;
+};
+
+__device__ inline void build_wave_tile_map(WaveTileMap &tm, const int32_t *offsets, int G,
+                                           int BM, int dense_m) {
+  static_assert(kMaxGroups + 1 <= 128, "two words per lane hold the group table");
+  const int lane = threadIdx.x & 63;
+  tm.G = G;
+  int carry = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = 64 * h + lane;
+    int off, next;
+    if (offsets == nullptr) {  // dense: one group of dense_m rows
+      off = e == 0 ? 0 : dense_m;
+      next = dense_m;
+    } else {
+      off = offsets[min(e, G)];
+      next = offsets[min(e + 1, G)];
+    }
+    const int tiles = (e < G && next > off) ? (next - off + BM - 1) / BM : 0;
+    int inc = tiles;  // inclusive scan over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int t = __shfl_up(inc, d);
+      if (lane >= d) inc += t;
+    }
+    tm.prefix[h] = carry + inc - tiles;
+    tm.offs[h] = off;
+    carry += __shfl(inc, 63);
+  }
+  tm.m_tiles = carry;
+}
+
+// Entry e (wave-uniform) of one of the two-word tables.
+__device__ __forceinline__ int wave_entry(const int (&w)[2], int e) {
+  return e < 64 ? __builtin_amdgcn_readlane(w[0], e) : __builtin_amdgcn_readlane(w[1], e - 64);
+}
+
+// Group of global M-tile mt: the number of groups e in [1, G) whose first
+// M-tile is <= mt (prefix is nondecreasing; empty groups own no tiles).
+__device__ __forceinline__ int wave_find_group(const WaveTileMap &tm, int mt) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long b0 = __ballot(lane >= 1 && lane < tm.G && tm.prefix[0] <= mt);
+  const unsigned long long b1 = __ballot(64 + lane < tm.G && tm.prefix[1] <= mt);
+  return __builtin_amdgcn_readfirstlane(__popcll(b0) + __popcll(b1));
 }
 
 // Group of global M-tile mt (empty groups own no tiles and are skipped).
@@ -174,6 +222,11 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 w, bf16x8 a, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, a, c, 0, 0, 0);
 }
 
+template <int... Is, class F>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, Is...>, F &&f) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+
 // Workgroup barrier without a memory fence: LDS-DMA completion is tracked by
 // the explicit vmcnt waits, and a fence would force vmcnt(0).
 __device__ inline void lds_barrier() {
@@ -182,8 +235,11 @@ __device__ inline void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
-  static constexpr int BM = BM_, BN = BN_, BK = kBK, kStages = 4;
+#ifndef PRICHS_BF16_STAGES
+#define PRICHS_BF16_STAGES 4
+#endif
+template <int BM_, int BN_, int WGM_, int WGN_, int S_ = PRICHS_BF16_STAGES> struct Bf16Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = kBK, kStages = S_;
   static constexpr int WGM = WGM_, WGN = WGN_;
   static constexpr int kWaves = WGM * WGN;
   static constexpr int kThreads = 64 * kWaves;
@@ -204,7 +260,7 @@ template <int BM_, int BN_, int WGM_, int WGN_> struct Bf16Cfg {
   static_assert(MI % 2 == 0 && WN % 16 == 0, "two A halves and whole fragments per wave");
   static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
                 "the DMA instructions of one stage cover the A and B tiles exactly");
-  static_assert(3 * kInstPerStage <= 63, "vmcnt immediates");
+  static_assert(kStages >= 3 && (kStages - 1) * kInstPerStage <= 63, "vmcnt immediates");
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a gfx950 CU");
 };
 // gate/up: 256x256 tiles; down: PRICHS_DOWN_BM x 256 tiles (smaller M tiles
@@ -242,7 +298,7 @@ template <class Cf, bool GATEUP>
 __device__ __forceinline__ void bf16_tile(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
-    bf16_t *__restrict__ C, int ldc, int n_store, const TileMap &tm, int G, int stage_c,
+    bf16_t *__restrict__ C, int ldc, int n_store, const WaveTileMap &tm, int stage_c,
     bf16_t *__restrict__ P, bf16_t *lds, int mt, int nt) {
   constexpr int BM = Cf::BM, BN = Cf::BN, BK = Cf::BK, kStages = Cf::kStages;
   constexpr int WGN = Cf::WGN, WM = Cf::WM, WN = Cf::WN, MI = Cf::MI, NJ = Cf::NJ;
@@ -270,10 +326,10 @@ __device__ __forceinline__ void bf16_tile(
   // B stage: whole packed fragments in weight order, lane-major (1 KiB each).
   const int b_rd = wn * WN * BK + lane * 8;
 
-  const int g = find_group(tm, G, mt);
-  const int row0 = tm.offs[g];
-  const int mg = tm.offs[g + 1] - row0;
-  const int m0 = (mt - tm.prefix[g]) * BM;
+  const int g = wave_find_group(tm, mt);
+  const int row0 = wave_entry(tm.offs, g);
+  const int mg = wave_entry(tm.offs, g + 1) - row0;
+  const int m0 = (mt - wave_entry(tm.prefix, g)) * BM;
   const int n0 = nt * BN;
 
   // A offsets are 64-bit (gathered rows: src * lda can pass 2^32 elements for
@@ -311,7 +367,7 @@ __device__ __forceinline__ void bf16_tile(
 
   // DMA instruction `which` of stage kt_: A rows first, then B fragments.
   auto issue_one = [&](int kt_, int which) {
-    bf16_t *st_ = lds + (kt_ & (kStages - 1)) * kStageElems;
+    bf16_t *st_ = lds + (kt_ % kStages) * kStageElems;
     if (which < kInstA) {
       dma_16b(A + a_goff[which] + kt_ * BK, st_ + (wave * kInstA + which) * kRowsPerInst * BK);
     } else {
@@ -325,11 +381,11 @@ __device__ __forceinline__ void bf16_tile(
     for (int w = 0; w < kInstPerStage; ++w) issue_one(kt_, w);
   };
 
-#if PRICHS_PINGPONG
-  // Ping-pong K loop.  Waves 0-3 (group 0) and 4-7 (group 1) sit one per
-  // SIMD each, so every SIMD hosts one wave of each group.  Every wave runs
-  // the same sequence per K-step kt -- a memory phase (read its fragments of
-  // stage kt from LDS, issue its share of stage kt + 3, wait for its share of
+  // Ping-pong K loop over a ring of S = kStages LDS stages, S - 1 of them in
+  // flight.  Waves 0-3 (group 0) and 4-7 (group 1) sit one per SIMD each, so
+  // every SIMD hosts one wave of each group.  Every wave runs the same
+  // sequence per K-step kt -- a memory phase (read its fragments of stage kt
+  // from LDS, issue its share of stage kt + S - 1, wait for its share of
   // stage kt + 1 and for its own LDS reads), a barrier, an MFMA phase on
   // those fragments, a barrier -- but group 1 starts one barrier late, so on
   // each SIMD one wave issues MFMAs while the other does its LDS reads and
@@ -340,7 +396,7 @@ __device__ __forceinline__ void bf16_tile(
   //  - Stage s is first read after b(2s-1); both groups waited for their
   //    shares of it in their memory phases of step s - 1, which end at b(2s-2)
   //    and b(2s-1).
-  //  - The share of stage kt + 3 issued in step kt's memory phase goes to
+  //  - The share of stage kt + S - 1 issued in step kt's memory phase goes to
   //    stage kt - 1's slot; both groups' LDS reads of stage kt - 1 completed
   //    before b(2kt-2) and b(2kt-1), and step kt's memory phases start after
   //    b(2kt-1) and b(2kt).
@@ -358,7 +414,7 @@ __device__ __forceinline__ void bf16_tile(
     bf16x8 w[NJ], a[MI];
   } F;
   auto read_frags = [&](int st) {
-    const bf16_t *as = lds + (st & (kStages - 1)) * kStageElems;
+    const bf16_t *as = lds + (st % kStages) * kStageElems;
     const bf16_t *bs = as + BM * BK;
 #pragma unroll
     for (int jj = 0; jj < NJ; ++jj)
@@ -367,22 +423,21 @@ __device__ __forceinline__ void bf16_tile(
     for (int ii = 0; ii < MI; ++ii)
       F.a[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + ii * 16 * BK);
   };
-  issue_stage(0);
-  if (KT > 1) issue_stage(1);
-  if (KT > 2) issue_stage(2);
-  wait_vmcnt(min(2, KT - 1) * kInstPerStage);  // own share of stage 0
+  constexpr int kMaxAhead = kStages - 2;  // own stages in flight after a step's wait
+  for (int s_ = 0; s_ <= kMaxAhead && s_ < KT; ++s_) issue_stage(s_);
+  wait_vmcnt(min(kMaxAhead, KT - 1) * kInstPerStage);  // own share of stage 0
   pp_barrier();
   if (grp == 1) pp_barrier();  // group 1 runs one phase behind
   // One K-step.  `ahead` = own stages still allowed in flight after the wait
-  // (stages kt + 2 .. min(kt + 3, KT - 1)) is a compile-time count, so the
-  // wait is one instruction: a count computed at run time compiled into a
-  // branch tree of ~20 scalar instructions per step, which cost 10% of the
+  // (stages kt + 2 .. min(kt + S - 1, KT - 1)) is a compile-time count, so
+  // the wait is one instruction: a count computed at run time compiled into
+  // a branch tree of ~20 scalar instructions per step, which cost 10% of the
   // kernel.  kFirst: the MFMAs start from an inline zero, not from acc.
   auto kstep = [&](int kt, auto ahead_c, auto first_c) {
     constexpr int kAhead = decltype(ahead_c)::value;
     constexpr bool kFirst = decltype(first_c)::value;
     read_frags(kt);
-    if constexpr (kAhead == 2) issue_stage(kt + 3);
+    if constexpr (kAhead == kMaxAhead) issue_stage(kt + kStages - 1);
     PRICHS_WAIT_VMCNT(kAhead * kInstPerStage);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS reads done
     pp_barrier();
@@ -393,127 +448,27 @@ __device__ __forceinline__ void bf16_tile(
         acc[i][j] = mfma_bf16(F.w[j], F.a[i], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
     pp_barrier();
   };
-  using A2 = std::integral_constant<int, 2>;
-  using A1 = std::integral_constant<int, 1>;
+  // Step kt allows min(S - 2, KT - 2 - kt) stages in flight (at least 0):
+  // step 0 and the steady state issue stage kt + S - 1 and allow S - 2, the
+  // last steps count down to 0.
+  using AMax = std::integral_constant<int, kMaxAhead>;
   using A0 = std::integral_constant<int, 0>;
-  // K-step 0, the steady state that issues stage kt + 3, then the last
-  // (up to three) steps.
-  if (KT > 3)
-    kstep(0, A2{}, bool_c<true>{});
-  else if (KT == 3)
-    kstep(0, A1{}, bool_c<true>{});
-  else
-    kstep(0, A0{}, bool_c<true>{});
+  if (KT - 2 >= kMaxAhead) {
+    kstep(0, AMax{}, bool_c<true>{});
+  } else {
+    static_for(std::make_integer_sequence<int, kMaxAhead>{}, [&](auto i_c) {
+      constexpr int a = kMaxAhead - 1 - decltype(i_c)::value;
+      if (max(KT - 2, 0) == a) kstep(0, std::integral_constant<int, a>{}, bool_c<true>{});
+    });
+  }
   int kt = 1;
-  for (; kt + 3 < KT; ++kt) kstep(kt, A2{}, bool_c<false>{});
-  if (kt + 2 < KT) kstep(kt++, A1{}, bool_c<false>{});
-  if (kt + 1 < KT) kstep(kt++, A0{}, bool_c<false>{});
+  for (; kt + kStages - 1 < KT; ++kt) kstep(kt, AMax{}, bool_c<false>{});
+  static_for(std::make_integer_sequence<int, kMaxAhead>{}, [&](auto i_c) {
+    constexpr int a = kMaxAhead - 1 - decltype(i_c)::value;
+    if (kt + a + 1 < KT) kstep(kt++, std::integral_constant<int, a>{}, bool_c<false>{});
+  });
   if (kt < KT) kstep(kt++, A0{}, bool_c<false>{});
   if (grp == 0) pp_barrier();  // both groups leave after the same barrier count
-#else
-  // Prologue: stages 0..3 in flight; stage 0 lands and is read.
-  issue_stage(0);
-  if (KT > 1) issue_stage(1);
-  if (KT > 2) issue_stage(2);
-  if (KT > 3) issue_stage(3);
-  {
-    const int ahead = min(3, KT - 1);  // stages issued after stage 0
-    if (ahead == 3)
-      wait_vmcnt(3 * kInstPerStage);
-    else if (ahead == 2)
-      wait_vmcnt(2 * kInstPerStage);
-    else if (ahead == 1)
-      wait_vmcnt(kInstPerStage);
-    else
-      wait_vmcnt(0);
-  }
-  lds_barrier();
-
-  // Fragments of one stage in registers: B (w) and the second half of A
-  // (ahi).  Two sets swap roles from step to step; the first half of A
-  // (alo) is consumed before the barrier, so one set of it is enough.
-  struct Frags {
-    bf16x8 w[NJ], ahi[MI / 2];
-  };
-  Frags fa, fb;
-  bf16x8 alo[MI / 2];
-  auto read_stage = [&](int st, Frags &f) {
-    const bf16_t *as = lds + (st & (kStages - 1)) * kStageElems;
-    const bf16_t *bs = as + BM * BK;
-#pragma unroll
-    for (int jj = 0; jj < NJ; ++jj)
-      f.w[jj] = *reinterpret_cast<const bf16x8 *>(bs + b_rd + jj * 16 * BK);
-#pragma unroll
-    for (int ii = 0; ii < MI / 2; ++ii)
-      alo[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + ii * 16 * BK);
-#pragma unroll
-    for (int ii = 0; ii < MI / 2; ++ii)
-      f.ahi[ii] = *reinterpret_cast<const bf16x8 *>(as + a_rd + (MI / 2 + ii) * 16 * BK);
-  };
-  read_stage(0, fa);
-
-  // One K-step: MFMAs of stage kt (fragments in cur) in two halves around
-  // the barrier that hands stage kt's slot to stage kt + 4 (issued here
-  // when kDma).  All of stage kt+1's fragments are read right after the
-  // barrier, into nxt and alo, so they land during the second half.
-  auto step = [&](int kt, auto dma_c, auto last_c, Frags &cur, Frags &nxt) {
-    constexpr bool kDma = decltype(dma_c)::value;    // issue stage kt + 4
-    constexpr bool kLast = decltype(last_c)::value;  // kt == KT - 1
-#pragma unroll
-    for (int i = 0; i < MI / 2; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(cur.w[j], alo[i], acc[i][j]);
-
-    if constexpr (!kLast) {
-      // Stage kt+1 must have landed; stages kt+2 and kt+3 (if any) may stay in flight.
-      const int ahead = min(2, KT - 2 - kt);
-      if (ahead == 2)
-        wait_vmcnt(2 * kInstPerStage);
-      else if (ahead == 1)
-        wait_vmcnt(kInstPerStage);
-      else
-        wait_vmcnt(0);
-      lds_barrier();
-      // Every wave has read stage kt (in the previous step), so its slot
-      // takes stage kt + 4.
-      if constexpr (kDma) issue_stage(kt + 4);
-      read_stage(kt + 1, nxt);
-      // Keep these reads ahead of the second half's MFMAs (the scheduler
-      // would otherwise sink them next to their use in the next step).
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int i = 0; i < MI / 2; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        acc[MI / 2 + i][j] = mfma_bf16(cur.w[j], cur.ahi[i], acc[MI / 2 + i][j]);
-  };
-
-  // Steps that refill the ring (in pairs, the fragment sets swapping
-  // roles), then the ones without loads, then the last step (no next
-  // stage).  An odd leftover step moves its next set into fa once.
-  int kt = 0;
-  for (; kt + 5 < KT; kt += 2) {
-    step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
-    step(kt + 1, bool_c<true>{}, bool_c<false>{}, fb, fa);
-  }
-  if (kt + 4 < KT) {
-    step(kt, bool_c<true>{}, bool_c<false>{}, fa, fb);
-    fa = fb;
-    ++kt;
-  }
-  for (; kt + 2 < KT; kt += 2) {
-    step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
-    step(kt + 1, bool_c<false>{}, bool_c<false>{}, fb, fa);
-  }
-  if (kt + 1 < KT) {
-    step(kt, bool_c<false>{}, bool_c<false>{}, fa, fb);
-    fa = fb;
-    ++kt;
-  }
-  step(kt, bool_c<false>{}, bool_c<true>{}, fa, fb);
-
-#endif
 
   // Epilogue: acc[i][j][r] = C[row m0 + wm*WM + 16i + (lane & 15)]
   //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
@@ -632,11 +587,11 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
   static_assert(!kSplit || (CfT::BM == Cf::BM && 2 * CfT::BN == Cf::BN && !GATEUP),
                 "tail tiles are the two column halves of a down / dense tile");
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  __shared__ TileMap tm;
-  build_tile_map(tm, offsets, G, Cf::BM, dense_m);
+  WaveTileMap tm;
+  build_wave_tile_map(tm, offsets, G, Cf::BM, dense_m);
 
   const int n_tiles = Np / Cf::BN;
-  const int m_tiles = tm.prefix[G];
+  const int m_tiles = tm.m_tiles;
   const int total = m_tiles * n_tiles;
   const int nblk = gridDim.x;
   int n_full = total, n_items = total;  // tiles computed whole; work items
@@ -651,14 +606,14 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     int mt, nt;
     if (t < n_full) {
       tile_coords(t, m_tiles, n_tiles, mt, nt);
-      bf16_tile<Cf, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm, G,
+      bf16_tile<Cf, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
                             stage_c, P, lds, mt, nt);
     } else if constexpr (kSplit) {
       // Items 2u, 2u + 1 are the halves of tail tile n_full + u (consecutive
       // items run on one XCD, so both halves share the A panel in its L2).
       const int u = t - n_full;
       tile_coords(n_full + u / 2, m_tiles, n_tiles, mt, nt);
-      bf16_tile<CfT, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm, G,
+      bf16_tile<CfT, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
                              stage_c, P, lds, mt, 2 * nt + (u & 1));
     }
   }
@@ -1102,7 +1057,7 @@ int gemm_cu_limit(int cus) {
 template <class Cf, bool GATEUP>
 using TailCfg = typename std::conditional<
     GATEUP || (Cf::BN / 2) % (Cf::kRowsPerInst * Cf::kWaves) != 0, Cf,
-    Bf16Cfg<Cf::BM, Cf::BN / 2, Cf::WGM, Cf::WGN>>::type;
+    Bf16Cfg<Cf::BM, Cf::BN / 2, Cf::WGM, Cf::WGN, Cf::kStages>>::type;
 
 // Persistent grid of a bf16 launch: one workgroup per CU (the LDS ring allows
 // one), fewer when the launch has fewer tiles (twice the tiles when the last
