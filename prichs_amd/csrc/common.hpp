@@ -171,12 +171,24 @@ int checkpoint_moe_weights(const prichs_checkpoint *ck, size_t layer, size_t d, 
 
 // prichs_router_topk then prichs_permute; when one router workgroup covers
 // the batch (decode-sized T) the router writes the permutation itself
-// (router.hip).  Same outputs either way.
+// (router.hip).  Same outputs either way.  w_lds (may be null): the router
+// weights in the router's LDS layout, W^T [E][d + 4] f32 with zero padding
+// (router_lds_layout), which spares each router workgroup the transpose.
 int router_topk_permute(const void *x, int x_dtype, const float *w_router,
                         const float *router_bias, const float *concept_bias, size_t n_concept,
                         size_t T, size_t d, size_t E, size_t k, float *logits, int32_t *topk_idx,
                         float *topk_w, int32_t *block_counts, int32_t *offsets,
-                        int32_t *row_token, float *row_weight, int32_t *token_row, void *stream);
+                        int32_t *row_token, float *row_weight, int32_t *token_row, void *stream,
+                        const float *w_lds = nullptr);
+// prichs_router_topk with the W^T copy above (may be null).
+int router_topk_lds(const void *x, int x_dtype, const float *w_router, const float *w_lds,
+                    const float *router_bias, const float *concept_bias, size_t n_concept,
+                    size_t T, size_t d, size_t E, size_t k, float *logits, int32_t *topk_idx,
+                    float *topk_w, int32_t *block_counts, void *stream);
+// Elements of that copy (0 when the router kernel that reads it does not
+// apply to the shape), and the copy of host weights W [d][E] into host memory.
+size_t router_lds_layout_elems(size_t d, size_t E);
+void router_lds_layout(const float *w_router, size_t d, size_t E, float *out);
 
 // moe_out = the MoE combine (bf16) and out = res + moe_out (the block's final
 // residual add) in one kernel (elementwise.hip).

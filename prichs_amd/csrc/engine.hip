@@ -32,6 +32,7 @@ struct prichs_moe_engine {
 
   void *arena = nullptr;  // one allocation for weights + workspace
   float *w_router = nullptr;
+  float *w_router_lds = nullptr;  // W^T [E][d + 4] for the router kernel's LDS (may be null)
   float *router_bias = nullptr;
   void *w_gate_up = nullptr;
   void *w_down = nullptr;
@@ -151,6 +152,8 @@ extern "C" int prichs_moe_engine_create(size_t d, size_t f, size_t E, size_t k, 
 
   Carve c;
   const size_t o_router = c.take(sizeof(float) * d * E);
+  const size_t n_rlds = router_lds_layout_elems(d, E);
+  const size_t o_rlds = c.take(sizeof(float) * (n_rlds > 0 ? n_rlds : 1));
   const size_t o_bias = c.take(sizeof(float) * E);
   const size_t o_gu = c.take(es * gu * G);
   const size_t o_dn = c.take(es * dn * G);
@@ -182,6 +185,7 @@ extern "C" int prichs_moe_engine_create(size_t d, size_t f, size_t E, size_t k, 
   }
   char *base = static_cast<char *>(eng->arena);
   eng->w_router = reinterpret_cast<float *>(base + o_router);
+  eng->w_router_lds = n_rlds > 0 ? reinterpret_cast<float *>(base + o_rlds) : nullptr;
   eng->router_bias = reinterpret_cast<float *>(base + o_bias);
   eng->w_gate_up = base + o_gu;
   eng->w_down = base + o_dn;
@@ -272,6 +276,13 @@ extern "C" int prichs_moe_engine_upload(prichs_moe_engine *eng, const float *w_r
   PRICHS_HIP_TRY(hipMemcpy(eng->w_router, w_router, sizeof(float) * eng->d * eng->E,
                            hipMemcpyHostToDevice),
                  "engine_upload: router");
+  if (eng->w_router_lds != nullptr) {
+    std::vector<float> wl(router_lds_layout_elems(eng->d, eng->E));
+    router_lds_layout(w_router, eng->d, eng->E, wl.data());
+    PRICHS_HIP_TRY(hipMemcpy(eng->w_router_lds, wl.data(), sizeof(float) * wl.size(),
+                             hipMemcpyHostToDevice),
+                   "engine_upload: router (router layout)");
+  }
   PRICHS_HIP_TRY(hipMemcpy(eng->router_bias, bias.data(), sizeof(float) * eng->E,
                            hipMemcpyHostToDevice),
                  "engine_upload: router bias");
@@ -406,13 +417,13 @@ static int moe_forward_impl(prichs_moe_engine *eng, const void *x, size_t T,
     rc = router_topk_permute(x, eng->dtype, eng->w_router, eng->router_bias, concept_bias,
                              n_concept, T, eng->d, eng->E, eng->k, eng->logits, eng->topk_idx,
                              eng->topk_w, eng->block_counts, eng->offsets, eng->row_token,
-                             eng->row_weight, eng->token_row, stream);
+                             eng->row_weight, eng->token_row, stream, eng->w_router_lds);
     if (rc) return rc;
     if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[1], s), "engine_forward: event");
   } else {
-    rc = prichs_router_topk(x, eng->dtype, eng->w_router, eng->router_bias, concept_bias,
-                            n_concept, T, eng->d, eng->E, eng->k, eng->logits, eng->topk_idx,
-                            eng->topk_w, eng->block_counts, stream);
+    rc = router_topk_lds(x, eng->dtype, eng->w_router, eng->w_router_lds, eng->router_bias,
+                         concept_bias, n_concept, T, eng->d, eng->E, eng->k, eng->logits,
+                         eng->topk_idx, eng->topk_w, eng->block_counts, stream);
     if (rc) return rc;
     if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[1], s), "engine_forward: event");
     rc = prichs_permute(eng->topk_idx, eng->topk_w, eng->block_counts, T, eng->E, eng->k,

@@ -478,7 +478,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
     const XT *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     const float *__restrict__ concept, int n_concept, int T, int d, int E, int k,
     float *__restrict__ logits, int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
-    int32_t *__restrict__ block_counts, FusedPerm perm) {
+    int32_t *__restrict__ block_counts, FusedPerm perm, const float *__restrict__ w_lds) {
 #pragma clang fp contract(off)
   using Cf = QuadRouter<XT>;
   constexpr int kTpb = kRouterThreads / 8;
@@ -504,10 +504,27 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
 #pragma unroll
   for (int j = 0; j < Cf::kRing; ++j) fetch(j, ring[j]);
 
-  // W [d][E] (row-major, the reference layout) -> W^T [e][k] in LDS, in
-  // batches of 8 float4 loads per thread issued before their stores (d * E
-  // is a multiple of 4 since d % 128 == 0).
-  {
+  if (w_lds != nullptr) {
+    // W^T already in the LDS layout [E][d + 4] (the engine keeps one): a
+    // straight copy, 8 float4 loads per thread in flight before their stores
+    // (E (d + 4) is a multiple of 4 since d % 128 == 0).
+    const int n4 = E * ws / 4;
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(w_lds);
+    f32x4 *dst = reinterpret_cast<f32x4 *>(wt_s);
+    for (int base = 0; base < n4; base += 8 * kRouterThreads) {
+      f32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = src[min(base + u * kRouterThreads + tid, n4 - 1)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * kRouterThreads + tid;
+        if (i < n4) dst[i] = v[u];
+      }
+    }
+  } else {
+    // W [d][E] (row-major, the reference layout) -> W^T [e][k] in LDS, in
+    // batches of 8 float4 loads per thread issued before their stores (d * E
+    // is a multiple of 4 since d % 128 == 0).
     const int n4 = d * E / 4;
     const f32x4 *w4 = reinterpret_cast<const f32x4 *>(w);
     for (int base = 0; base < n4; base += 8 * kRouterThreads) {
@@ -628,7 +645,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_quad_kernel(
 template <typename XT>
 int launch_quad_t(const XT *x, const float *w, const float *bias, const float *concept, int nc,
                   int T, int d, int E, int k, float *logits, int32_t *idx, float *wt, int32_t *bc,
-                  int nb, hipStream_t s, FusedPerm perm = FusedPerm{nullptr, nullptr, nullptr, nullptr}) {
+                  int nb, hipStream_t s, FusedPerm perm = FusedPerm{nullptr, nullptr, nullptr, nullptr},
+                  const float *w_lds = nullptr) {
   const size_t lds = (size_t)8 * (d + 4) * sizeof(float);
   static int attr_bytes = 0;
   if ((int)lds > attr_bytes) {
@@ -638,7 +656,7 @@ int launch_quad_t(const XT *x, const float *w, const float *bias, const float *c
     attr_bytes = (int)lds;
   }
   hipLaunchKernelGGL((router_topk_quad_kernel<XT>), dim3(nb), dim3(kRouterThreads), lds, s, x, w,
-                     bias, concept, nc, T, d, E, k, logits, idx, wt, bc, perm);
+                     bias, concept, nc, T, d, E, k, logits, idx, wt, bc, perm, w_lds);
   return PRICHS_OK;
 }
 
@@ -841,12 +859,14 @@ extern "C" size_t prichs_router_num_blocks(size_t T, size_t E) {
 }
 
 // The router; with perm.offsets set and a batch one workgroup covers, the
-// quad kernel also writes the permutation (*fused = true).
+// quad kernel also writes the permutation (*fused = true).  w_lds (may be
+// null): the router weights already in the quad kernel's LDS layout, W^T
+// [E][d + 4] with zero padding.
 static int router_topk_impl(const void *x, int x_dtype, const float *w_router,
                             const float *router_bias, const float *concept_bias, size_t n_concept,
                             size_t T, size_t d, size_t E, size_t k, float *logits,
                             int32_t *topk_idx, float *topk_w, int32_t *block_counts, void *stream,
-                            FusedPerm perm, bool *fused) {
+                            FusedPerm perm, bool *fused, const float *w_lds = nullptr) {
   *fused = false;
   PRICHS_REQUIRE(dtype_ok(x_dtype), "router: bad x dtype %d", x_dtype);
   PRICHS_REQUIRE(E >= 1 && E <= PRICHS_MAX_EXPERTS, "router: E=%zu outside [1, %d]", E,
@@ -877,10 +897,10 @@ static int router_topk_impl(const void *x, int x_dtype, const float *w_router,
     int rc = x_dtype == PRICHS_DTYPE_BF16
                  ? launch_quad_t<bf16_t>(static_cast<const bf16_t *>(x), w_router, router_bias,
                                          concept_bias, nc, (int)T, (int)d, (int)E, (int)k, logits,
-                                         topk_idx, topk_w, block_counts, nb, s, perm)
+                                         topk_idx, topk_w, block_counts, nb, s, perm, w_lds)
                  : launch_quad_t<float>(static_cast<const float *>(x), w_router, router_bias,
                                         concept_bias, nc, (int)T, (int)d, (int)E, (int)k, logits,
-                                        topk_idx, topk_w, block_counts, nb, s, perm);
+                                        topk_idx, topk_w, block_counts, nb, s, perm, w_lds);
     if (rc) return rc;
     *fused = perm.offsets != nullptr;
   } else if (staged) {
@@ -922,19 +942,43 @@ extern "C" int prichs_router_topk(const void *x, int x_dtype, const float *w_rou
 }
 
 namespace prichs {
+size_t router_lds_layout_elems(size_t d, size_t E) {
+  // The quad kernel's shapes (eight lanes per token, whole 128-wide chunks).
+  if (lanes_per_token_log2((int)E) != 3 || d % 128 != 0 || (size_t)8 * (d + 4) * 4 > 150 * 1024)
+    return 0;
+  return E * (d + 4);
+}
+
+void router_lds_layout(const float *w_router, size_t d, size_t E, float *out) {
+  for (size_t e = 0; e < E; ++e) {
+    for (size_t c = 0; c < d; ++c) out[e * (d + 4) + c] = w_router[c * E + e];
+    for (size_t c = d; c < d + 4; ++c) out[e * (d + 4) + c] = 0.0f;
+  }
+}
+
+int router_topk_lds(const void *x, int x_dtype, const float *w_router, const float *w_lds,
+                    const float *router_bias, const float *concept_bias, size_t n_concept,
+                    size_t T, size_t d, size_t E, size_t k, float *logits, int32_t *topk_idx,
+                    float *topk_w, int32_t *block_counts, void *stream) {
+  bool fused;
+  return router_topk_impl(x, x_dtype, w_router, router_bias, concept_bias, n_concept, T, d, E, k,
+                          logits, topk_idx, topk_w, block_counts, stream,
+                          FusedPerm{nullptr, nullptr, nullptr, nullptr}, &fused, w_lds);
+}
+
 int router_topk_permute(const void *x, int x_dtype, const float *w_router,
                         const float *router_bias, const float *concept_bias, size_t n_concept,
                         size_t T, size_t d, size_t E, size_t k, float *logits, int32_t *topk_idx,
                         float *topk_w, int32_t *block_counts, int32_t *offsets,
                         int32_t *row_token, float *row_weight, int32_t *token_row,
-                        void *stream) {
+                        void *stream, const float *w_lds) {
   bool fused = false;
   if (T > 0) {
     PRICHS_REQUIRE(offsets && row_token && row_weight && token_row,
                    "router_permute: null permutation output");
     int rc = router_topk_impl(x, x_dtype, w_router, router_bias, concept_bias, n_concept, T, d, E,
                               k, logits, topk_idx, topk_w, block_counts, stream,
-                              FusedPerm{offsets, row_token, row_weight, token_row}, &fused);
+                              FusedPerm{offsets, row_token, row_weight, token_row}, &fused, w_lds);
     if (rc) return rc;
   }
   if (fused) return PRICHS_OK;
