@@ -511,42 +511,63 @@ __device__ __forceinline__ void bf16_tile(
     // blocks: in block q, gate column c (16-column piece jj) pairs with up
     // column c, kIl / 16 pieces on.
     constexpr int kPieces = Cf::kIl / 16;  // 16-column pieces per gate (or up) half
+    static_assert(kPieces == 2 && NJ % 2 == 0, "pairs of 16-column pieces");
+    // Each lane holds 4 consecutive values of one row in each 16-column
+    // piece.  Lanes l and l + 16 (16-lane rows 2r, 2r + 1) hold columns
+    // cq .. cq + 3 and cq + 4 .. cq + 7 of the same row, so for a pair of
+    // pieces one v_permlane16_swap per dword hands the even row both halves
+    // of the first piece and the odd row both halves of the second: with
+    // stage_c (16-byte aligned outputs) every lane writes 8 consecutive
+    // columns with one 16-byte store (a wave store covers 16 rows x 64 bytes
+    // instead of 16 rows x 32 bytes); otherwise 8-byte stores of its own 4.
+    const bool odd = (lane >> 4) & 1;
+    auto store_pair = [&](bf16_t *row_ptr, int col0, u32x2 v0, u32x2 v1, bool ok0, bool ok1) {
+      // col0: the pair's first column for this lane's cq (piece 1 is 16 on).
+      if (stage_c) {
+        const auto sx = __builtin_amdgcn_permlane16_swap(v0[0], v1[0], false, false);
+        const auto sy = __builtin_amdgcn_permlane16_swap(v0[1], v1[1], false, false);
+        if (odd ? ok1 : ok0)
+          *reinterpret_cast<u32x4 *>(row_ptr + col0 + (odd ? 12 : 0)) =
+              u32x4{sx[0], sy[0], sx[1], sy[1]};
+      } else {
+        if (ok0) *reinterpret_cast<u32x2 *>(row_ptr + col0) = v0;
+        if (ok1) *reinterpret_cast<u32x2 *>(row_ptr + col0 + 16) = v1;
+      }
+    };
     if (P != nullptr) {
       // Training forward: the gate/up pre-activations too, [rows][Np] in
       // packed column order (the backward's SwiGLU derivative needs them).
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = lr + 16 * i;
-        if (m < mg) {
-          bf16_t *prow = P + (long long)(row0 + m) * Np + n0 + wn * WN + cq;
+        bf16_t *prow = P + (long long)(row0 + m) * Np;
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const f32x4 a = acc[i][j];
-            *reinterpret_cast<u32x2 *>(prow + 16 * j) =
-                u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-          }
+        for (int jp = 0; jp < NJ; jp += 2) {
+          const f32x4 a = acc[i][jp], b = acc[i][jp + 1];
+          store_pair(prow, n0 + wn * WN + 16 * jp + cq,
+                     u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])},
+                     u32x2{pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])}, m < mg, m < mg);
         }
       }
     }
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int m = lr + 16 * i;
-      if (m < mg) {
-        bf16_t *crow = C + (long long)(row0 + m) * ldc;
+      bf16_t *crow = C + (long long)(row0 + m) * ldc;
 #pragma unroll
-        for (int jg = 0; jg < NJ / 2; ++jg) {
-          const int q = jg / kPieces, jj = jg - q * kPieces;
+      for (int q = 0; q < NJ / (2 * kPieces); ++q) {
+        u32x2 v[kPieces];
+#pragma unroll
+        for (int jj = 0; jj < kPieces; ++jj) {
           const int j = 2 * kPieces * q + jj;  // gate piece; up piece is j + kPieces
-          const int col = (n0 + wn * WN + 2 * Cf::kIl * q) / 2 + 16 * jj + cq;
-          if (col < n_store) {
-            float h[4];
+          float h[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + kPieces][r];
-            *reinterpret_cast<u32x2 *>(crow + col) =
-                u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-          }
+          for (int r = 0; r < 4; ++r)
+            h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + kPieces][r];
+          v[jj] = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
         }
+        const int col0 = (n0 + wn * WN + 2 * Cf::kIl * q) / 2 + cq;
+        store_pair(crow, col0, v[0], v[1], m < mg && col0 < n_store, m < mg && col0 + 16 < n_store);
       }
     }
   } else {
@@ -1083,11 +1104,13 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
                    "grouped gemm: set LDS size");
     attr_set = true;
   }
-  // Staged 16-byte epilogue stores need C 16-byte aligned and whole 8-column
-  // chunks; otherwise each lane stores its 8-byte pieces directly.
-  const int stage_c = !GATEUP && PRICHS_GEMM_STAGE_C &&
+  // 16-byte epilogue stores (down / dense: rows staged in LDS; gate/up:
+  // lane pairs' halves exchanged) need C (and the pre-activations) 16-byte
+  // aligned and whole 8-column chunks; otherwise each lane stores its 8-byte
+  // pieces directly.
+  const int stage_c = (GATEUP || PRICHS_GEMM_STAGE_C) &&
                       reinterpret_cast<uintptr_t>(Cp) % 16 == 0 && ldc % 8 == 0 &&
-                      n_store % 8 == 0;
+                      n_store % 8 == 0 && reinterpret_cast<uintptr_t>(pre) % 16 == 0;
   static_assert(CfT::kLdsBytes <= Cf::kLdsBytes, "tail tiles fit the launch's LDS");
   hipLaunchKernelGGL((bf16_gemm_kernel<Cf, CfT, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
