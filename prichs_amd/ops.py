@@ -138,10 +138,12 @@ def to_device_packed(packed: list, dtype, device="cuda") -> torch.Tensor:
 
 
 # ------------------------------------------------------------------- GEMMs --
-def grouped_gate_up_swiglu(x, row_token, offsets, G, rows, w_packed, d, f, stream=None):
-    """prichs_grouped_gate_up_swiglu -> act [rows, f] (rows = offsets[G])."""
+def grouped_gate_up_swiglu(x, row_token, offsets, G, rows, w_packed, d, f, stream=None,
+                           out=None):
+    """prichs_grouped_gate_up_swiglu -> act [rows, f] (rows = offsets[G]); out: a
+    contiguous [rows, f] tensor to write (any element alignment)."""
     lib = L.load()
-    act = torch.empty((rows, f), dtype=x.dtype, device=x.device)
+    act = torch.empty((rows, f), dtype=x.dtype, device=x.device) if out is None else _dev(out)
     L.check(lib.prichs_grouped_gate_up_swiglu(_p(_dev(x)), _p(row_token), _p(offsets), G, rows,
                                               _p(w_packed), d, f, dtype_code(x), _p(act),
                                               _stream(stream)))

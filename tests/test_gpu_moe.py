@@ -173,6 +173,24 @@ def test_grouped_gemms_against_oracle(cuda, orc, cfg):
         assert rel_err(h_y[sel], y_ref) <= tol, ("y", g)
 
 
+# The tiled gate/up kernel writes 16 bytes per lane when the activations are
+# 16-byte aligned and 8 bytes otherwise: an output 8 bytes off alignment must
+# get the same bits (groups over 64 rows, so not the skinny kernel).
+def test_gate_up_unaligned_output_bit_identical(cuda):
+    inp = synth.make_moe_inputs(512, 256, 192, E=8, k=2, dtype="bf16", seed=3)
+    x, idx, w, off, rt, tr, gu, dn, order = _stage_inputs(inp)
+    G, rows = inp.E + inp.n_shared, inp.T * inp.k + inp.T
+    assert int(np.diff(host(off)[: G + 1]).max()) > 64
+    say("gate/up unaligned output", rows)
+    act = ops.grouped_gate_up_swiglu(x, rt, off, G, rows, gu, inp.d, inp.f)
+    flat = torch.zeros(rows * inp.f + 4, dtype=torch.bfloat16, device="cuda")
+    view = flat[4:].view(rows, inp.f)  # data 8 bytes past a 16-byte boundary
+    assert view.data_ptr() % 16 == 8
+    ops.grouped_gate_up_swiglu(x, rt, off, G, rows, gu, inp.d, inp.f, out=view)
+    assert torch.equal(act.view(torch.int16), view.view(torch.int16))
+    assert int(flat[:4].view(torch.int16).abs().sum()) == 0  # nothing written before it
+
+
 # Decode-sized groups (every group <= 64 rows) take the skinny weight-streaming
 # kernel: empty groups, one 16-row MFMA tile, two tiles, two 32-row M-tiles;
 # K with 8, 4 and 2 K-steps per chunk (K % 256, % 128, % 64).
