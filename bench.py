@@ -363,7 +363,7 @@ def main():
     def gbps(b, stage, m=ms):
         return b / (m[stage] / 1e3) / 1e9 if m[stage] > 0 else None
 
-    kernel = "grouped gate/up GEMM + fused SwiGLU (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, Bf16Cfg<256,256,2,4>, true>)"
+    kernel = "grouped gate/up GEMM + fused SwiGLU (bf16_gemm_kernel<Bf16Cfg<256,256,4,2>, Bf16Cfg<256,256,4,2>, true>)"
     if T * k < 64 * E:  # fewer than 64 rows per routed expert on average
         # Decode shape: every touched expert's gate/up weights are streamed once
         # for a handful of rows, so the launch is bound by HBM, not MFMA.
@@ -548,9 +548,9 @@ def bench_backward(args):
     }
     kernels = {
         "dw_down": "grouped weight gradient dW_down += act^T dY (wgrad_bf16_kernel<false>)",
-        "d_act": "grouped GEMM dA = dY Wd^T (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, Bf16Cfg<256,128,2,4>, false>)",
+        "d_act": "grouped GEMM dA = dY Wd^T (bf16_gemm_kernel<Bf16Cfg<256,256,4,2>, Bf16Cfg<256,128,4,2>, false>)",
         "dw_gate_up": "grouped weight gradient dW_gate/up += x^T [dG dU] (wgrad_bf16_kernel<true>)",
-        "d_x_gemm": "grouped GEMM dX = [dG dU] [Wg Wu]^T (bf16_gemm_kernel<Bf16Cfg<256,256,2,4>, Bf16Cfg<256,128,2,4>, false>)",
+        "d_x_gemm": "grouped GEMM dX = [dG dU] [Wg Wu]^T (bf16_gemm_kernel<Bf16Cfg<256,256,4,2>, Bf16Cfg<256,128,4,2>, false>)",
     }
     per = {kk: {"ms": bms[kk], "tflops": fl / (bms[kk] / 1e3) / 1e12}
            for kk, fl in gemm_flops.items()}

@@ -53,12 +53,16 @@ constexpr int kBf16KMultiple = 64;   // bf16 kernels need d and f to be multiple
 #ifndef PRICHS_BF16_SILU
 #define PRICHS_BF16_SILU silu_fast
 #endif
-// Wave grid of the bf16 kernel (WGM x WGN wave64s per 256x256 tile).
+// Wave grids of the bf16 kernel (WGM x WGN wave64s per tile): 256 x 256
+// tiles as 4 x 2 waves of 64 x 128 (against 2 x 4 waves of 128 x 64, the same
+// LDS bytes per MFMA: config 2 gate/up 155.6 -> 155.0 us, down 98.6 -> 98.1,
+// and 2.4 / 2.8 us less after an L2/MALL flush); the 128 x 384 tiles keep
+// 2 x 4 waves of 64 x 96.
 #ifndef PRICHS_BF16_WGM
-#define PRICHS_BF16_WGM 2
+#define PRICHS_BF16_WGM 4
 #endif
 #ifndef PRICHS_BF16_WGN
-#define PRICHS_BF16_WGN 4
+#define PRICHS_BF16_WGN 2
 #endif
 // Down / dense epilogue through an LDS copy of the tile with 16-byte row
 // stores (1) or direct 8-byte stores from the accumulators (0).
@@ -280,7 +284,7 @@ static_assert(Bf16::BN % Bf16Down::BN == 0,
 // tile count that can fill the CUs where 256 x 256 tiles leave a round part
 // empty (8192 x 1536 outputs: 256 such tiles against 192).  Each output
 // element is the same MFMA chain over K either way, so the bits are the same.
-using Bf16Wide = Bf16Cfg<128, 384, PRICHS_BF16_WGM, PRICHS_BF16_WGN>;
+using Bf16Wide = Bf16Cfg<128, 384, 2, 4>;
 
 // C[m, n] = sum_k A[row(m), k] * B[n, k] for the rows of each group, with
 // B = packed weights [Np, K] of group g.  The MFMA takes the weight fragment
