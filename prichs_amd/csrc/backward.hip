@@ -397,23 +397,44 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
     for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = (mg + BK - 1) / BK;
-  issue(0);
-  if (KT > 1) issue(1);
-  if (KT > 2) issue(2);
-  // One K-step.  kAhead = this wave's later stages (4 instructions each)
-  // still allowed in flight when stage kt has landed: a compile-time count,
-  // so the wait is one instruction and the steady state carries no branch.
-  auto kstep = [&](int kt, auto ahead_c) {
-    constexpr int kAhead = decltype(ahead_c)::value;
-    PRICHS_WG_VMCNT(4 * kAhead);
-    // Every wave's DMAs of stage kt landed, and every wave is done reading
-    // stage kt - 1, whose slot the next issue refills.
+  // Ping-pong K loop (as the forward GEMM's): waves 0-3 (group 0) and 4-7
+  // (group 1) sit one per SIMD each.  Every wave runs, per K-step kt, a
+  // memory phase (the transposing reads of stage kt, its share of stage
+  // kt + 3, a wait for its share of stage kt + 1 and for its reads), a
+  // barrier, an MFMA phase, a barrier; group 1 runs one barrier behind, so on
+  // each SIMD one wave multiplies while the other reads and loads.
+  //  - Stage s is first read after b(2s-1); both groups waited for their
+  //    shares of it in their memory phases of step s - 1, which end at
+  //    b(2s-2) and b(2s-1).
+  //  - Stage kt + 3 goes to stage kt - 1's slot; both groups' reads of stage
+  //    kt - 1 completed before b(2kt-2) and b(2kt-1), and step kt's memory
+  //    phases start after b(2kt-1) and b(2kt).
+  // Each output element is the same MFMA chain over K, so the results do not
+  // depend on the schedule.
+  const int grp = wave >> 2;
+  auto pp_barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if constexpr (kAhead == 2) {
-      if (kt + 3 < KT) issue(kt + 3);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  issue(0);
+  if (KT > 1) issue(1);
+  if (KT > 2) issue(2);
+  // Own share of stage 0 (4 instructions per stage and wave).
+  if (KT > 2)
+    PRICHS_WG_VMCNT(8);
+  else if (KT > 1)
+    PRICHS_WG_VMCNT(4);
+  else
+    PRICHS_WG_VMCNT(0);
+  pp_barrier();
+  if (grp == 1) pp_barrier();  // group 1 runs one phase behind
+  // One K-step; kAhead = this wave's stages still allowed in flight after the
+  // wait (stages kt + 2 .. min(kt + 3, KT - 1)), a compile-time count.
+  auto kstep = [&](int kt, auto ahead_c) {
+    constexpr int kAhead = decltype(ahead_c)::value;
     const uint32_t st = (uint32_t)(kt & (kStages - 1)) * kStageBytes;
     u32x2 alo[8], ahi[8], bt[8];  // bt: B lo (0..3) and hi (4..7)
 #pragma unroll
@@ -426,9 +447,12 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
       alo[blk] = wg_read_tr<0>(a_rd[blk] + st);
       ahi[blk] = wg_read_tr<(int)kHiOff>(a_rd[blk] + st);
     }
+    if constexpr (kAhead == 2) issue(kt + 3);
+    PRICHS_WG_VMCNT(4 * kAhead);
     wg_wait_tied(bt);
     wg_wait_tied(alo);
     wg_wait_tied(ahi);
+    pp_barrier();
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const bf16x8 bf =
@@ -440,13 +464,15 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
         acc[jb][ib] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, af, acc[jb][ib], 0, 0, 0);
       }
     }
+    pp_barrier();
   };
-  // Steps with two later stages in flight (issuing stage kt + 3 when it
-  // exists), then the last two.
+  // Steps that issue stage kt + 3, then the last (up to three).
   int kt = 0;
-  for (; kt + 2 < KT; ++kt) kstep(kt, std::integral_constant<int, 2>{});
-  if (kt + 1 < KT) kstep(kt++, std::integral_constant<int, 1>{});
+  for (; kt + 3 < KT; ++kt) kstep(kt, std::integral_constant<int, 2>{});
+  if (kt + 2 < KT) kstep(kt++, std::integral_constant<int, 1>{});
+  if (kt + 1 < KT) kstep(kt++, std::integral_constant<int, 0>{});
   if (kt < KT) kstep(kt++, std::integral_constant<int, 0>{});
+  if (grp == 0) pp_barrier();  // both groups leave after the same barrier count
 
   // acc[jb][ib] lane l holds out[i = 16 ib + l % 16][j = 16 jb + 4 (l / 16) + r]
   // of the wave's 128 x 64 block.
