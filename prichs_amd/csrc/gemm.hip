@@ -15,14 +15,15 @@
 //             weight interleave), so SwiGLU is applied in the epilogue.
 //   down:     y[r] = act[r] @ Wd  (moe.rs:170, 106).
 //
-// bf16 kernel: 256x256 output tiles per workgroup on v_mfma_f32_16x16x32_bf16
-// (fp32 accumulation).  K advances 32 at a time through a ring of 4 LDS
-// stages that global_load_lds_dwordx4 fills directly (no staging registers),
-// 3 stages ahead of the MFMAs; each stage's MFMAs are split in two halves
-// around the workgroup barrier so the next stage's fragment reads overlap
-// MFMA work.  Workgroups are persistent and walk an XCD-aware tile order.
-// The down / dense epilogue stages the finished tile in LDS and writes whole
-// rows with 16-byte lanes.
+// bf16 kernel: 256x256 output tiles per workgroup (8 waves of 64x128) on
+// v_mfma_f32_16x16x32_bf16 (fp32 accumulation).  K advances 32 at a time
+// through a ring of 4 LDS stages that global_load_lds_dwordx4 fills directly
+// (no staging registers), 3 stages ahead of the MFMAs; the two halves of the
+// workgroup ping-pong, one wave per SIMD multiplying while the other reads
+// its fragments and issues loads.  Workgroups are persistent and walk an
+// XCD-aware tile order.  The down / dense epilogue stages the finished tile
+// in LDS and writes whole rows with 16-byte lanes; the gate/up epilogue
+// exchanges halves between lane pairs and writes 16 bytes per lane.
 // f32 kernel: 128x128x16 tiles on v_mfma_f32_16x16x4_f32 (the fp32-checked
 // mode; accumulates in fp32 like the reference CPU path).
 #include <algorithm>
@@ -404,8 +405,8 @@ __device__ __forceinline__ void bf16_tile(
   //    stage kt - 1's slot; both groups' LDS reads of stage kt - 1 completed
   //    before b(2kt-2) and b(2kt-1), and step kt's memory phases start after
   //    b(2kt-1) and b(2kt).
-  // Each output element is the same MFMA chain over K as with the in-step
-  // loop, so the results are bit-identical.
+  // Each output element is the same MFMA chain over K whatever the
+  // schedule, so the results are bit-identical.
   const int grp = wave >> 2;
   // Barrier that nothing is scheduled across (MFMAs touch no memory, so the
   // memory clobber alone would let the scheduler move them over it).
