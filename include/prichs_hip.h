@@ -535,8 +535,9 @@ int prichs_block_engine_forward(prichs_block_engine *eng, const void *x,
                                 void *out, int out_dtype, void *stream);
 
 /* Device views of the last forward's intermediates: normed1 bf16 [T, d],
- * qkv bf16 [T, d + 2 * n_kv_heads * head_dim] (q and k after RoPE), attn
- * bf16 [T, d] (concatenated heads), attn_out bf16 [T, d] (after Wo),
+ * qkv bf16 [T, d + 2 * n_kv_heads * head_dim] (k after RoPE; q as projected:
+ * the attention kernel rotates q as it loads it), attn bf16 [T, d]
+ * (concatenated heads), attn_out bf16 [T, d] (after Wo),
  * x1 f32 [T, d], normed2 bf16 [T, d], moe_out bf16 [T, d], and the embedded
  * MoE engine (for prichs_moe_engine_stash).  Valid until the next forward. */
 typedef struct prichs_block_stash {

@@ -136,11 +136,31 @@ constexpr uint32_t kStageBytes = kStageElems * sizeof(bf16_t);
 // q/k/v/o: row r of sequence b is row b*S + r; head h of q/o starts at column
 // h*128, kv head j of k/v at column j*128 (leading dimensions ldq/ldk/ldv/ldo;
 // 64 rows of k or v span less than 4 GiB).
+// RoPE of one Q fragment (8 consecutive head dims 8 c .. 8 c + 7, 4 pairs)
+// with the cos / sin of its pairs: the reference's rotation with each
+// product and each sum rounded (crates/prichs-core/src/backward.rs:175-184),
+// then bf16 -- the same operations and rounding as rope_kernel, so the result
+// is the bf16 value that kernel would have stored.
+__device__ __forceinline__ bf16x8 rope_frag(bf16x8 f, float4 c4, float4 s4) {
+#pragma clang fp contract(off)
+  u32x4 u = __builtin_bit_cast(u32x4, f);
+  const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float q0 = __uint_as_float(u[j] << 16), q1 = __uint_as_float(u[j] & 0xffff0000u);
+    const float a0 = q0 * c[j], b0 = q1 * sn[j];
+    const float a1 = q0 * sn[j], b1 = q1 * c[j];
+    u[j] = pack_bf16(a0 - b0, a1 + b1);
+  }
+  return __builtin_bit_cast(bf16x8, u);
+}
+
 template <int HPW>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const bf16_t *__restrict__ q, int ldq, const bf16_t *__restrict__ k, int ldk,
     const bf16_t *__restrict__ v, int ldv, bf16_t *__restrict__ o, int ldo, int S, int Hq,
-    int group, float scale_log2) {
+    int group, float scale_log2, const float *__restrict__ rcos, const float *__restrict__ rsin,
+    int pos_offset) {
   static_assert(kWaves % HPW == 0, "whole row blocks per head");
   constexpr int kRowsWg = 32 * kWaves / HPW;  // query rows per workgroup
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
@@ -175,6 +195,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
     const bf16_t *qrow = q + (seq0 + qr) * ldq + (size_t)h * kHd + 8 * g;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[nb][kk] = *reinterpret_cast<const bf16x8 *>(qrow + 32 * kk);
+    if (rcos != nullptr) {
+      // q as projected: rotate it here (the fragment's pairs are 16 kk + 4 g ..).
+      const size_t cbase = (size_t)(qr + pos_offset) * (kHd / 2) + 4 * g;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        qf[nb][kk] = rope_frag(qf[nb][kk], *reinterpret_cast<const float4 *>(rcos + cbase + 16 * kk),
+                               *reinterpret_cast<const float4 *>(rsin + cbase + 16 * kk));
+    }
   }
 
   f32x4 oacc[8][2];  // O^T blocks: d block jd, query block nb
@@ -433,11 +461,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(
 
 using namespace prichs;
 
-extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k, size_t ldk,
-                                        const void *v, size_t ldv, void *o, size_t ldo,
-                                        size_t batch, size_t seq_len, size_t n_heads,
-                                        size_t n_kv_heads, size_t head_dim, int dtype,
-                                        void *stream) {
+namespace prichs {
+int attention_forward_impl(const void *q, size_t ldq, const void *k, size_t ldk, const void *v,
+                           size_t ldv, void *o, size_t ldo, size_t batch, size_t seq_len,
+                           size_t n_heads, size_t n_kv_heads, size_t head_dim, int dtype,
+                           const float *rope_cos, const float *rope_sin, size_t cache_rows,
+                           size_t pos_offset, void *stream) {
   PRICHS_REQUIRE(dtype == PRICHS_DTYPE_BF16, "attention: only bf16 is supported (dtype=%d)", dtype);
   if (head_dim != (size_t)kHd)
     return fail(PRICHS_ERR_UNSUPPORTED, "attention: head_dim=%zu (only %d is supported)",
@@ -457,6 +486,10 @@ extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k
   PRICHS_REQUIRE(ldk < ((size_t)1 << 25) && ldv < ((size_t)1 << 25),
                  "attention: ldk / ldv must be below 2^25 elements");
   if (batch == 0 || seq_len == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(rope_cos == nullptr || (rope_sin != nullptr && seq_len + pos_offset <= cache_rows &&
+                                         pos_offset <= (size_t)INT32_MAX),
+                 "attention: rope cache of %zu rows does not cover positions %zu + %zu",
+                 cache_rows, pos_offset, seq_len);
   PRICHS_REQUIRE(q && k && v && o, "attention: null pointer argument");
   const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
@@ -474,9 +507,19 @@ extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k
                      static_cast<const bf16_t *>(q), (int)ldq, static_cast<const bf16_t *>(k),
                      (int)ldk, static_cast<const bf16_t *>(v), (int)ldv,
                      static_cast<bf16_t *>(o), (int)ldo, (int)seq_len, (int)n_heads, group,
-                     scale_log2);
+                     scale_log2, rope_cos, rope_sin, (int)pos_offset);
   PRICHS_LAUNCH_CHECK("attention launch");
   return PRICHS_OK;
+}
+}  // namespace prichs
+
+extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k, size_t ldk,
+                                        const void *v, size_t ldv, void *o, size_t ldo,
+                                        size_t batch, size_t seq_len, size_t n_heads,
+                                        size_t n_kv_heads, size_t head_dim, int dtype,
+                                        void *stream) {
+  return attention_forward_impl(q, ldq, k, ldk, v, ldv, o, ldo, batch, seq_len, n_heads,
+                                n_kv_heads, head_dim, dtype, nullptr, nullptr, 0, 0, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -5,8 +5,8 @@
 // independent sequences of seq_len rows:
 //   n1 = rms_norm(x, input_norm)                    prichs_rmsnorm_forward
 //   qkv = n1 [Wq | Wk | Wv]                         prichs_gemm (one fused GEMM)
-//   RoPE on the q and k columns of qkv in place     prichs_rope_forward_ld (one launch)
-//   attn = causal GQA attention(q, k, v)            prichs_attention_forward
+//   RoPE on the k columns of qkv in place           prichs_rope_forward_ld (one launch)
+//   attn = causal GQA attention(RoPE(q), k, v)      attention kernel, rotating q on load
 //   x1 = x + attn Wo                                prichs_gemm, then one kernel for the
 //   n2 = rms_norm(x1, post_attn_norm)               residual add (x1 in f32) and the norm
 //   out = x1 + MoE(n2)                              the MoE engine forward, whose combine
@@ -258,13 +258,14 @@ extern "C" int prichs_block_engine_forward(prichs_block_engine *eng, const void 
                                    stream)))
     return rc;
   if ((rc = prichs_gemm(eng->n1, d, T, d, eng->w_qkv, n, qkv, n, bf, stream))) return rc;
-  // The k heads follow the q heads in each qkv row and rotate alike, so one
-  // launch over Hq + Hkv heads covers both.
-  if ((rc = prichs_rope_forward_ld(qkv, n, bf, eng->rope_cos, eng->rope_sin, eng->cache_rows, batch,
-                                   seq_len, eng->Hq + eng->Hkv, eng->hd, pos_offset, 1, stream)))
+  // RoPE: the k heads in place (one launch), q inside the attention kernel
+  // as it loads its fragments (same bf16 values, one pass over q saved).
+  if ((rc = prichs_rope_forward_ld(qkv + d, n, bf, eng->rope_cos, eng->rope_sin, eng->cache_rows,
+                                   batch, seq_len, eng->Hkv, eng->hd, pos_offset, 1, stream)))
     return rc;
-  if ((rc = prichs_attention_forward(qkv, n, qkv + d, n, qkv + d + kvw, n, eng->attn, d, batch,
-                                     seq_len, eng->Hq, eng->Hkv, eng->hd, bf, stream)))
+  if ((rc = attention_forward_impl(qkv, n, qkv + d, n, qkv + d + kvw, n, eng->attn, d, batch,
+                                   seq_len, eng->Hq, eng->Hkv, eng->hd, bf, eng->rope_cos,
+                                   eng->rope_sin, eng->cache_rows, pos_offset, stream)))
     return rc;
   if ((rc = prichs_gemm(eng->attn, d, T, d, eng->w_o, d, eng->attn_out, d, bf, stream))) return rc;
   if ((rc = add_rmsnorm_forward(x, bf, eng->attn_out, bf, eng->x1, eng->post_norm, eng->n2, T, d,

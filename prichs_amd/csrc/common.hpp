@@ -169,6 +169,16 @@ struct CheckpointMoe {
 int checkpoint_moe_weights(const prichs_checkpoint *ck, size_t layer, size_t d, size_t f,
                            size_t E, CheckpointMoe &w);
 
+// prichs_attention_forward, with q rotated by RoPE as the kernel loads it
+// when rope_cos is set (the cos / sin tables of prichs_rope_cache, cache_rows
+// positions of head_dim / 2 pairs; positions pos_offset .. pos_offset +
+// seq_len - 1): the attention of the q that prichs_rope_forward would leave.
+int attention_forward_impl(const void *q, size_t ldq, const void *k, size_t ldk, const void *v,
+                           size_t ldv, void *o, size_t ldo, size_t batch, size_t seq_len,
+                           size_t n_heads, size_t n_kv_heads, size_t head_dim, int dtype,
+                           const float *rope_cos, const float *rope_sin, size_t cache_rows,
+                           size_t pos_offset, void *stream);
+
 // prichs_router_topk then prichs_permute; when one router workgroup covers
 // the batch (decode-sized T) the router writes the permutation itself
 // (router.hip).  Same outputs either way.  w_lds (may be null): the router

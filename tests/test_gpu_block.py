@@ -242,6 +242,28 @@ def test_block_small(cuda, orc):
     _check_block(orc, inp)
 
 
+@pytest.mark.parametrize("pos_offset", [0, 37])
+def test_block_rotates_q_in_attention_bit_exact(cuda, pos_offset):
+    # The block rotates k with the RoPE kernel and q inside the attention
+    # kernel as it loads it: its attention output equals that of q rotated by
+    # the RoPE kernel first, bit for bit (also with a position offset).
+    inp = synth.make_block_inputs(batch=2, seq_len=192, name="block-2x192")
+    blk = block.PrichsBlock.from_inputs(inp)
+    B, S, Hq, Hkv, hd = inp.batch, inp.seq_len, inp.n_heads, inp.n_kv_heads, inp.head_dim
+    say("block q rope in attention", pos_offset)
+    blk.engine.forward(dev(inp.x), B, S, pos_offset=pos_offset)
+    st = blk.engine.stash()
+    qkv, d = st["qkv"], Hq * hd
+    q = qkv[:, :d].contiguous().view(B, S, Hq, hd)
+    cos, sin = synth.rope_cache(S + pos_offset, hd, inp.rope_theta)
+    cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    ops.rope_(q, cos_d, sin_d, S + pos_offset, B, S, pos_offset=pos_offset)
+    attn = ops.attention(q.view(B * S, d), qkv[:, d:d + Hkv * hd], qkv[:, d + Hkv * hd:], B, S,
+                         Hq, Hkv)
+    assert torch.equal(attn.view(torch.int16), st["attn"].view(torch.int16))
+    blk.engine.close()
+
+
 @pytest.mark.parametrize("k", [1, 4])
 def test_block_other_top_k(cuda, orc, k):
     # The block's final residual add rides in the combine, whose top-k is a
