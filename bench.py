@@ -13,9 +13,10 @@ forwards; `cpu_baseline` times the CPU oracle (the reference algorithm
 restated in C) on a bounded sample of the same workload on this host.
 
 Order of the GPU passes: W warmup + K timed forwards from idle
-(`value_first_pass`), K forwards with stage events (per-kernel times,
-roofline), K forwards with the caches flushed, copy references, and last
-W warmup + K timed forwards (`value`).  The GPU clock takes tens of
+(`value_first_pass`), about 30 ms of untimed forwards (the clock settles), K
+forwards with stage events (per-kernel times, roofline), K forwards with the
+caches flushed, copy references, and last W warmup + K timed forwards
+(`value`).  The GPU clock takes tens of
 milliseconds of sustained load to settle after idle, so the first pass
 carries the ramp; `value` is the settled rate a serving loop sees.
 """
@@ -84,11 +85,24 @@ def timed_pass(step, steps: int, warmup: int) -> float:
 # idle spell (same box, config 2: the first 30 forwards after 10 warmup ones
 # average 323 us, later ones 288 us), so K = 20 steps right after setup would
 # time the ramp.  Each bench therefore runs W + K steps once from idle
-# ("value_first_pass" in the line), then its diagnostic passes (stage events,
-# cache-flushed passes, the copy references -- all GPU work), then W warmup
-# and the K timed steps that give `value`.
+# ("value_first_pass" in the line), about 30 ms of untimed steps, then its
+# diagnostic passes (stage events, cache-flushed passes, the copy references
+# -- all GPU work), then W warmup and the K timed steps that give `value`.
 TIMING_NOTE = ("value: W warmup then K timed steps after the bench's diagnostic passes (GPU "
                "clock settled); value_first_pass: the same W + K straight after setup")
+
+
+def settle(step, seconds_per_step: float, target_s: float = 0.03) -> int:
+    """Untimed steps for about target_s of GPU work, so that the diagnostic
+    passes that follow (the stage events behind the roofline) run at the
+    settled clock the timed pass sees, not in the ramp after idle."""
+    import torch
+
+    n = int(min(2000, max(10, target_s / max(seconds_per_step, 1e-6))))
+    for _ in range(n):
+        step()
+    torch.cuda.synchronize()
+    return n
 
 
 def device_caps():
@@ -316,6 +330,7 @@ def main():
     # third of a decode-sized forward, so they stay out of `value`.
     log(f"bench: first pass, {args.warmup} warmup + {args.steps} timed steps")
     elapsed_first = timed_pass(fwd, args.steps, args.warmup)
+    n_settle = settle(fwd, elapsed_first / args.steps)
     eng.set_timing(args.steps)
     for _ in range(args.steps):
         eng.forward(x, out=out)
@@ -381,7 +396,8 @@ def main():
                     "algorithmic_bytes_per_launch": gu_bytes, "experts_touched": touched,
                     "avg_launch_ms": ms["gate_up"],
                     "timed_over": "HIP events on the engine's launch stream between the stages, "
-                                  "over a second pass of the same K forwards"}
+                                  f"over a pass of the same K forwards after {n_settle} untimed "
+                                  "settling forwards"}
     else:
         roofline = {
             "kernel": kernel, "bound": "mfma", "achieved": gu_tflops, "peak": peak,
@@ -394,7 +410,7 @@ def main():
             "algorithmic_flops_per_launch": flops_gate_up,
             "avg_launch_ms": ms["gate_up"],
             "timed_over": "HIP events on the engine's launch stream between the stages, over a "
-                          "second pass of the same K forwards",
+                          f"pass of the same K forwards after {n_settle} untimed settling forwards",
         }
 
     res = {
@@ -525,6 +541,7 @@ def bench_backward(args):
     # events for the per-kernel times (as in the forward bench).
     log(f"bench: first pass, {args.warmup} warmup + {args.steps} timed training steps")
     elapsed_first = timed_pass(step, args.steps, args.warmup)
+    n_settle = settle(step, elapsed_first / args.steps)
     eng.set_timing(args.steps)
     for _ in range(args.steps):
         step()
@@ -589,7 +606,9 @@ def bench_backward(args):
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": per[dom]["tflops"] / PEAK_BF16_TFLOPS, "traffic": None,
                      "algorithmic_flops_per_launch": gemm_flops[dom],
-                     "avg_launch_ms": per[dom]["ms"]},
+                     "avg_launch_ms": per[dom]["ms"],
+                     "timed_over": "HIP events on the engine's launch stream between the stages, "
+                                   f"over K training steps after {n_settle} untimed settling steps"},
         "backward_gemms": {"tflops": bwd_gemm_tflops, "frac_of_peak": bwd_gemm_tflops / PEAK_BF16_TFLOPS,
                            "per_stage": per},
         "memory_bound_stages": {
