@@ -293,108 +293,97 @@ __device__ __forceinline__ void wg_wait_tied(u32x2 (&a)[8]) {
 // s_waitcnt with only vmcnt constrained (gfx9 encoding, vmcnt < 16 here).
 #define PRICHS_WG_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8))
 
-template <bool GATEUP>
-__global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
+// One work item: P rows [i0, i0 + BPT) x Q columns [j0, j0 + 256) of group g's
+// dW over the item's rows (BPT = 256: a whole tile; 128: half of one).
+template <bool GATEUP, int BPT>
+__device__ __forceinline__ void wgrad_item(
     const bf16_t *__restrict__ A, int lda, uint32_t a_bytes, const bf16_t *__restrict__ B,
-    int ldb, uint32_t b_bytes, const int32_t *__restrict__ offsets, int G, int E, int P, int Q,
-    int tiles_q, int tiles, float *out0, float *out1, int ldo, long long slot_stride, int f,
-    float *__restrict__ part, int beta) {
+    int ldb, uint32_t b_bytes, int E, int P, int Q, float *out0, float *out1, int ldo,
+    long long slot_stride, int f, float *__restrict__ part, int beta, bf16_t *lds, int g,
+    int row_lo, int mg, int pslot, int i0, int j0) {
   using namespace wgb;
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  // Work item of this block: groups in launch order (shared first), each as
-  // its chunks x tiles.  The offsets come to LDS in one parallel load.
-  __shared__ int item[5];  // group (-1: none), first row, end row, partial slot (-1: none), tile
-  __shared__ int offs_s[PRICHS_MAX_EXPERTS + 2];
-  if ((int)threadIdx.x <= G) offs_s[threadIdx.x] = offsets[threadIdx.x];
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int rest = (int)blockIdx.x, pslot = 0;
-    item[0] = -1;
-    for (int gi = 0; gi < G; ++gi) {
-      const int g = (gi + G - 1) % G;
-      const int lo = offs_s[g], m = offs_s[g + 1] - lo;
-      if (m <= 0) continue;
-      int L, nc;
-      wg_split(m, L, nc);
-      if (rest < nc * tiles) {
-        const int c = rest / tiles;
-        item[0] = g;
-        item[1] = lo + c * L;
-        item[2] = min(lo + (c + 1) * L, lo + m);
-        item[3] = nc == 1 ? -1 : pslot + c;
-        item[4] = rest - c * tiles;
-        break;
-      }
-      rest -= nc * tiles;
-      if (nc > 1) pslot += nc;
-    }
-  }
-  __syncthreads();
-  const int g = item[0];
-  if (g < 0) return;
-  const int row_lo = item[1];
-  const int mg = item[2] - row_lo;
-  const int pslot = item[3];
-  const int tile = item[4];
-  const int tp = tile / tiles_q;
-  const int i0 = tp * BP, j0 = (tile - tp * tiles_q) * BQ;
+  static_assert(BPT == 256 || BPT == 128, "whole or half tiles");
+  // A tile: [BK][BPT] bf16 (rows of kRowA bytes); B tile: [BK][256].
+  constexpr int kRowA = 2 * BPT;
+  constexpr uint32_t kTileA = BK * kRowA;
+  constexpr uint32_t kStage = kTileA + kTileBytes;
+  constexpr uint32_t kHiA = 16 * kRowA;
+  constexpr int kIB = BPT / 2 / 16;           // 16-row A blocks per wave
+  constexpr int kInstA = BPT == 256 ? 2 : 1;  // A DMA instructions per wave and stage
+  constexpr int kInst = kInstA + 2;           // with B's two
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int wp = wave >> 2, wq = wave & 3;
   const __amdgpu_buffer_rsrc_t ra = wg_rsrc(A, a_bytes), rb = wg_rsrc(B, b_bytes);
 
-  // DMA: wave w's instruction i fills tile rows 4w + 2i, + 1; lane l lands in
-  // row 4w + 2i + l/32, physical chunk l % 32, holding logical chunk
-  // (l % 32) ^ key(row).
-  uint32_t a_col[2], b_col[2];
+  // DMA (B, 512-byte rows): wave w's instruction i fills tile rows 4w + 2i,
+  // + 1; lane l lands in row 4w + 2i + l/32, physical chunk l % 32, holding
+  // logical chunk (l % 32) ^ key(row).  A (kRowA-byte rows) likewise: whole
+  // tiles as B; half tiles one instruction of rows 4w .. 4w + 3, lane l in
+  // row 4w + l/16, physical chunk l % 16.
+  uint32_t a_col[kInstA], b_col[2];
+  int a_row[kInstA], b_row[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int R = 4 * wave + 2 * i + (lane >> 5);
     const int lc = (lane & 31) ^ wg_key(R);
-    a_col[i] = 2u * (uint32_t)(i0 + lc * 8);
+    b_row[i] = R;
     b_col[i] = 2u * (uint32_t)(j0 + lc * 8);
   }
-  auto issue = [&](int kt) {
-    bf16_t *sa = lds + (size_t)(kt & (kStages - 1)) * (kStageBytes / 2);
-    bf16_t *sb = sa + kTileBytes / 2;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int rr = kt * BK + 4 * wave + 2 * i + (lane >> 5);
+  for (int i = 0; i < kInstA; ++i) {
+    const int R = BPT == 256 ? 4 * wave + 2 * i + (lane >> 5) : 4 * wave + (lane >> 4);
+    const int lc = (BPT == 256 ? (lane & 31) : (lane & 15)) ^ wg_key(R);
+    a_row[i] = R;
+    a_col[i] = 2u * (uint32_t)(i0 + lc * 8);
+  }
+  auto issue = [&](int kt) {
+    bf16_t *sa = lds + (size_t)(kt & (kStages - 1)) * (kStage / 2);
+    bf16_t *sb = sa + kTileA / 2;
+#pragma unroll
+    for (int i = 0; i < kInstA; ++i) {
+      const int rr = kt * BK + a_row[i];
       const bool ok = rr < mg;
       const uint32_t row = (uint32_t)(row_lo + rr);
       wg_dma(ra, ok ? row * (uint32_t)lda * 2u + a_col[i] : kOutOfRange,
-             sa + (4 * wave + 2 * i) * BP);
+             sa + (BPT == 256 ? 4 * wave + 2 * i : 4 * wave) * BPT);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rr = kt * BK + b_row[i];
+      const bool ok = rr < mg;
+      const uint32_t row = (uint32_t)(row_lo + rr);
       wg_dma(rb, ok ? row * (uint32_t)ldb * 2u + b_col[i] : kOutOfRange,
-             sb + (4 * wave + 2 * i) * BP);
+             sb + (4 * wave + 2 * i) * BQ);
     }
   };
 
   // Transposing reads: lane 16g + m reads row 4g + m/4 at column
-  // 16 blk + 4 (m % 4) of the wave's columns (128 of A, 64 of B).
+  // 16 blk + 4 (m % 4) of the wave's columns (BPT / 2 of A, 64 of B).
   const uint32_t lds_base = (uint32_t)(size_t)(const __attribute__((address_space(3))) bf16_t *)lds;
-  uint32_t a_rd[8], b_rd[4];
+  uint32_t a_rd[kIB], b_rd[4];
   {
     const int g4 = lane >> 4, m = lane & 15;
     const int R = 4 * g4 + (m >> 2);
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
-      const int ca = wp * 128 + blk * 16 + 4 * (m & 3);
-      a_rd[blk] = lds_base + (uint32_t)(R * kRowBytes + (((ca >> 3) ^ wg_key(R)) << 4) + (ca & 7) * 2);
+    for (int blk = 0; blk < kIB; ++blk) {
+      const int ca = wp * (BPT / 2) + blk * 16 + 4 * (m & 3);
+      a_rd[blk] = lds_base + (uint32_t)(R * kRowA + (((ca >> 3) ^ wg_key(R)) << 4) + (ca & 7) * 2);
     }
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       const int cb = wq * 64 + blk * 16 + 4 * (m & 3);
-      b_rd[blk] = lds_base + kTileBytes +
+      b_rd[blk] = lds_base + kTileA +
                   (uint32_t)(R * kRowBytes + (((cb >> 3) ^ wg_key(R)) << 4) + (cb & 7) * 2);
     }
   }
 
-  f32x4 acc[4][8];
+  f32x4 acc[4][kIB];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < kIB; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = (mg + BK - 1) / BK;
   // Ping-pong K loop (as the forward GEMM's): waves 0-3 (group 0) and 4-7
@@ -422,11 +411,11 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
   issue(0);
   if (KT > 1) issue(1);
   if (KT > 2) issue(2);
-  // Own share of stage 0 (4 instructions per stage and wave).
+  // Own share of stage 0 (kInst instructions per stage and wave).
   if (KT > 2)
-    PRICHS_WG_VMCNT(8);
+    PRICHS_WG_VMCNT(2 * kInst);
   else if (KT > 1)
-    PRICHS_WG_VMCNT(4);
+    PRICHS_WG_VMCNT(kInst);
   else
     PRICHS_WG_VMCNT(0);
   pp_barrier();
@@ -435,8 +424,8 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
   // wait (stages kt + 2 .. min(kt + 3, KT - 1)), a compile-time count.
   auto kstep = [&](int kt, auto ahead_c) {
     constexpr int kAhead = decltype(ahead_c)::value;
-    const uint32_t st = (uint32_t)(kt & (kStages - 1)) * kStageBytes;
-    u32x2 alo[8], ahi[8], bt[8];  // bt: B lo (0..3) and hi (4..7)
+    const uint32_t st = (uint32_t)(kt & (kStages - 1)) * kStage;
+    u32x2 alo[8], ahi[8], bt[8];  // bt: B lo (0..3) and hi (4..7); A: kIB used
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       bt[blk] = wg_read_tr<0>(b_rd[blk] + st);
@@ -444,11 +433,15 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
     }
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
-      alo[blk] = wg_read_tr<0>(a_rd[blk] + st);
-      ahi[blk] = wg_read_tr<(int)kHiOff>(a_rd[blk] + st);
+      if (blk < kIB) {
+        alo[blk] = wg_read_tr<0>(a_rd[blk] + st);
+        ahi[blk] = wg_read_tr<(int)kHiA>(a_rd[blk] + st);
+      } else {
+        alo[blk] = ahi[blk] = u32x2{0u, 0u};
+      }
     }
     if constexpr (kAhead == 2) issue(kt + 3);
-    PRICHS_WG_VMCNT(4 * kAhead);
+    PRICHS_WG_VMCNT(kInst * kAhead);
     wg_wait_tied(bt);
     wg_wait_tied(alo);
     wg_wait_tied(ahi);
@@ -458,7 +451,7 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
       const bf16x8 bf =
           __builtin_bit_cast(bf16x8, u32x4{bt[jb][0], bt[jb][1], bt[4 + jb][0], bt[4 + jb][1]});
 #pragma unroll
-      for (int ib = 0; ib < 8; ++ib) {
+      for (int ib = 0; ib < kIB; ++ib) {
         const bf16x8 af =
             __builtin_bit_cast(bf16x8, u32x4{alo[ib][0], alo[ib][1], ahi[ib][0], ahi[ib][1]});
         acc[jb][ib] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, af, acc[jb][ib], 0, 0, 0);
@@ -475,7 +468,7 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
   if (grp == 0) pp_barrier();  // both groups leave after the same barrier count
 
   // acc[jb][ib] lane l holds out[i = 16 ib + l % 16][j = 16 jb + 4 (l / 16) + r]
-  // of the wave's 128 x 64 block.
+  // of the wave's (BPT / 2) x 64 block.
   const long long base = (long long)slot_of(g, E) * slot_stride;
   if (pslot >= 0 || beta == 0) {
     // Stores only: a chunk partial, or the gradient itself when beta = 0.
@@ -483,8 +476,8 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int ib = 0; ib < 8; ++ib) {
-        const int i = i0 + wp * 128 + ib * 16 + (lane & 15);
+      for (int ib = 0; ib < kIB; ++ib) {
+        const int i = i0 + wp * (BPT / 2) + ib * 16 + (lane & 15);
         const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
         const f32x4 a = acc[jb][ib];
         float *dst = pbase != nullptr ? (i < P && j < Q ? pbase + (long long)i * Q + j : nullptr)
@@ -497,17 +490,17 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
   // its stores (a load cannot move past a store that may alias it).
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) {
-    float *dst[8];
-    float4 old[8];
+    float *dst[kIB];
+    float4 old[kIB];
 #pragma unroll
-    for (int ib = 0; ib < 8; ++ib) {
-      const int i = i0 + wp * 128 + ib * 16 + (lane & 15);
+    for (int ib = 0; ib < kIB; ++ib) {
+      const int i = i0 + wp * (BPT / 2) + ib * 16 + (lane & 15);
       const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
       dst[ib] = wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
       old[ib] = dst[ib] ? *reinterpret_cast<const float4 *>(dst[ib]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int ib = 0; ib < 8; ++ib) {
+    for (int ib = 0; ib < kIB; ++ib) {
       const f32x4 a = acc[jb][ib];
       if (dst[ib]) {
         float4 v = old[ib];
@@ -518,6 +511,92 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
         *reinterpret_cast<float4 *>(dst[ib]) = v;
       }
     }
+  }
+}
+
+// The tile kernel: one work item per workgroup.  Items are the groups in
+// launch order (shared first), each as its chunks x tiles; when the items
+// fill the last round of `cus` workgroups at most half, each of that round's
+// items is computed as two half-height items (128 P rows) on two
+// workgroups, so the round takes about half as long.  Every output element
+// is the same MFMA chain over the item's rows either way.  HALVES selects
+// this: dW_down's launch takes it (config 2: 360 items, a last round of 104
+// on 256 CUs, 152 -> 144 us); dW_gate/up's does not (its last rounds are
+// fuller, and with the half-height path compiled in its whole items ran
+// 1-3% slower).
+template <bool GATEUP, bool HALVES>
+__global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
+    const bf16_t *__restrict__ A, int lda, uint32_t a_bytes, const bf16_t *__restrict__ B,
+    int ldb, uint32_t b_bytes, const int32_t *__restrict__ offsets, int G, int E, int P, int Q,
+    int tiles_q, int tiles, float *out0, float *out1, int ldo, long long slot_stride, int f,
+    float *__restrict__ part, int beta, int cus) {
+  using namespace wgb;
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  // The offsets come to LDS in one parallel load.
+  __shared__ int item[6];  // group (-1: none), first row, end row, partial slot (-1: none), tile, half
+  __shared__ int offs_s[PRICHS_MAX_EXPERTS + 2];
+  if ((int)threadIdx.x <= G) offs_s[threadIdx.x] = offsets[threadIdx.x];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int n_items = 0x7fffffff;  // (without halves the walk below finds the end)
+    if (HALVES) {
+      n_items = 0;
+      for (int g = 0; g < G; ++g) {
+        const int m = offs_s[g + 1] - offs_s[g];
+        if (m <= 0) continue;
+        int L, nc;
+        wg_split(m, L, nc);
+        n_items += nc * tiles;
+      }
+    }
+    const int tail = HALVES && cus > 0 ? n_items % cus : 0;
+    const bool halves = tail > 0 && 2 * tail <= cus;
+    const int n_whole = halves ? n_items - tail : n_items;
+    int rest = (int)blockIdx.x, half = -1;
+    if (rest >= n_whole) {
+      const int u = rest - n_whole;
+      rest = halves && u < 2 * tail ? n_whole + u / 2 : n_items;  // n_items: no item
+      half = u & 1;
+    }
+    int pslot = 0;
+    item[0] = -1;
+    for (int gi = 0; gi < G && rest < n_items; ++gi) {
+      const int g = (gi + G - 1) % G;
+      const int lo = offs_s[g], m = offs_s[g + 1] - lo;
+      if (m <= 0) continue;
+      int L, nc;
+      wg_split(m, L, nc);
+      if (rest < nc * tiles) {
+        const int c = rest / tiles;
+        item[0] = g;
+        item[1] = lo + c * L;
+        item[2] = min(lo + (c + 1) * L, lo + m);
+        item[3] = nc == 1 ? -1 : pslot + c;
+        item[4] = rest - c * tiles;
+        item[5] = half;
+        break;
+      }
+      rest -= nc * tiles;
+      if (nc > 1) pslot += nc;
+    }
+  }
+  __syncthreads();
+  const int g = item[0];
+  if (g < 0) return;
+  const int row_lo = item[1];
+  const int mg = item[2] - row_lo;
+  const int pslot = item[3];
+  const int tile = item[4];
+  const int half = item[5];
+  const int tp = tile / tiles_q;
+  const int i0 = tp * BP, j0 = (tile - tp * tiles_q) * BQ;
+  if (half < 0) {
+    wgrad_item<GATEUP, 256>(A, lda, a_bytes, B, ldb, b_bytes, E, P, Q, out0, out1, ldo,
+                            slot_stride, f, part, beta, lds, g, row_lo, mg, pslot, i0, j0);
+  } else if constexpr (HALVES) {
+    wgrad_item<GATEUP, 128>(A, lda, a_bytes, B, ldb, b_bytes, E, P, Q, out0, out1, ldo,
+                            slot_stride, f, part, beta, lds, g, row_lo, mg, pslot, i0 + 128 * half,
+                            j0);
   }
 }
 
@@ -1082,8 +1161,9 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
     if (ab >= wgb::kOutOfRange || bb >= wgb::kOutOfRange)
       return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: operands of %zu and %zu bytes exceed 2 GiB",
                   ab, bb);
-    if (items > (size_t)INT32_MAX) return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: too many tiles");
-    auto kern = gateup ? wgrad_bf16_kernel<true> : wgrad_bf16_kernel<false>;
+    if (items + (size_t)cus > (size_t)INT32_MAX)
+      return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: too many tiles");
+    auto kern = gateup ? wgrad_bf16_kernel<true, false> : wgrad_bf16_kernel<false, true>;
     static bool attr_set[2] = {false, false};
     if (!attr_set[gateup]) {
       PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -1092,11 +1172,16 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
                      "moe backward: set LDS size");
       attr_set[gateup] = true;
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)items), dim3(wgb::kThreads), wgb::kLdsBytes, s,
+    // The item bound plus half a round: a last round of at most cus / 2
+    // items may run as twice as many half-height items.  (Workgroups past
+    // the items exit at once, but each still waits for a free CU.)
+    const bool halves = !gateup;  // dW_down (see wgrad_bf16_kernel)
+    const size_t grid = items + (halves ? (size_t)(cus / 2) : 0);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(wgb::kThreads), wgb::kLdsBytes, s,
                        static_cast<const bf16_t *>(A), (int)lda, (uint32_t)ab,
                        static_cast<const bf16_t *>(B), (int)ldb, (uint32_t)bb, offsets, (int)G,
                        (int)E, (int)P, (int)Q, tiles_q, tiles, out0, out1, (int)ldo,
-                       (long long)slot_stride, (int)f, part, beta);
+                       (long long)slot_stride, (int)f, part, beta, cus);
     PRICHS_LAUNCH_CHECK("moe backward: weight gradient");
     // Some group may have been split, or (beta = 0) may have no rows.
     if (total_rows > (size_t)wgb::kSplitRows || beta == 0) {
