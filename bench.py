@@ -564,9 +564,9 @@ def bench_backward(args):
         "dw_gate_up": 4.0 * rows * d * f, "d_x_gemm": 4.0 * rows * f * d,
     }
     kernels = {
-        "dw_down": "grouped weight gradient dW_down += act^T dY (wgrad_bf16_kernel<false>)",
+        "dw_down": "grouped weight gradient dW_down += act^T dY (wgrad_bf16_kernel<false>, then wgrad_reduce_kernel<false>; the stage times both)",
         "d_act": "grouped GEMM dA = dY Wd^T (bf16_gemm_kernel<Bf16Cfg<256,256,4,2>, Bf16Cfg<256,128,4,2>, false>)",
-        "dw_gate_up": "grouped weight gradient dW_gate/up += x^T [dG dU] (wgrad_bf16_kernel<true>)",
+        "dw_gate_up": "grouped weight gradient dW_gate/up += x^T [dG dU] (wgrad_bf16_kernel<true>, then wgrad_reduce_kernel<true> adding the shared expert's K-chunk partials; the stage times both)",
         "d_x_gemm": "grouped GEMM dX = [dG dU] [Wg Wu]^T (bf16_gemm_kernel<Bf16Cfg<256,256,4,2>, Bf16Cfg<256,128,4,2>, false>)",
     }
     per = {kk: {"ms": bms[kk], "tflops": fl / (bms[kk] / 1e3) / 1e12}
