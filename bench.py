@@ -121,52 +121,104 @@ def device_caps():
             "bf16_dense_peak_TFLOPs_from_caps": cus * clk * 1e3 * 4096 / 1e12}
 
 
+def _lib_copy(src, dst):
+    from prichs_amd import ops
+
+    ops.hbm_copy(src, dst)
+
+
+def graph_event_ms(fn, reps: int = 20) -> float:
+    """Mean device time of fn() over `reps` back-to-back calls, captured into
+    one HIP graph and replayed between two events, so host launch overhead
+    (Python and ctypes, ~10 us a call) cannot leave the GPU idle inside the
+    interval -- short kernels would otherwise be timed at the host's pace."""
+    import torch
+
+    fn()  # one-time launch attributes stay outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    del g
+    return a.elapsed_time(b) / reps
+
+
 def copy_bandwidth(reps: int = 10):
-    """Device-to-device copy of 2 GiB (torch's copy kernel) timed with HIP
-    events: read + write bytes per second, a measured practical HBM peak."""
+    """Device-to-device copy of 2 GiB with the library's streaming copy kernel
+    (prichs_hbm_copy), timed with HIP events: read + write bytes per second,
+    the measured practical HBM peak.  torch's copy of the same buffers is
+    timed beside it for reference."""
     import torch
 
     n = (2 << 30) // 4
     src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
-    for _ in range(2):
-        dst.copy_(src)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
+    res = {}
+    for name, fn in (("prichs_hbm_copy", lambda: _lib_copy(src, dst)),
+                     ("torch_copy", lambda: dst.copy_(src))):
+        for _ in range(2):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        res[name] = {"GB/s": 2 * n * 4 / (ms * 1e-3) / 1e9, "ms": ms}
     del src, dst
-    return {"GB/s": 2 * n * 4 / (ms * 1e-3) / 1e9, "bytes_per_copy": 2 * n * 4, "ms": ms,
-            "kernel": "torch copy_ of 2 GiB (read + write counted), HIP events, mean of "
-                      f"{reps}"}
+    out = dict(res["prichs_hbm_copy"])
+    out.update({"bytes_per_copy": 2 * n * 4, "torch_copy_GB/s": res["torch_copy"]["GB/s"],
+                "kernel": "prichs_hbm_copy of 2 GiB (read + write counted), HIP events, mean of "
+                          f"{reps}; torch_copy_GB/s: torch copy_ of the same buffers"})
+    return out
 
 
-def copy_same_bytes_flushed(moved_bytes: int, flush, reps: int = 10):
-    """The practical cold roof of a memory-bound kernel that moves moved_bytes
-    (reads + writes): a device copy of moved_bytes / 2 (torch's copy kernel),
-    L2 and MALL flushed before each repetition, event-timed like the kernels.
-    At tens of MB the ramp of a cold launch, not the 8 TB/s HBM peak, bounds
-    any streaming kernel."""
+def copy_same_bytes(moved_bytes: int, flush=None, reps: int = 10):
+    """The practical roof of a memory-bound kernel that moves moved_bytes
+    (reads + writes): the library's streaming copy (prichs_hbm_copy) of
+    moved_bytes / 2, event-timed like the kernels -- warm (back to back), or
+    with L2 and MALL flushed before each repetition when flush is given.  At
+    tens of MB the ramp of a launch, not the 8 TB/s HBM peak, bounds any
+    streaming kernel."""
     import torch
 
-    n = max(1, moved_bytes // 2 // 4)
+    n = max(4, (moved_bytes // 2 // 16) * 4)
     src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
-    dst.copy_(src)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(reps)]
-    for a, b in evs:
-        flush()
-        a.record()
-        dst.copy_(src)
-        b.record()
-    torch.cuda.synchronize()
-    ms = sum(a.elapsed_time(b) for a, b in evs) / reps
+    _lib_copy(src, dst)
+    if flush is None:  # warm: back-to-back copies in one graph
+        ms = graph_event_ms(lambda: _lib_copy(src, dst), reps)
+    else:  # each copy after a flush (the flush keeps the host ahead of the GPU)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps)]
+        for a, b in evs:
+            flush()
+            a.record()
+            _lib_copy(src, dst)
+            b.record()
+        torch.cuda.synchronize()
+        ms = sum(a.elapsed_time(b) for a, b in evs) / reps
     del src, dst
     return {"ms": ms, "GB/s": 2 * n * 4 / (ms * 1e-3) / 1e9}
+
+
+def stage_vs_copy(ms: float, ms_flushed: float, nbytes: int, flush):
+    """A memory-bound stage's rate against the library copy of the same bytes,
+    warm and flushed: {"copy_same_bytes": .., "copy_same_bytes_flushed": ..,
+    "frac_of_copy": .., "frac_of_copy_flushed": ..}."""
+    warm = copy_same_bytes(nbytes)
+    cold = copy_same_bytes(nbytes, flush)
+    return {"copy_same_bytes": warm, "copy_same_bytes_flushed": cold,
+            "frac_of_copy": warm["ms"] / ms, "frac_of_copy_flushed": cold["ms"] / ms_flushed}
 
 
 def library_dense_equivalent(rows: int, d: int, f: int, reps: int = 50, rounds: int = 3):
@@ -348,10 +400,11 @@ def main():
     ms_cold = eng.stage_ms()
     eng.set_timing(0)
     es_ = 2 if inp.dtype == "bf16" else 4
-    copy_ref = {"router": copy_same_bytes_flushed(T * d * es_ + d * E * 4 + T * E * 4 + T * k * 8,
-                                                  flush),
-                "combine": copy_same_bytes_flushed((T * k + S * T) * d * es_ + T * k * 12
-                                                   + T * d * es_, flush)}
+    copy_ref = {
+        "router": stage_vs_copy(ms["router"], ms_cold["router"],
+                                T * d * es_ + d * E * 4 + T * E * 4 + T * k * 8, flush),
+        "combine": stage_vs_copy(ms["combine"], ms_cold["combine"],
+                                 (T * k + S * T) * d * es_ + T * k * 12 + T * d * es_, flush)}
     del flush
     # Library yardstick (prefill bf16 shapes only; decode is HBM-bound).
     rows_ = T * k + S * T
@@ -439,7 +492,7 @@ def main():
             "router": {"ms": ms["router"], "GB/s": gbps(router_bytes, "router"),
                        "ms_flushed": ms_cold["router"],
                        "GB/s_flushed": gbps(router_bytes, "router", ms_cold), "bytes": router_bytes,
-                       "copy_same_bytes_flushed": copy_ref["router"]},
+                       **copy_ref["router"]},
             "permute": {"ms": ms["permute"], "GB/s": gbps(permute_bytes, "permute"),
                         "ms_flushed": ms_cold["permute"],
                         "GB/s_flushed": gbps(permute_bytes, "permute", ms_cold),
@@ -447,11 +500,12 @@ def main():
             "combine": {"ms": ms["combine"], "GB/s": gbps(combine_bytes, "combine"),
                         "ms_flushed": ms_cold["combine"],
                         "GB/s_flushed": gbps(combine_bytes, "combine", ms_cold),
-                        "bytes": combine_bytes,
-                        "copy_same_bytes_flushed": copy_ref["combine"]},
+                        "bytes": combine_bytes, **copy_ref["combine"]},
             "peak_GB/s": PEAK_HBM_GBPS,
             "note": "flushed = L2 and MALL overwritten (512 MiB) before each forward, outside the "
-                    "stage intervals; the combine reads y right after the down GEMM wrote it",
+                    "stage intervals; the combine reads y right after the down GEMM wrote it; "
+                    "copy_same_bytes* = the library's streaming copy (prichs_hbm_copy) of the "
+                    "stage's bytes, timed the same way; frac_of_copy = copy ms / stage ms",
         },
         "stage_ms": {kk: v for kk, v in ms.items() if kk != "n"},
         "stage_ms_flushed": {kk: v for kk, v in ms_cold.items() if kk != "n"},
@@ -689,31 +743,29 @@ def bench_block(args):
         eng.forward(x, B, S, out=out)
 
     elapsed_first = timed_pass(fwd, args.steps, args.warmup)
-    # Attention alone on the last forward's roped q/k/v, HIP events on the stream.
+    # Attention alone, as the block runs it: on the last forward's stashed
+    # q/k/v (q as projected, k rotated) through the entry point that rotates q
+    # as it loads it, with the block's RoPE tables; HIP events on the stream.
     qkv = eng.stash()["qkv"]
     Hq, Hkv, hd = inp.n_heads, inp.n_kv_heads, inp.head_dim
     q, k, v = qkv[:, :Hq * hd], qkv[:, Hq * hd:(Hq + Hkv) * hd], qkv[:, (Hq + Hkv) * hd:]
+    cos, sin = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to("cuda")
+                for a in synth.rope_cache(S, hd, inp.rope_theta))
     ao = torch.empty((T, d), dtype=torch.bfloat16, device="cuda")
+    att_fn = lambda: ops.attention(q, k, v, B, S, Hq, Hkv, out=ao, rope_q=(cos, sin, 0))  # noqa: E731
     for _ in range(3):
-        ops.attention(q, k, v, B, S, Hq, Hkv, out=ao)
+        att_fn()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(args.steps):
-        ops.attention(q, k, v, B, S, Hq, Hkv, out=ao)
+        att_fn()
     e1.record()
     torch.cuda.synchronize()
     att_ms = e0.elapsed_time(e1) / args.steps
 
-    def event_ms(fn, reps=args.steps):
-        for _ in range(3):
-            fn()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(reps):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps
+    def event_ms(fn, reps=max(args.steps, 20)):
+        # back-to-back calls replayed from a graph (no host gaps)
+        return graph_event_ms(fn, reps)
 
     flush = Flusher()
 
@@ -738,8 +790,6 @@ def bench_block(args):
     rn_out = torch.empty_like(x)
     rn_ms = event_ms(lambda: ops.rmsnorm(x, w_norm, want_rstd=False, out=rn_out))
     rn_ms_cold = event_ms_flushed(lambda: ops.rmsnorm(x, w_norm, want_rstd=False, out=rn_out))
-    cos, sin = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to("cuda")
-                for a in synth.rope_cache(S, hd, inp.rope_theta))
     qr = q.contiguous().view(B, S, Hq, hd)
     kr = k.contiguous().view(B, S, Hkv, hd)
     rope_fn = lambda: (ops.rope_(qr, cos, sin, S, B, S), ops.rope_(kr, cos, sin, S, B, S))  # noqa: E731
@@ -747,8 +797,8 @@ def bench_block(args):
     rope_ms_cold = event_ms_flushed(rope_fn)
     rn_bytes = 2 * T * d * 2 + d * 4
     rope_bytes = 2 * T * (Hq + Hkv) * hd * 2 + 2 * S * (hd // 2) * 4
-    rn_copy = copy_same_bytes_flushed(rn_bytes, flush)
-    rope_copy = copy_same_bytes_flushed(rope_bytes, flush)
+    rn_copy = stage_vs_copy(rn_ms, rn_ms_cold, rn_bytes, flush)
+    rope_copy = stage_vs_copy(rope_ms, rope_ms_cold, rope_bytes, flush)
     del flush
     elapsed = timed_pass(fwd, args.steps, args.warmup)
     att_flops = B * Hq * 4.0 * hd * S * (S + 1) / 2  # causal QK^T + PV
@@ -763,7 +813,8 @@ def bench_block(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded SplitMix64 + Box-Muller, seed 0)",
         "config": {"workload": WORKLOADS[5], "batch": B, "seq_len": S, "d_model": d},
-        "roofline": {"kernel": "attn_fwd_kernel (causal GQA flash attention)", "bound": "mfma",
+        "roofline": {"kernel": "attn_fwd_kernel (causal GQA flash attention, q rotated by RoPE "
+                               "as it is loaded, as in the block)", "bound": "mfma",
                      "achieved": att_flops / (att_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": att_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
                      "traffic": None, "algorithmic_flops_per_launch": att_flops,
@@ -773,16 +824,18 @@ def bench_block(args):
             "rmsnorm": {"ms": rn_ms, "GB/s": rn_bytes / (rn_ms * 1e-3) / 1e9,
                         "ms_flushed": rn_ms_cold,
                         "GB/s_flushed": rn_bytes / (rn_ms_cold * 1e-3) / 1e9, "bytes": rn_bytes,
-                        "copy_same_bytes_flushed": rn_copy},
+                        **rn_copy},
             "rope_q_and_k": {"ms": rope_ms, "GB/s": rope_bytes / (rope_ms * 1e-3) / 1e9,
                              "ms_flushed": rope_ms_cold,
                              "GB/s_flushed": rope_bytes / (rope_ms_cold * 1e-3) / 1e9,
                              "bytes": rope_bytes,
-                             "copy_same_bytes_flushed": rope_copy,
+                             **rope_copy,
                              "note": "two launches (Q 12 heads, K 3 heads); the copy is one"},
             "peak_GB/s": PEAK_HBM_GBPS,
             "note": "flushed = L2 and MALL overwritten (512 MiB) before each repetition, outside "
-                    "its event pair",
+                    "its event pair; copy_same_bytes* = the library's streaming copy "
+                    "(prichs_hbm_copy) of the stage's bytes, timed the same way; frac_of_copy = "
+                    "copy ms / stage ms",
         },
         "inputs": inputs_record("config5", inp.digest()),
         "device": torch.cuda.get_device_name(0),

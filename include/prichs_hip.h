@@ -294,6 +294,12 @@ int prichs_rope_forward_ld(void *qk, size_t row_stride, int dtype,
 int prichs_add(const void *a, int a_dtype, const void *b, int b_dtype,
                void *out, int out_dtype, size_t n, void *stream);
 
+/* dst = src, bytes a multiple of 16, both 16-byte aligned, no overlap: a
+ * streaming copy kernel of this library (16 bytes per lane, 8 chunks per
+ * thread in flight), the practical HBM yardstick that the memory-bound
+ * stages are measured against.  No counterpart in the reference. */
+int prichs_hbm_copy(const void *src, void *dst, size_t bytes, void *stream);
+
 /* Dense GEMM C[M, N] = A[M, K] @ W on the bf16 (or f32) MFMA kernel of the
  * grouped GEMMs: replaces matmul_2d's device dispatch / forward_gemm
  * (crates/prichs-core/src/ops.rs:24-31; crates/prichs-cuda/src/engine.rs:
@@ -323,6 +329,24 @@ int prichs_attention_forward(const void *q, size_t ldq, const void *k,
                              size_t ldo, size_t batch, size_t seq_len,
                              size_t n_heads, size_t n_kv_heads,
                              size_t head_dim, int dtype, void *stream);
+
+/* The same attention with RoPE applied to q as the kernel loads it: query
+ * row r of sequence b is rotated at position pos_offset + r with the tables
+ * cos / sin [cache_rows, head_dim / 2] of prichs_rope_cache (device memory),
+ * by the interleaved-pair rotation of crates/prichs-core/src/backward.rs:
+ * 160-188 with the same roundings as prichs_rope_forward, so the output is
+ * bit-identical to prichs_rope_forward on q followed by
+ * prichs_attention_forward.  k must be rotated already (the reference's
+ * SelfAttention::forward_with_rope rotates q and k, attention.rs:56-92).
+ * seq_len + pos_offset <= cache_rows.  The block engine runs its attention
+ * this way (q is never written back rotated). */
+int prichs_attention_forward_rope_q(const void *q, size_t ldq, const void *k,
+                                    size_t ldk, const void *v, size_t ldv, void *o,
+                                    size_t ldo, size_t batch, size_t seq_len,
+                                    size_t n_heads, size_t n_kv_heads,
+                                    size_t head_dim, int dtype, const float *rope_cos,
+                                    const float *rope_sin, size_t cache_rows,
+                                    size_t pos_offset, void *stream);
 
 /* f32 causal attention of one sequence with the probabilities kept: the
  * per-head computation of crates/prichs-model/src/attention.rs:96-149 (scores
@@ -635,7 +659,10 @@ int prichs_matmul_f32(int op, const float *a, const float *b, float *c, size_t m
 /* GpuWorkspace (cublas.rs:46-115): three device slabs for A, B and C, sized in
  * bytes; 0 selects the reference's sizes (16 MB, 32 MB, 16 MB,
  * cublas.rs:77-84).  The workspace belongs to the device current at
- * creation.  A handle is not internally synchronised. */
+ * creation.  Calls on one handle are serialised by a lock of its own (the
+ * reference hands its workspace out as a Mutex<GpuWorkspace>), so threads may
+ * share a handle.  Destroying the process-wide handle of
+ * prichs_get_gpu_workspace is refused (PRICHS_ERR_INVALID_ARGUMENT). */
 typedef struct prichs_gpu_workspace prichs_gpu_workspace;
 int prichs_gpu_workspace_create(size_t a_bytes, size_t b_bytes, size_t c_bytes,
                                 prichs_gpu_workspace **out);

@@ -117,11 +117,14 @@ SIGNATURES = {
     "prichs_rope_cache": (_i, [_sz, _sz, _f, _vp, _vp]),
     "prichs_rope_forward_ld": (_i, [_vp, _sz, _i, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _vp]),
     "prichs_add": (_i, [_vp, _i, _vp, _i, _vp, _i, _sz, _vp]),
+    "prichs_hbm_copy": (_i, [_vp, _vp, _sz, _vp]),
     "prichs_packed_weight_elems": (_sz, [_sz, _sz, _i]),
     "prichs_pack_weight": (_i, [_vp, _sz, _sz, _i, _vp]),
     "prichs_gemm": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _i, _vp]),
     "prichs_attention_forward": (_i, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
                                       _sz, _i, _vp]),
+    "prichs_attention_forward_rope_q": (_i, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                                             _sz, _sz, _i, _vp, _vp, _sz, _sz, _vp]),
     "prichs_attention_probs_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     "prichs_checkpoint_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
     "prichs_checkpoint_close": (_i, [_vp]),

@@ -522,6 +522,19 @@ extern "C" int prichs_attention_forward(const void *q, size_t ldq, const void *k
                                 n_kv_heads, head_dim, dtype, nullptr, nullptr, 0, 0, stream);
 }
 
+extern "C" int prichs_attention_forward_rope_q(const void *q, size_t ldq, const void *k,
+                                               size_t ldk, const void *v, size_t ldv, void *o,
+                                               size_t ldo, size_t batch, size_t seq_len,
+                                               size_t n_heads, size_t n_kv_heads,
+                                               size_t head_dim, int dtype, const float *rope_cos,
+                                               const float *rope_sin, size_t cache_rows,
+                                               size_t pos_offset, void *stream) {
+  PRICHS_REQUIRE(rope_cos && rope_sin, "attention_rope_q: null RoPE table");
+  return attention_forward_impl(q, ldq, k, ldk, v, ldv, o, ldo, batch, seq_len, n_heads,
+                                n_kv_heads, head_dim, dtype, rope_cos, rope_sin, cache_rows,
+                                pos_offset, stream);
+}
+
 // ---------------------------------------------------------------------------
 // f32 causal attention with materialised probabilities: the computation of
 // the reference's per-head CPU attention (crates/prichs-model/src/

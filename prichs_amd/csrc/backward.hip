@@ -254,6 +254,7 @@ constexpr uint32_t kHiOff = 16 * kRowBytes;           // rows 16.. of a tile
 constexpr uint32_t kOutOfRange = 0x80000000u;         // buffer offset that loads zeros
 constexpr int kSplitRows = 2560;
 static_assert(BQ == 4 * 64 && BP == 2 * 128, "wave grid 2 x 4 of 128 x 64");
+static_assert(kThreads == 8 * 64, "ping-pong K loop: two groups of 4 waves, one of each per SIMD");
 }  // namespace wgb
 
 // Chunking of a group of m > 0 rows: nc chunks of L rows (the last shorter).

@@ -5,6 +5,7 @@
 // the shape allows it (one wave64 sweeps 1 KiB per instruction), with scalar
 // fallbacks for ragged shapes.
 #include <cmath>
+#include <algorithm>
 
 #include "common.hpp"
 
@@ -806,4 +807,59 @@ extern "C" void launch_moe_scatter_add(const float *dev_exp_out, const int *dev_
                      hidden_dim);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) set_error("launch_moe_scatter_add: %s", hipGetErrorString(e));
+}
+
+// ------------------------------------------------------------------------
+// Streaming device copy: the build's own practical HBM yardstick for the
+// memory-bound stages (what a plain 16-byte-per-lane kernel moves on this
+// chip), timed like them.  Each thread loads kCopyUnroll 16-byte chunks of a
+// workgroup block (consecutive lanes, consecutive chunks: every wave
+// instruction covers 1 KiB contiguous), then stores them; workgroups stride
+// over the buffer block by block.
+// ------------------------------------------------------------------------
+namespace prichs {
+namespace {
+typedef uint32_t cp_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kCopyThreads = 256, kCopyUnroll = 8;
+
+__global__ __launch_bounds__(kCopyThreads) void hbm_copy_kernel(const cp_u32x4 *__restrict__ src,
+                                                                cp_u32x4 *__restrict__ dst,
+                                                                size_t n16) {
+  constexpr size_t kBlock = (size_t)kCopyThreads * kCopyUnroll;
+  for (size_t base = (size_t)blockIdx.x * kBlock; base < n16; base += (size_t)gridDim.x * kBlock) {
+    const size_t i0 = base + threadIdx.x;
+    if (base + kBlock <= n16) {
+      cp_u32x4 v[kCopyUnroll];
+#pragma unroll
+      for (int u = 0; u < kCopyUnroll; ++u) v[u] = src[i0 + (size_t)u * kCopyThreads];
+#pragma unroll
+      for (int u = 0; u < kCopyUnroll; ++u) dst[i0 + (size_t)u * kCopyThreads] = v[u];
+    } else {
+      for (int u = 0; u < kCopyUnroll; ++u) {
+        const size_t i = i0 + (size_t)u * kCopyThreads;
+        if (i < n16) dst[i] = src[i];
+      }
+    }
+  }
+}
+}  // namespace
+}  // namespace prichs
+
+extern "C" int prichs_hbm_copy(const void *src, void *dst, size_t bytes, void *stream) {
+  PRICHS_REQUIRE(bytes % 16 == 0, "hbm_copy: bytes=%zu must be a multiple of 16", bytes);
+  if (bytes == 0) return PRICHS_OK;
+  PRICHS_REQUIRE(src && dst, "hbm_copy: null pointer argument");
+  PRICHS_REQUIRE(((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0,
+                 "hbm_copy: src and dst must be 16-byte aligned");
+  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
+  PRICHS_REQUIRE(s0 + bytes <= d0 || d0 + bytes <= s0, "hbm_copy: src and dst overlap");
+  const int cus = device_cu_count();
+  if (cus <= 0) return fail(PRICHS_ERR_HIP, "hbm_copy: cannot query the device");
+  const size_t n16 = bytes / 16;
+  const size_t blocks = (n16 + (size_t)kCopyThreads * kCopyUnroll - 1) / ((size_t)kCopyThreads * kCopyUnroll);
+  const unsigned grid = (unsigned)std::min<size_t>(blocks, (size_t)cus * 8);
+  hipLaunchKernelGGL(hbm_copy_kernel, dim3(grid), dim3(kCopyThreads), 0, as_stream(stream),
+                     static_cast<const cp_u32x4 *>(src), static_cast<cp_u32x4 *>(dst), n16);
+  PRICHS_LAUNCH_CHECK("hbm_copy launch");
+  return PRICHS_OK;
 }

@@ -310,6 +310,7 @@ __device__ __forceinline__ void bf16_tile(
   constexpr int kRowsPerInst = Cf::kRowsPerInst, kInstA = Cf::kInstA, kInstB = Cf::kInstB;
   constexpr int kInstPerStage = Cf::kInstPerStage, kStageElems = Cf::kStageElems;
   static_assert(Cf::kThreads == kBf16Threads, "launch bound of the bf16 kernels");
+  static_assert(Cf::kWaves == 8, "ping-pong K loop: two groups of 4 waves, one of each per SIMD");
   static_assert(!GATEUP || (WN % (2 * Cf::kIl) == 0 && BN % (2 * Cf::kIl) == 0),
                 "whole [gate | up] blocks per wave; packed gate/up rows padded to BN");
 

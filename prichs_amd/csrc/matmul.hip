@@ -19,6 +19,7 @@
 #include "common.hpp"
 
 struct prichs_gpu_workspace {
+  std::mutex mu;  // serialises the calls on this handle (the reference's Mutex<GpuWorkspace>)
   int device = 0;
   void *base = nullptr;
   float *a = nullptr, *b = nullptr, *c = nullptr;  // slabs A, B, C
@@ -241,12 +242,24 @@ prichs_gpu_workspace *global_workspace_locked() {
   return g_ws;
 }
 
+// One call on a handle, under that handle's lock: the slabs are shared by
+// every caller of the handle (the process-wide one included).
+int locked_run(prichs_gpu_workspace *ws, int op, const float *a, const float *b, float *c,
+               size_t m, size_t k, size_t n, const char *who) {
+  PRICHS_REQUIRE(ws != nullptr, "%s: null workspace", who);
+  std::lock_guard<std::mutex> lock(ws->mu);
+  return workspace_run(ws, op, a, b, c, m, k, n, who);
+}
+
 int global_run(int op, const float *a, const float *b, float *c, size_t m, size_t k, size_t n,
                const char *who) {
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  prichs_gpu_workspace *ws = global_workspace_locked();
+  prichs_gpu_workspace *ws;
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    ws = global_workspace_locked();
+  }
   if (!ws) return PRICHS_ERR_HIP;
-  return workspace_run(ws, op, a, b, c, m, k, n, who);
+  return locked_run(ws, op, a, b, c, m, k, n, who);
 }
 
 }  // namespace
@@ -300,6 +313,13 @@ extern "C" int prichs_gpu_workspace_create(size_t a_bytes, size_t b_bytes, size_
 
 extern "C" int prichs_gpu_workspace_destroy(prichs_gpu_workspace *ws) {
   if (!ws) return PRICHS_OK;
+  {
+    // The process-wide workspace lives until the process ends, as the
+    // reference's static does (cublas.rs:283-300).
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    PRICHS_REQUIRE(ws != g_ws, "gpu_workspace_destroy: the process-wide workspace "
+                               "(get_gpu_workspace) is not destroyed by callers");
+  }
   int rc = PRICHS_OK;
   {
     Guard g(ws->device);
@@ -322,19 +342,19 @@ extern "C" int prichs_gpu_workspace_slabs(const prichs_gpu_workspace *ws, size_t
 extern "C" int prichs_gpu_workspace_matmul(prichs_gpu_workspace *ws, const float *a,
                                            const float *b, float *c, size_t m, size_t k,
                                            size_t n) {
-  return workspace_run(ws, PRICHS_MATMUL_AB, a, b, c, m, k, n, "gpu_workspace_matmul");
+  return locked_run(ws, PRICHS_MATMUL_AB, a, b, c, m, k, n, "gpu_workspace_matmul");
 }
 
 extern "C" int prichs_gpu_workspace_matmul_at_b(prichs_gpu_workspace *ws, const float *a,
                                                 const float *b, float *dw, size_t m, size_t k,
                                                 size_t n) {
-  return workspace_run(ws, PRICHS_MATMUL_ATB, a, b, dw, m, k, n, "gpu_workspace_matmul_at_b");
+  return locked_run(ws, PRICHS_MATMUL_ATB, a, b, dw, m, k, n, "gpu_workspace_matmul_at_b");
 }
 
 extern "C" int prichs_gpu_workspace_matmul_a_bt(prichs_gpu_workspace *ws, const float *dy,
                                                 const float *w, float *dx, size_t m, size_t k,
                                                 size_t n) {
-  return workspace_run(ws, PRICHS_MATMUL_ABT, dy, w, dx, m, k, n, "gpu_workspace_matmul_a_bt");
+  return locked_run(ws, PRICHS_MATMUL_ABT, dy, w, dx, m, k, n, "gpu_workspace_matmul_a_bt");
 }
 
 extern "C" prichs_gpu_workspace *prichs_get_gpu_workspace(void) {

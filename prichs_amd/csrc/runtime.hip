@@ -46,7 +46,7 @@ extern "C" const char *prichs_last_error(void) { return prichs::g_last_error; }
 
 extern "C" void prichs_clear_error(void) { prichs::g_last_error[0] = 0; }
 
-extern "C" int prichs_abi_version(void) { return 100; }
+extern "C" int prichs_abi_version(void) { return 200; }
 
 // Capabilities of the current device for the roofline (all outputs may be
 // NULL): compute units, peak engine clock and memory clock in kHz, memory

@@ -198,6 +198,16 @@ def rope_(qk, cos, sin, cache_rows, batch, seq_len, pos_offset=0, sign=1, stream
     return qk
 
 
+def hbm_copy(src, dst, stream=None):
+    """prichs_hbm_copy: dst = src (device tensors of equal byte size, a multiple
+    of 16), the library's streaming copy kernel."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("hbm_copy: src and dst sizes differ")
+    L.check(L.load().prichs_hbm_copy(_p(src), _p(dst), nbytes, _stream(stream)))
+    return dst
+
+
 # ------------------------------------------------------- block sub-layers --
 def pack_weight(w: np.ndarray, dtype) -> np.ndarray:
     """prichs_pack_weight (host): W [K, N] -> packed [roundup(N, 256), K]."""
@@ -258,17 +268,29 @@ def add(a, b, out_dtype=None, stream=None):
 
 
 def attention(q, k, v, batch, seq_len, n_heads, n_kv_heads, head_dim=128, out=None,
-              stream=None):
+              stream=None, rope_q=None):
     """prichs_attention_forward on 2-D row views (rows = batch * seq_len; q/k/v may
-    be column slices of one fused buffer: their row strides are passed)."""
+    be column slices of one fused buffer: their row strides are passed).
+
+    rope_q = (cos, sin, pos_offset): prichs_attention_forward_rope_q instead --
+    q is rotated by RoPE as the kernel loads it (cos / sin: device f32 tables
+    [cache_rows, head_dim / 2]); k must be rotated already."""
     lib = L.load()
     if out is None:
         out = torch.empty((batch * seq_len, n_heads * head_dim), dtype=q.dtype, device=q.device)
     for t in (q, k, v, out):
         if t.stride(1) != 1:
             raise ValueError("attention operands need unit column stride")
-    L.check(lib.prichs_attention_forward(_p(q), q.stride(0), _p(k), k.stride(0), _p(v),
-                                         v.stride(0), _p(out), out.stride(0), batch, seq_len,
-                                         n_heads, n_kv_heads, head_dim, dtype_code(q),
-                                         _stream(stream)))
+    args = (_p(q), q.stride(0), _p(k), k.stride(0), _p(v), v.stride(0), _p(out), out.stride(0),
+            batch, seq_len, n_heads, n_kv_heads, head_dim, dtype_code(q))
+    if rope_q is None:
+        L.check(lib.prichs_attention_forward(*args, _stream(stream)))
+    else:
+        cos, sin, pos_offset = rope_q
+        for t in (cos, sin):
+            if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+                raise ValueError("rope tables must be contiguous f32 device tensors")
+        cache_rows = cos.numel() // (head_dim // 2)
+        L.check(lib.prichs_attention_forward_rope_q(*args, _p(cos), _p(sin), cache_rows,
+                                                    pos_offset, _stream(stream)))
     return out

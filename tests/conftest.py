@@ -42,3 +42,19 @@ def rel_err(a, b) -> float:
     den = np.abs(b).max() if b.size else 0.0
     num = np.abs(a - b).max() if a.size else 0.0
     return float(num / den) if den > 0 else float(num)
+
+
+def row_rel_err(a, b):
+    """Per-row bar: max over rows r of max |a[r] - b[r]| / max |b[r]| (rows whose
+    reference is all zero count their absolute error).  Returns (worst error,
+    worst row), so a wrong result confined to a few small-magnitude rows
+    cannot hide under the magnitude of the others."""
+    a = np.asarray(a, dtype=np.float64).reshape(len(a), -1)
+    b = np.asarray(b, dtype=np.float64).reshape(len(b), -1)
+    if a.size == 0:
+        return 0.0, -1
+    num = np.abs(a - b).max(axis=1)
+    den = np.abs(b).max(axis=1)
+    err = np.where(den > 0, num / np.where(den > 0, den, 1.0), num)
+    r = int(np.argmax(err))
+    return float(err[r]), r

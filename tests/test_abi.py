@@ -80,7 +80,7 @@ def test_legacy_backward_launchers_record_null_arguments(lib):
 
 
 def test_abi_version_and_error_slot(lib):
-    assert lib.prichs_abi_version() == 100
+    assert lib.prichs_abi_version() == 200
     lib.prichs_clear_error()
     assert L.last_error() == ""
 
@@ -89,6 +89,19 @@ def _expect(status, code, needle=None):
     assert status == code, (status, L.last_error())
     if needle:
         assert needle in L.last_error()
+
+
+def test_hbm_copy_argument_errors(lib):
+    # Validation runs before any device query: these fail the same way with
+    # or without a GPU.
+    p, q = C.c_void_p(4096), C.c_void_p(1 << 20)
+    _expect(lib.prichs_hbm_copy(p, q, 24, None), L.PRICHS_ERR_INVALID_ARGUMENT, "multiple of 16")
+    _expect(lib.prichs_hbm_copy(None, q, 32, None), L.PRICHS_ERR_INVALID_ARGUMENT, "null")
+    _expect(lib.prichs_hbm_copy(C.c_void_p(4104), q, 32, None), L.PRICHS_ERR_INVALID_ARGUMENT,
+            "aligned")
+    _expect(lib.prichs_hbm_copy(p, C.c_void_p(4096 + 16), 64, None),
+            L.PRICHS_ERR_INVALID_ARGUMENT, "overlap")
+    assert lib.prichs_hbm_copy(None, None, 0, None) == L.PRICHS_OK  # empty: no-op
 
 
 def test_router_argument_errors(lib):

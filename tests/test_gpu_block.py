@@ -261,6 +261,11 @@ def test_block_rotates_q_in_attention_bit_exact(cuda, pos_offset):
     attn = ops.attention(q.view(B * S, d), qkv[:, d:d + Hkv * hd], qkv[:, d + Hkv * hd:], B, S,
                          Hq, Hkv)
     assert torch.equal(attn.view(torch.int16), st["attn"].view(torch.int16))
+    # The public entry point that rotates q on load (prichs_attention_forward_
+    # rope_q) on the stashed, unrotated q: the same bits again.
+    attn_rq = ops.attention(qkv[:, :d], qkv[:, d:d + Hkv * hd], qkv[:, d + Hkv * hd:], B, S, Hq,
+                            Hkv, rope_q=(cos_d, sin_d, pos_offset))
+    assert torch.equal(attn_rq.view(torch.int16), st["attn"].view(torch.int16))
     blk.engine.close()
 
 

@@ -64,6 +64,53 @@ def test_process_wide_workspace_has_the_reference_slabs(cuda):
     assert workspace.get_gpu_workspace().handle.value == ws.handle.value
 
 
+def test_process_wide_workspace_is_locked_and_not_destroyed(cuda, orc):
+    # The reference hands its workspace out only as &Mutex<GpuWorkspace>
+    # (cublas.rs:283-300): every use is locked and the static lives on.  Here
+    # destroying the process-wide handle is refused, and threads that share
+    # its slabs -- through the handle and through matmul_gpu -- each get their
+    # own product (a race on slabs A/B/C would mix the operands of two calls).
+    import threading
+
+    say("case: process-wide workspace: destroy refused, 4 threads sharing the slabs")
+    ws = workspace.get_gpu_workspace()
+    assert L.load().prichs_gpu_workspace_destroy(ws.handle) == L.PRICHS_ERR_INVALID_ARGUMENT
+    assert "process-wide" in L.last_error()
+    rng = np.random.default_rng(11)
+    jobs = []
+    for t in range(4):
+        m, k, n = 48 + 16 * t, 64 + 8 * t, 40 + 24 * t
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        jobs.append((m, k, n, a, b, orc.matmul_2d(a, b)))
+    errors = []
+
+    def run(t):
+        m, k, n, a, b, ref = jobs[t]
+        for i in range(25):
+            out = np.zeros((m, n), np.float32)
+            if (i + t) % 2:
+                ws.matmul(a, b, out, m, k, n)
+            else:
+                workspace.matmul_gpu(a, b, out, m, k, n)
+            e = rel_err(out, ref)
+            if not e <= TOL:
+                errors.append((t, i, e))
+                return
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    # the handle still works after the refused destroy
+    m, k, n, a, b, ref = jobs[0]
+    out = np.zeros((m, n), np.float32)
+    ws.matmul(a, b, out, m, k, n)
+    assert rel_err(out, ref) <= TOL
+
+
 def test_capacity_error_before_any_copy(cuda):
     # The router shape's A operand (8192 x 1536 f32 = 48 MB) exceeds slab A:
     # PRICHS_ERR_CAPACITY, the reference's "exceed preallocated GPU workspace

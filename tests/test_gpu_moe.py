@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import rel_err
+from conftest import rel_err, row_rel_err
 from prichs_amd import _lib as L
 from prichs_amd import moe, ops, synth
 
@@ -144,7 +144,7 @@ def _stage_inputs(inp):
     return x, idx, w, off, rt, tr, gu, dn, order
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 4])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
 def test_grouped_gemms_against_oracle(cuda, orc, cfg):
     inp = synth.config_inputs(cfg)
     say("gemm", cfg)
@@ -156,21 +156,34 @@ def test_grouped_gemms_against_oracle(cuda, orc, cfg):
     h_off, h_rt = host(off), host(rt)
     h_act, h_y = host(act), host(y)
     tol = TOL[inp.dtype]
-    # Every row of every group (config 2: 24,576 rows).
+    rng = np.random.default_rng(cfg)
+    # Every row of every group (config 2: 24,576 rows); at config 3 (49,152
+    # rows, skewed groups of ~9.8k and ~2.2k rows) the first and last 96 rows
+    # of each group -- its first tiles and its ragged last M-tile -- and 192
+    # random rows between them.  Each group's rows meet the bar as a whole and
+    # row by row.
     for g in range(G):
         r0, r1 = h_off[g], h_off[g + 1]
         if r1 == r0:
             continue
         sel = np.arange(r0, r1)
+        if cfg == 3 and len(sel) > 384:
+            mid = rng.choice(sel[96:-96], 192, replace=False)
+            sel = np.unique(np.concatenate([sel[:96], sel[-96:], mid]))
         j = order[g]
         xr = inp.x[h_rt[sel]]
         ga = orc.matmul_2d(xr, inp.gate[j])
         ua = orc.matmul_2d(xr, inp.up[j])
         a_ref = orc.swiglu(ga, ua)
         assert rel_err(h_act[sel], a_ref) <= tol, ("act", g)
+        e_row, worst = row_rel_err(h_act[sel], a_ref)
+        assert e_row <= tol, ("act row", g, int(sel[worst]), e_row)
         # down GEMM on the GPU's own act rows isolates the second GEMM's error
         y_ref = orc.matmul_2d(h_act[sel], inp.down[j])
         assert rel_err(h_y[sel], y_ref) <= tol, ("y", g)
+        e_row, worst = row_rel_err(h_y[sel], y_ref)
+        assert e_row <= tol, ("y row", g, int(sel[worst]), e_row)
+        say(f"  group {g}: {r1 - r0} rows, {len(sel)} checked")
 
 
 # The tiled gate/up kernel writes 16 bytes per lane when the activations are
@@ -312,6 +325,10 @@ def test_moe_layer_full_against_oracle(cuda, orc, cfg):
     np.testing.assert_array_equal(stash.row_token, r["row_token"])
     assert rel_err(stash.gating_weights, r["gw"]) <= 1e-6
     assert rel_err(out, r["out"]) <= TOL[inp.dtype]
+    # The same bar on every token's row on its own.
+    e_row, worst = row_rel_err(out, r["out"])
+    say(f"  worst row {worst}: rel err {e_row:.3e} (experts {r['sel'][worst].tolist()})")
+    assert e_row <= TOL[inp.dtype], (worst, e_row)
     layer.engine.close()
 
 
@@ -332,6 +349,15 @@ def test_moe_layer_skewed_config3_full(cuda, orc):
     r = orc.moe_forward(inp)
     np.testing.assert_array_equal(stash.row_token, r["row_token"])
     assert rel_err(out, r["out"]) <= TOL["bf16"]
+    e_row, worst = row_rel_err(out, r["out"])
+    say(f"  worst row {worst}: rel err {e_row:.3e} (experts {r['sel'][worst].tolist()})")
+    assert e_row <= TOL["bf16"], (worst, e_row)
+    # Per token group: the bar on the tokens routed to each expert alone
+    # (experts 0 and 1 hold ~9.8k tokens each, the rest ~2.2k).
+    for e in range(inp.E):
+        tok = np.nonzero((rs == e).any(axis=1))[0]
+        e_g = rel_err(out[tok], r["out"][tok])
+        assert e_g <= TOL["bf16"], (e, len(tok), e_g)
     layer.engine.close()
 
 

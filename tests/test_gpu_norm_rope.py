@@ -218,3 +218,19 @@ def test_legacy_backward_launchers_run_the_reference_expert_backward(cuda, orc):
     for key in ("gate", "up", "down"):
         for j in range(E + 1):
             assert rel_err(grads[key][j], ref["d_" + key][j]) <= 1e-4, (key, j)
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, 64 << 20])
+def test_hbm_copy_exact(cuda, nbytes):
+    # prichs_hbm_copy (the HBM yardstick of the memory-bound stages): every
+    # byte copied, nothing past the end touched (whole blocks and a ragged
+    # last block).
+    print("case: hbm_copy", nbytes, flush=True)
+    g = torch.Generator(device="cuda").manual_seed(nbytes % 1000)
+    src = torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device="cuda",
+                        generator=g)
+    dst = torch.full((nbytes // 4 + 64,), 0x5A5A5A5A, dtype=torch.int32, device="cuda")
+    ops.hbm_copy(src, dst[:nbytes // 4])
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes // 4], src)
+    assert bool((dst[nbytes // 4:] == 0x5A5A5A5A).all())

@@ -445,3 +445,19 @@ def test_update_aux_free_bias(orc):
     bal = orc.update_aux_free_bias(bias, np.full(E, k * T // E), k, T, gamma)
     np.testing.assert_array_equal(bal, bias)
     np.testing.assert_array_equal(orc.update_aux_free_bias(bias, counts, k, 0, gamma), bias)
+
+
+def test_row_bar_catches_an_error_confined_to_a_small_row():
+    # The per-row bar of the GPU tests: a 50% error planted in one row whose
+    # magnitude is 1e-3 of the others passes the normwise bar but not the
+    # per-row one, which also names the row.
+    from conftest import rel_err, row_rel_err
+
+    ref = np.random.default_rng(0).standard_normal((64, 32)).astype(np.float32)
+    ref[17] *= 1e-3
+    got = ref.copy()
+    got[17] *= 1.5
+    assert rel_err(got, ref) <= 2e-2
+    err, row = row_rel_err(got, ref)
+    assert row == 17 and abs(err - 0.5) < 1e-6
+    assert row_rel_err(ref, ref) == (0.0, 0)

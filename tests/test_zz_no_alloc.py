@@ -83,3 +83,45 @@ def test_noalloc_rejects_a_batch_past_the_scratch(cuda):
     assert rc == L.PRICHS_ERR_CAPACITY and "scratch" in L.last_error()
     torch.cuda.synchronize()
     assert not out.any()
+
+
+@pytest.mark.parametrize("cfg,T", [(2, 512), (4, 32)], ids=["config2_dims_512", "decode_32"])
+def test_noalloc_forward_replays_in_a_hip_graph(cuda, orc, cfg, T):
+    # The documented use: a caller under HIP graph capture.  One eager call
+    # first (the per-device scratch lookup and the kernels' one-time launch
+    # attributes happen outside the capture), then the call captured into a
+    # graph, then three replays, each after an eager call with fewer tokens
+    # that overwrites the scratch and a host synchronisation.  Every replay is
+    # bit-identical to the engine forward and within 2e-2 of the oracle.
+    from conftest import rel_err
+
+    inp = synth.config_inputs(cfg, T=T)
+    say(f"case: noalloc graph capture cfg {cfg} T {T} ({inp.dtype})")
+    eng = moe.MoEEngine(inp.d, inp.f, inp.E, inp.k, inp.n_shared, inp.dtype, max_tokens=T)
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    gu, dn = packed_weights(inp)
+    wr, rb = dev(inp.w_router), dev(inp.router_bias)
+    x = dev(inp.x, inp.dtype)
+    ref = eng.forward(x).clone()
+    want = orc.moe_forward(inp)["out"]
+    out = torch.empty_like(ref)
+    assert noalloc_forward(inp, x, wr, rb, gu, dn, out) == L.PRICHS_OK, L.last_error()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = noalloc_forward(inp, x, wr, rb, gu, dn, out)
+    assert rc == L.PRICHS_OK, L.last_error()
+    xs = x[: max(1, T // 3)].contiguous()
+    other = torch.empty((xs.shape[0], inp.d), dtype=ref.dtype, device="cuda")
+    for rep in range(3):
+        out.fill_(float("nan"))
+        assert noalloc_forward(inp, xs, wr, rb, gu, dn, other) == L.PRICHS_OK, L.last_error()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), rep
+        err = rel_err(out.float().cpu().numpy(), want)
+        assert err <= 2e-2, (rep, err)
+        say(f"  replay {rep}: bit-identical to the engine, rel err {err:.2e} against the oracle")
+    del graph
+    eng.close()
