@@ -450,8 +450,12 @@ int prichs_moe_engine_stash(const prichs_moe_engine *eng,
  * [0] router, [1] permute, [2] gate/up GEMM, [3] down GEMM, [4] combine,
  * [5] whole forward; *n_forwards (may be NULL) gets the number averaged.
  * It then re-arms recording for another n forwards.  When one router
- * workgroup covers the batch (decode-sized T), the router also writes the
- * permutation and [1] times only the gap between two events.  Each event
+ * workgroup covers the batch (decode-sized T, bf16, one shared expert, 5-8
+ * routed experts, d % 128 == 0, no backward enabled), the router and the
+ * permutation run inside the gate/up launch, which covers every token of
+ * every expert, and the down GEMM gathers the routed rows: [0] and [1] then
+ * time only event gaps and [2] covers the router too.  The stash's rows and
+ * every output are bit-identical either way.  Each event
  * costs a few microseconds on the stream, so time throughput with timing
  * off. */
 #define PRICHS_NUM_STAGES 6

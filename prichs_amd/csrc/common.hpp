@@ -123,6 +123,29 @@ int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t 
                       size_t max_group_rows, const void *w_packed, size_t d, size_t f, int dtype,
                       void *y, void *stream);
 
+// Decode path (gemm.hip).  When one router workgroup covers the batch, every
+// expert's weights are streamed whatever the routing, so one launch runs the
+// router (which also writes the permutation) in its first workgroup while the
+// others run the gate/up GEMM densely over all T tokens of every group:
+// act_dense [(E + 1) T][f], group g's rows g T .. g T + T - 1 (routed experts,
+// then the shared expert).  The router also writes dense_row [T k + T], the
+// dense row of every row-space row.  decode_down then runs the down GEMM over
+// the row space only, its A rows gathered as act_dense[dense_row[r]], and
+// copies those rows to act (the row-space activations) as it stages them.
+// Every row's values are bit-identical to the routed path's.
+bool decode_dense_applies(size_t T, size_t d, size_t f, size_t E, size_t k, size_t n_shared,
+                          int dtype, const void *x, const float *w_router);
+int decode_gate_up_router(const void *x, size_t T, size_t d, size_t f, size_t E, size_t k,
+                          const float *w_router, const float *w_lds, const float *router_bias,
+                          const float *concept_bias, size_t n_concept, float *logits,
+                          int32_t *topk_idx, float *topk_w, int32_t *block_counts,
+                          int32_t *offsets, int32_t *row_token, float *row_weight,
+                          int32_t *token_row, int32_t *dense_row, const void *w_gate_up,
+                          void *act_dense, void *stream);
+int decode_down(const void *act_dense, const int32_t *dense_row, const int32_t *offsets, size_t T,
+                size_t d, size_t f, size_t E, size_t k, const void *w_down, void *y, void *act,
+                void *stream);
+
 // Plain grouped GEMM over the engine's row space (no SwiGLU):
 // C[r][n] = sum_k A[a_rows ? a_rows[r] : r][k] * B_g[n][k] for the rows r of
 // each group g, B_g the g-th packed [Np, K] weight (prichs_pack_weight layout,

@@ -46,6 +46,11 @@ struct prichs_moe_engine {
   int32_t *token_row = nullptr;
   void *act = nullptr;
   void *y = nullptr;
+  // Decode path (decode_gate_up_router / decode_down): the dense gate/up
+  // activations [(E + 1) dense_tokens][f] and the dense row of every row.
+  size_t dense_tokens = 0;
+  void *act_dense = nullptr;
+  int32_t *dense_row = nullptr;
   size_t gu_elems = 0, dn_elems = 0;  // packed elements per expert
   size_t last_T = 0;
   bool stash_valid = false;  // a forward's intermediates await a backward
@@ -167,6 +172,10 @@ extern "C" int prichs_moe_engine_create(size_t d, size_t f, size_t E, size_t k, 
   const size_t o_tr = c.take(sizeof(int32_t) * Tm * k);
   const size_t o_act = c.take(es * rows * f);
   const size_t o_y = c.take(es * rows * d);
+  // Decode buffers for batches one router workgroup covers (32 tokens).
+  const size_t Td = (dtype == PRICHS_DTYPE_BF16 && n_shared == 1) ? std::min<size_t>(Tm, 32) : 0;
+  const size_t o_actd = c.take(es * (E + 1) * Td * f + 1);
+  const size_t o_drow = c.take(sizeof(int32_t) * (Td * k + Td) + 1);
 
   int rc = PRICHS_OK;
   if (hipGetDevice(&eng->device) != hipSuccess) {
@@ -198,6 +207,9 @@ extern "C" int prichs_moe_engine_create(size_t d, size_t f, size_t E, size_t k, 
   eng->row_weight = reinterpret_cast<float *>(base + o_rw);
   eng->token_row = reinterpret_cast<int32_t *>(base + o_tr);
   eng->act = base + o_act;
+  eng->dense_tokens = Td;
+  eng->act_dense = Td > 0 ? base + o_actd : nullptr;
+  eng->dense_row = Td > 0 ? reinterpret_cast<int32_t *>(base + o_drow) : nullptr;
   eng->y = base + o_y;
   *out = eng;
   return PRICHS_OK;
@@ -381,6 +393,9 @@ extern "C" int prichs_moe_engine_get_router_bias(const prichs_moe_engine *eng, f
   return PRICHS_OK;
 }
 
+static int moe_finish(prichs_moe_engine *eng, size_t T, void *out, int out_dtype, void *stream,
+                      const float *residual, void *moe_out, bool tm, hipEvent_t *ev);
+
 // The forward; with residual != nullptr the combine writes the layer output
 // to moe_out (bf16) and residual + that output to out (the block's final
 // residual add, in the same kernel).
@@ -411,6 +426,27 @@ static int moe_forward_impl(prichs_moe_engine *eng, const void *x, size_t T,
   const size_t rows = T * eng->k + eng->S * T;
   int rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[0], s), "engine_forward: event");
+  if (!eng->bwd && T <= eng->dense_tokens &&
+      decode_dense_applies(T, eng->d, eng->f, eng->E, eng->k, eng->S, eng->dtype, x,
+                           eng->w_router)) {
+    // Decode: the router (and the permutation) runs in the first workgroup
+    // of the gate/up launch, which covers every token of every expert; the
+    // down GEMM gathers the routed rows.  Events [0]-[2] bracket no work.
+    if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[1], s), "engine_forward: event");
+    if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[2], s), "engine_forward: event");
+    rc = decode_gate_up_router(x, T, eng->d, eng->f, eng->E, eng->k, eng->w_router,
+                               eng->w_router_lds, eng->router_bias, concept_bias, n_concept,
+                               eng->logits, eng->topk_idx, eng->topk_w, eng->block_counts,
+                               eng->offsets, eng->row_token, eng->row_weight, eng->token_row,
+                               eng->dense_row, eng->w_gate_up, eng->act_dense, stream);
+    if (rc) return rc;
+    if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[3], s), "engine_forward: event");
+    rc = decode_down(eng->act_dense, eng->dense_row, eng->offsets, T, eng->d, eng->f, eng->E,
+                     eng->k, eng->w_down, eng->y, eng->act, stream);
+    if (rc) return rc;
+    if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[4], s), "engine_forward: event");
+    return moe_finish(eng, T, out, out_dtype, stream, residual, moe_out, tm, ev);
+  }
   if (prichs_router_num_blocks(T, eng->E) == 1) {
     // Decode-sized batch: the router's one workgroup also writes the
     // permutation (the permute stage then times as zero).
@@ -442,6 +478,15 @@ static int moe_forward_impl(prichs_moe_engine *eng, const void *x, size_t T,
                          eng->dtype, eng->y, stream);
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[4], s), "engine_forward: event");
+  return moe_finish(eng, T, out, out_dtype, stream, residual, moe_out, tm, ev);
+}
+
+// The combine (with the block's residual add when residual is set) and the
+// forward's bookkeeping.
+static int moe_finish(prichs_moe_engine *eng, size_t T, void *out, int out_dtype, void *stream,
+                      const float *residual, void *moe_out, bool tm, hipEvent_t *ev) {
+  hipStream_t s = as_stream(stream);
+  int rc;
   if (residual != nullptr && eng->dtype == PRICHS_DTYPE_BF16) {
     rc = moe_combine_residual(eng->y, eng->topk_idx, eng->topk_w, eng->token_row, T, eng->d,
                               eng->k, (int)eng->S, moe_out, residual, out, out_dtype, stream);

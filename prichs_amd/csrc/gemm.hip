@@ -33,6 +33,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "router_quad.hpp"
 
 namespace prichs {
 namespace {
@@ -847,11 +848,38 @@ __device__ inline void load_w(const bf16_t *__restrict__ wp, int s0, bf16x8 (&w)
 // load its [32 rows][32 U] tile once (16 bytes per load) into one of two
 // buffers, and every N-wave reads its MFMA fragments from there.
 // (K / SK) % (32 * U) == 0.
+// One skinny launch.  Group g owns rows [offsets[g], offsets[g+1]) of the
+// row space, or with dense_T > 0 rows [g dense_T, (g+1) dense_T) whose A rows
+// are 0 .. dense_T - 1 (every token of every group; offsets is not read).  A
+// row r of the row space is A[a_rows[r]] when a_rows is set.  a_copy (may be
+// null): the workgroups of N-slab 0 also write the A rows they stage to
+// a_copy [row][lda] at their row-space rows.
+struct SkinnyArgs {
+  const bf16_t *A;
+  const int32_t *a_rows;
+  int lda;
+  const bf16_t *B;
+  long long b_stride;
+  int K;
+  bf16_t *C;
+  int ldc, n_store;
+  const int32_t *offsets;
+  int dense_T;
+  bf16_t *P;
+  int ldp;
+  bf16_t *a_copy;
+};
+
+// The workgroup (N-slab bx, group g, M-tile bz) of a skinny launch.
 template <bool GATEUP, int U, int SK>
-__global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
-    const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
-    const bf16_t *__restrict__ B, long long b_stride, int K, bf16_t *__restrict__ C, int ldc,
-    int n_store, const int32_t *__restrict__ offsets, bf16_t *__restrict__ P, int ldp) {
+__device__ __forceinline__ void skinny_body(const SkinnyArgs &sa, int bx, int g, int bz) {
+  const bf16_t *__restrict__ A = sa.A;
+  const int32_t *__restrict__ a_rows = sa.a_rows;
+  const int lda = sa.lda, K = sa.K, ldc = sa.ldc, n_store = sa.n_store, ldp = sa.ldp;
+  const bf16_t *__restrict__ B = sa.B;
+  const long long b_stride = sa.b_stride;
+  bf16_t *__restrict__ C = sa.C;
+  bf16_t *__restrict__ P = sa.P;
   constexpr int kRow = 32 * U + 8;                 // LDS row (16-byte pad: conflict-free reads)
   constexpr int kSegs = BM * 4 * U;                // 16-byte segments of one chunk tile
   constexpr int kSegPerThread = kSegs / kThreads;  // U / 2
@@ -859,9 +887,10 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
   __shared__ __attribute__((aligned(16))) bf16_t a_s[SK][2][BM * kRow];
   __shared__ f32x4 red_s[SK > 1 ? SK - 1 : 1][4][2][64];  // [slice-1][N-wave][tile][lane]
   __shared__ f32x4 gate_s[2][2][64];                      // [gate wave][tile][lane]
-  const int g = blockIdx.y;
-  const int r1 = offsets[g + 1];
-  const int m0 = offsets[g] + (int)blockIdx.z * BM;
+  const bool dense = sa.dense_T > 0;
+  const int g0 = dense ? g * sa.dense_T : sa.offsets[g];
+  const int r1 = dense ? g0 + sa.dense_T : sa.offsets[g + 1];
+  const int m0 = g0 + bz * BM;
   if (m0 >= r1) return;  // uniform: this M-tile of the group is empty
   const int mrows = min(BM, r1 - m0);
   const bool two = mrows > 16;
@@ -871,7 +900,7 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
   const int Ks = K / SK;
   const int nc = Ks / (32 * U);
   // Fragment (16-row block nb, K-step ks * Ks / 32 + s) of the packed weights.
-  const int nb = blockIdx.x * (BN / 16) + wn;
+  const int nb = bx * (BN / 16) + wn;
   const bf16_t *wp =
       B + g * b_stride + ((long long)nb * (K / 32) + ks * (Ks / 32)) * 512 + lane * 8;
 
@@ -880,14 +909,21 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
   // row (their outputs are never stored).
   const bf16_t *asrc[kSegPerThread];
   int adst[kSegPerThread];
+  bf16_t *acpy[kSegPerThread];  // row-space copy of the staged rows (N-slab 0 only)
 #pragma unroll
   for (int j = 0; j < kSegPerThread; ++j) {
     const int i = st + kThreads * j;
     const int r = i / (4 * U), sc = i % (4 * U);
     int src = min(m0 + r, r1 - 1);
-    if (a_rows != nullptr) src = a_rows[src];
+    if (a_rows != nullptr)
+      src = a_rows[src];
+    else if (dense)
+      src -= g0;
     asrc[j] = A + (long long)src * lda + ks * Ks + sc * 8;
     adst[j] = r * kRow + sc * 8;
+    acpy[j] = (sa.a_copy != nullptr && bx == 0 && m0 + r < r1)
+                  ? sa.a_copy + (long long)(m0 + r) * lda + ks * Ks + sc * 8
+                  : nullptr;
   }
   bf16x8 areg[kSegPerThread];
   auto load_a = [&](int c) {
@@ -895,10 +931,13 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
     for (int j = 0; j < kSegPerThread; ++j)
       areg[j] = *reinterpret_cast<const bf16x8 *>(asrc[j] + c * 32 * U);
   };
-  auto store_a = [&](int buf) {
+  // Chunk c's staged A values go to LDS buffer buf (and to the copy).
+  auto store_a = [&](int buf, int c) {
 #pragma unroll
-    for (int j = 0; j < kSegPerThread; ++j)
+    for (int j = 0; j < kSegPerThread; ++j) {
       *reinterpret_cast<bf16x8 *>(&a_s[ks][buf][adst[j]]) = areg[j];
+      if (acpy[j] != nullptr) *reinterpret_cast<bf16x8 *>(acpy[j] + c * 32 * U) = areg[j];
+    }
   };
   const int rd = (lane & 15) * kRow + 8 * (lane >> 4);  // fragment read offset, tile 0
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -918,19 +957,19 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
   bf16x8 w0[U], w1[U];
   load_a(0);
   load_w<U>(wp, 0, w0);
-  store_a(0);
+  store_a(0, 0);
   load_a(min(1, nc - 1));
   load_w<U>(wp, min(1, nc - 1) * U, w1);
   __syncthreads();
   for (int c = 0; c < nc; c += 2) {
     mma(w0, 0);
-    if (c + 1 < nc) store_a(1);
+    if (c + 1 < nc) store_a(1, c + 1);
     load_a(min(c + 2, nc - 1));
     load_w<U>(wp, min(c + 2, nc - 1) * U, w0);
     __syncthreads();
     if (c + 1 < nc) {
       mma(w1, 1);
-      if (c + 2 < nc) store_a(0);
+      if (c + 2 < nc) store_a(0, c + 2);
     }
     load_a(min(c + 3, nc - 1));
     load_w<U>(wp, min(c + 3, nc - 1) * U, w1);
@@ -957,7 +996,7 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
   if (GATEUP) {
     if (P != nullptr && ks == 0) {
       // Training forward: this wave's pre-activations (packed rows 16 wn..).
-      const int pcol = blockIdx.x * BN + wn * 16 + cq;
+      const int pcol = bx * BN + wn * 16 + cq;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int m = mr + 16 * t;
@@ -974,7 +1013,7 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
     }
     __syncthreads();
     if (ks == 0 && wn >= 2) {
-      const int col = blockIdx.x * (BN / 2) + (wn - 2) * 16 + cq;
+      const int col = bx * (BN / 2) + (wn - 2) * 16 + cq;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int m = mr + 16 * t;
@@ -990,7 +1029,7 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
       }
     }
   } else if (ks == 0) {
-    const int col = blockIdx.x * BN + wn * 16 + cq;
+    const int col = bx * BN + wn * 16 + cq;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int m = mr + 16 * t;
@@ -1001,6 +1040,44 @@ __global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(
       }
     }
   }
+}
+template <bool GATEUP, int U, int SK>
+__global__ __launch_bounds__(kThreads * SK) void skinny_gemm_kernel(SkinnyArgs sa) {
+  skinny_body<GATEUP, U, SK>(sa, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z);
+}
+
+// The router workgroup's arguments in the decode launch (router_quad_body).
+struct RouterArgs {
+  const bf16_t *x;
+  const float *w, *bias, *concept;
+  int n_concept, T, d, E, k;
+  float *logits;
+  int32_t *topk_idx;
+  float *topk_w;
+  int32_t *block_counts;
+  rq::FusedPerm perm;
+  const float *w_lds;
+};
+
+// Decode launch: workgroup 0 routes the batch (one router workgroup covers
+// it) and writes its permutation; workgroups 1.. are the dense gate/up GEMM
+// (N-slab, group, M-tile) = the workgroups of skinny_gemm_kernel<true, U, 1>
+// over nx x ny x .. blocks, dispatched after the router's so it starts first.
+template <int U>
+__global__ __launch_bounds__(kThreads) void decode_gate_up_router_kernel(SkinnyArgs sa,
+                                                                        RouterArgs ra, int nx,
+                                                                        int ny) {
+  static_assert(kThreads == rq::kRouterThreads, "one workgroup size for both roles");
+  extern __shared__ __attribute__((aligned(16))) float router_wt_s[];  // W^T [8][d + 4]
+  const int b = (int)blockIdx.x;
+  if (b == 0) {
+    rq::router_quad_body<bf16_t>(ra.x, ra.w, ra.bias, ra.concept, ra.n_concept, ra.T, ra.d, ra.E,
+                                 ra.k, ra.logits, ra.topk_idx, ra.topk_w, ra.block_counts,
+                                 ra.perm, ra.w_lds, 0, router_wt_s);
+    return;
+  }
+  const int i = b - 1;
+  skinny_body<true, U, 1>(sa, i % nx, (i / nx) % ny, i / (nx * ny));
 }
 }  // namespace skinny
 
@@ -1160,13 +1237,15 @@ bool dense_prefers_wide(size_t M, size_t Np, int cus) {
 template <bool GATEUP, int U, int SK>
 int launch_skinny_u(const void *A, const int32_t *a_rows, int lda, const void *B,
                     long long b_stride, int Np, int K, void *Cp, int ldc, int n_store,
-                    const int32_t *offsets, int G, int mtiles, hipStream_t s, void *pre) {
+                    const int32_t *offsets, int G, int mtiles, hipStream_t s, void *pre,
+                    void *a_copy = nullptr) {
   static_assert(Bf16::kIl == skinny::BN / 2, "a skinny slab is one [gate | up] block");
+  const skinny::SkinnyArgs sa{static_cast<const bf16_t *>(A), a_rows, lda,
+                              static_cast<const bf16_t *>(B), b_stride, K,
+                              static_cast<bf16_t *>(Cp), ldc, n_store, offsets, 0,
+                              static_cast<bf16_t *>(pre), Np, static_cast<bf16_t *>(a_copy)};
   hipLaunchKernelGGL((skinny::skinny_gemm_kernel<GATEUP, U, SK>),
-                     dim3(Np / skinny::BN, G, mtiles), dim3(skinny::kThreads * SK), 0, s,
-                     static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
-                     b_stride, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets,
-                     static_cast<bf16_t *>(pre), Np);
+                     dim3(Np / skinny::BN, G, mtiles), dim3(skinny::kThreads * SK), 0, s, sa);
   PRICHS_LAUNCH_CHECK("skinny grouped gemm launch");
   return PRICHS_OK;
 }
@@ -1186,7 +1265,7 @@ int launch_skinny_u(const void *A, const int32_t *a_rows, int lda, const void *B
 template <bool GATEUP>
 int launch_skinny(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                   int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
-                  size_t max_group_rows, hipStream_t s, void *pre) {
+                  size_t max_group_rows, hipStream_t s, void *pre, void *a_copy = nullptr) {
   const int mtiles = (int)std::max<size_t>(1, (max_group_rows + skinny::BM - 1) / skinny::BM);
   int sk = PRICHS_SKINNY_SK;
   while (sk > 1 && K % (sk * 64) != 0) sk /= 2;
@@ -1196,7 +1275,7 @@ int launch_skinny(const void *A, const int32_t *a_rows, int lda, const void *B, 
 #define PRICHS_SKINNY(U_, SK_)                                                                   \
   if (u == U_ && sk == SK_)                                                                     \
   return launch_skinny_u<GATEUP, U_, SK_>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store, \
-                                          offsets, G, mtiles, s, pre)
+                                          offsets, G, mtiles, s, pre, a_copy)
   PRICHS_SKINNY(2, 1);
   PRICHS_SKINNY(4, 1);
   PRICHS_SKINNY(8, 1);
@@ -1318,6 +1397,76 @@ int grouped_down_rows(const void *act, const int32_t *offsets, size_t G, size_t 
                         (int)f, y, (int)d, (int)d, offsets, (int)G, 0, max_rows, dtype,
                         as_stream(stream), std::min(max_rows, max_group_rows));
 }
+bool decode_dense_applies(size_t T, size_t d, size_t f, size_t E, size_t k, size_t n_shared,
+                          int dtype, const void *x, const float *w_router) {
+  constexpr size_t kTokens = rq::kRouterThreads / 8;  // one quad-router workgroup
+  return dtype == PRICHS_DTYPE_BF16 && n_shared == 1 && E > 4 && E <= 8 && k >= 1 && k <= E &&
+         T >= 1 && T <= kTokens && d % 128 == 0 && (size_t)8 * (d + 4) * 4 <= 150 * 1024 &&
+         f % kBf16KMultiple == 0 && d <= (1u << 20) && f <= (1u << 20) &&
+         reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w_router) % 16 == 0;
+}
+
+int decode_gate_up_router(const void *x, size_t T, size_t d, size_t f, size_t E, size_t k,
+                          const float *w_router, const float *w_lds, const float *router_bias,
+                          const float *concept_bias, size_t n_concept, float *logits,
+                          int32_t *topk_idx, float *topk_w, int32_t *block_counts,
+                          int32_t *offsets, int32_t *row_token, float *row_weight,
+                          int32_t *token_row, int32_t *dense_row, const void *w_gate_up,
+                          void *act_dense, void *stream) {
+  PRICHS_REQUIRE(decode_dense_applies(T, d, f, E, k, 1, PRICHS_DTYPE_BF16, x, w_router),
+                 "decode_gate_up_router: T=%zu, d=%zu, f=%zu, E=%zu, k=%zu not a decode shape",
+                 T, d, f, E, k);
+  PRICHS_REQUIRE(x && w_router && router_bias && logits && topk_idx && topk_w && block_counts &&
+                     offsets && row_token && row_weight && token_row && dense_row && w_gate_up &&
+                     act_dense,
+                 "decode_gate_up_router: null pointer argument");
+  PRICHS_REQUIRE(concept_bias != nullptr || n_concept == 0,
+                 "decode_gate_up_router: concept_bias is NULL but n_concept=%zu", n_concept);
+  constexpr int U = 4;
+  const size_t np = gate_up_np(f, PRICHS_DTYPE_BF16);
+  const int G = (int)E + 1;
+  const int nx = (int)(np / skinny::BN);
+  const int mtiles = (int)((T + skinny::BM - 1) / skinny::BM);
+  const size_t lds = (size_t)8 * (d + 4) * sizeof(float);
+  static int attr_bytes = 0;
+  if ((int)lds > attr_bytes) {
+    PRICHS_HIP_TRY(hipFuncSetAttribute(
+                       reinterpret_cast<const void *>(&skinny::decode_gate_up_router_kernel<U>),
+                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                   "decode_gate_up_router: set LDS size");
+    attr_bytes = (int)lds;
+  }
+  const skinny::SkinnyArgs sa{static_cast<const bf16_t *>(x), nullptr, (int)d,
+                              static_cast<const bf16_t *>(w_gate_up), (long long)(np * d), (int)d,
+                              static_cast<bf16_t *>(act_dense), (int)f, (int)f, nullptr, (int)T,
+                              nullptr, (int)np, nullptr};
+  const int nc = (int)(n_concept < E ? n_concept : E);
+  const skinny::RouterArgs ra{static_cast<const bf16_t *>(x), w_router, router_bias, concept_bias,
+                              nc, (int)T, (int)d, (int)E, (int)k, logits, topk_idx, topk_w,
+                              block_counts,
+                              rq::FusedPerm{offsets, row_token, row_weight, token_row, dense_row},
+                              w_lds};
+  const unsigned grid = 1u + (unsigned)(nx * G * mtiles);
+  hipLaunchKernelGGL((skinny::decode_gate_up_router_kernel<U>), dim3(grid), dim3(skinny::kThreads),
+                     lds, as_stream(stream), sa, ra, nx, G);
+  PRICHS_LAUNCH_CHECK("decode gate/up + router launch");
+  return PRICHS_OK;
+}
+
+int decode_down(const void *act_dense, const int32_t *dense_row, const int32_t *offsets, size_t T,
+                size_t d, size_t f, size_t E, size_t k, const void *w_down, void *y, void *act,
+                void *stream) {
+  if (int rc = check_gemm_shape(d, f, PRICHS_DTYPE_BF16, "decode_down")) return rc;
+  PRICHS_REQUIRE(act_dense && dense_row && offsets && w_down && y && act,
+                 "decode_down: null pointer argument");
+  PRICHS_REQUIRE(T >= 1 && T <= (size_t)skinny::kSkinnyRows && k <= E,
+                 "decode_down: T=%zu, k=%zu, E=%zu not a decode shape", T, k, E);
+  const size_t np = roundup(d, kPadRowsDown);
+  return launch_skinny<false>(act_dense, dense_row, (int)f, w_down, (long long)(np * f), (int)np,
+                              (int)f, y, (int)d, (int)d, offsets, (int)E + 1, T,
+                              as_stream(stream), nullptr, act);
+}
+
 int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const void *B,
                       size_t b_group_stride, size_t Np, size_t K, void *C, size_t ldc,
                       size_t n_store, const int32_t *offsets, size_t G, size_t max_rows,

@@ -311,6 +311,51 @@ def test_decode_fused_permutation_other_experts(cuda, orc, E, k):
     layer.engine.close()
 
 
+# ------------------------------------------------------------ decode path --
+@pytest.mark.parametrize("T,E,k,concept", [(32, 8, 2, False), (17, 8, 2, True), (1, 8, 2, False),
+                                           (5, 6, 3, False), (32, 5, 1, True)],
+                         ids=["T32", "T17_concept", "T1", "T5_E6_k3", "T32_E5_k1_concept"])
+def test_decode_path_bit_identical_to_routed_path(cuda, orc, T, E, k, concept):
+    # When one router workgroup covers the batch, the engine runs the router
+    # (and the permutation) inside a gate/up launch that covers every token
+    # of every expert, and the down GEMM gathers the routed rows.  An engine
+    # with the backward enabled keeps the routed stages (router, permutation,
+    # routed gate/up, down).  Routing, the permutation, the stash's act and y
+    # rows and the output are the same bits on both; the output is within
+    # 2e-2 of the oracle.
+    d, f = (1536, 1280) if E == 8 and k == 2 else (256, 128)
+    inp = synth.make_moe_inputs(T=T, d=d, f=f, E=E, k=k, dtype="bf16", seed=100 + T + E,
+                                name=f"decode-T{T}-E{E}-k{k}")
+    say("decode vs routed", T, E, k, concept)
+    cb = None
+    if concept:
+        cb_np = np.zeros(E, np.float32)
+        cb_np[E - 1] = 0.5
+        cb = dev(cb_np)
+    x = dev(inp.x, "bf16")
+    outs, stashes = [], []
+    for backward in (False, True):
+        eng = moe.MoEEngine(d, f, E, k, 1, "bf16", max_tokens=max(T, 32))
+        if backward:
+            eng.enable_backward()
+        eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+        outs.append(eng.forward(x, concept_bias=cb).clone())
+        stashes.append(eng.stash())
+        eng.close()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    for name in ("router_logits", "selected_experts", "gating_weights", "offsets", "row_token",
+                 "row_weight", "token_row", "act", "y"):
+        a, b = stashes[0][name], stashes[1][name]
+        a, b = (a.view(torch.int16), b.view(torch.int16)) if a.dtype == torch.bfloat16 else (a, b)
+        assert torch.equal(a, b), name
+    r = orc.moe_forward(inp, concept_bias=None if cb is None else host(cb))
+    np.testing.assert_array_equal(host(stashes[0]["selected_experts"]), r["sel"])
+    np.testing.assert_array_equal(host(stashes[0]["row_token"])[:T * k], r["row_token"])
+    np.testing.assert_array_equal(host(stashes[0]["offsets"])[:E + 1], r["offsets"])
+    e_row, worst = row_rel_err(host(outs[0].float()), r["out"])
+    assert e_row <= TOL["bf16"], (worst, e_row)
+
+
 # ------------------------------------------------------------- full layer --
 @pytest.mark.parametrize("cfg", [1, 2, 4])
 def test_moe_layer_full_against_oracle(cuda, orc, cfg):
