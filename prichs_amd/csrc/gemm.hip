@@ -253,9 +253,19 @@ template <int BM_, int BN_, int WGM_, int WGN_, int S_ = PRICHS_BF16_STAGES> str
   static constexpr int MI = WM / 16, NJ = WN / 16;
   static constexpr int kIl = 32;             // gate/up interleave: packed blocks [kIl gate | kIl up]
   static constexpr int kRowsPerInst = 16;    // one wave instruction fills 1 KiB = 16 rows of 64 B
-  static constexpr int kInstA = BM / kRowsPerInst / kWaves;
-  static constexpr int kInstB = BN / kRowsPerInst / kWaves;
-  static constexpr int kInstPerStage = kInstA + kInstB;
+  // DMA instructions of one stage: one per 16-row block of A and of B.  When
+  // a count is a multiple of the waves, wave w moves blocks w kInst ..
+  // (w + 1) kInst - 1; otherwise blocks are dealt round-robin (block i kWaves
+  // + w), so some waves issue one more.  kInstA / kInstB are the per-wave
+  // maxima; kInstPerStage, which sets the waits, is the per-wave MINIMUM:
+  // vector-memory operations complete in issue order, so allowing only that
+  // many of the newest instructions per stage in flight waits for at least
+  // as much as a wave needs.
+  static constexpr int kBlkA = BM / kRowsPerInst, kBlkB = BN / kRowsPerInst;
+  static constexpr bool kEvenA = kBlkA % kWaves == 0, kEvenB = kBlkB % kWaves == 0;
+  static constexpr int kInstA = (kBlkA + kWaves - 1) / kWaves;
+  static constexpr int kInstB = (kBlkB + kWaves - 1) / kWaves;
+  static constexpr int kInstPerStage = kBlkA / kWaves + kBlkB / kWaves;
   static constexpr int kStageElems = (BM + BN) * BK;
   static constexpr size_t kRingBytes = (size_t)kStages * kStageElems * sizeof(bf16_t);
   // Epilogue staging of a finished tile: [BM][BN + 8] bf16 (16-byte row pad)
@@ -264,9 +274,10 @@ template <int BM_, int BN_, int WGM_, int WGN_, int S_ = PRICHS_BF16_STAGES> str
   static constexpr size_t kStgBytes = (size_t)BM * kStgStride * sizeof(bf16_t);
   static constexpr size_t kLdsBytes = kRingBytes > kStgBytes ? kRingBytes : kStgBytes;
   static_assert(MI % 2 == 0 && WN % 16 == 0, "two A halves and whole fragments per wave");
-  static_assert(kInstA * kRowsPerInst * kWaves == BM && kInstB * kRowsPerInst * kWaves == BN,
+  static_assert(kBlkA * kRowsPerInst == BM && kBlkB * kRowsPerInst == BN,
                 "the DMA instructions of one stage cover the A and B tiles exactly");
-  static_assert(kStages >= 3 && (kStages - 1) * kInstPerStage <= 63, "vmcnt immediates");
+  static_assert(kInstPerStage >= 1, "every wave issues DMA in every stage");
+  static_assert(kStages >= 3 && (kStages - 1) * (kInstA + kInstB) <= 63, "vmcnt immediates");
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget of a gfx950 CU");
 };
 // gate/up: 256x256 tiles; down: PRICHS_DOWN_BM x 256 tiles (smaller M tiles
@@ -287,6 +298,12 @@ static_assert(Bf16::BN % Bf16Down::BN == 0,
 // empty (8192 x 1536 outputs: 256 such tiles against 192).  Each output
 // element is the same MFMA chain over K either way, so the bits are the same.
 using Bf16Wide = Bf16Cfg<128, 384, 2, 4>;
+// ... and launches whose padded N is a multiple of 288 may use 256 x 288
+// tiles (8 waves of 64 x 144; 18 B blocks per stage dealt unevenly): the
+// block's q/k/v projection (8192 x 2304) is then exactly 256 tiles, one
+// round of the CUs, where 256 x 256 tiles make 1.125 rounds and 128 x 384
+// tiles 1.5.
+using Bf16Tall = Bf16Cfg<256, 288, 4, 2>;
 
 // C[m, n] = sum_k A[row(m), k] * B[n, k] for the rows of each group, with
 // B = packed weights [Np, K] of group g.  The MFMA takes the weight fragment
@@ -342,11 +359,17 @@ __device__ __forceinline__ void bf16_tile(
   // A offsets are 64-bit (gathered rows: src * lda can pass 2^32 elements for
   // a large row space); B offsets stay within one group's packed weights,
   // which the host bounds to 2^32 elements.
+  // 16-row block of DMA instruction i of this wave (see Bf16Cfg), and
+  // whether the wave issues that instruction at all (uneven deals).
+  auto blk_a = [&](int i) { return Cf::kEvenA ? wave * kInstA + i : i * Cf::kWaves + wave; };
+  auto blk_b = [&](int i) { return Cf::kEvenB ? wave * kInstB + i : i * Cf::kWaves + wave; };
+  auto has_a = [&](int i) { return Cf::kEvenA || blk_a(i) < Cf::kBlkA; };
+  auto has_b = [&](int i) { return Cf::kEvenB || blk_b(i) < Cf::kBlkB; };
   long long a_goff[kInstA];
   uint32_t b_goff[kInstB];
 #pragma unroll
   for (int i = 0; i < kInstA; ++i) {
-    int lr = m0 + (wave * kInstA + i) * kRowsPerInst + dma_row;
+    int lr = m0 + min(blk_a(i), Cf::kBlkA - 1) * kRowsPerInst + dma_row;
     lr = lr < mg ? lr : mg - 1;  // rows past the group repeat its last row
     const int vr = row0 + lr;
     const int src = a_rows ? a_rows[vr] : vr;
@@ -356,7 +379,7 @@ __device__ __forceinline__ void bf16_tile(
   for (int i = 0; i < kInstB; ++i) {
     // Instruction i moves fragment (16-row block nb, K-step kt): 1 KiB at
     // (nb * KT + kt) * 512 elements, lane l's 16 bytes at l * 8.
-    const int nb = n0 / kRowsPerInst + wave * kInstB + i;
+    const int nb = n0 / kRowsPerInst + min(blk_b(i), Cf::kBlkB - 1);
     b_goff[i] = (uint32_t)nb * (uint32_t)KT * 512u + (uint32_t)(lane * 8);
   }
   const bf16_t *Bg = B + (long long)g * b_group_stride;
@@ -376,16 +399,17 @@ __device__ __forceinline__ void bf16_tile(
   auto issue_one = [&](int kt_, int which) {
     bf16_t *st_ = lds + (kt_ % kStages) * kStageElems;
     if (which < kInstA) {
-      dma_16b(A + a_goff[which] + kt_ * BK, st_ + (wave * kInstA + which) * kRowsPerInst * BK);
+      if (has_a(which))
+        dma_16b(A + a_goff[which] + kt_ * BK, st_ + blk_a(which) * kRowsPerInst * BK);
     } else {
       const int i_ = which - kInstA;
-      dma_16b(Bg + b_goff[i_] + kt_ * 512,
-              st_ + BM * BK + (wave * kInstB + i_) * kRowsPerInst * BK);
+      if (has_b(i_))
+        dma_16b(Bg + b_goff[i_] + kt_ * 512, st_ + BM * BK + blk_b(i_) * kRowsPerInst * BK);
     }
   };
   auto issue_stage = [&](int kt_) {
 #pragma unroll
-    for (int w = 0; w < kInstPerStage; ++w) issue_one(kt_, w);
+    for (int w = 0; w < kInstA + kInstB; ++w) issue_one(kt_, w);
   };
 
   // Ping-pong K loop over a ring of S = kStages LDS stages, S - 1 of them in
@@ -513,7 +537,7 @@ __device__ __forceinline__ void bf16_tile(
     }
     return;  // the next tile's barrier keeps the ring refill behind these reads
   }
-  if (GATEUP) {
+  if constexpr (GATEUP) {
     // Packed rows [n0 + wn*WN, +WN) are WN / (2 kIl) [kIl gate | kIl up]
     // blocks: in block q, gate column c (16-column piece jj) pairs with up
     // column c, kIl / 16 pieces on.
@@ -993,7 +1017,7 @@ __device__ __forceinline__ void skinny_body(const SkinnyArgs &sa, int bx, int g,
 
   const int cq = 4 * (lane >> 4);
   const int mr = m0 + (lane & 15);
-  if (GATEUP) {
+  if constexpr (GATEUP) {
     if (P != nullptr && ks == 0) {
       // Training forward: this wave's pre-activations (packed rows 16 wn..).
       const int pcol = bx * BN + wn * 16 + cq;
@@ -1218,20 +1242,30 @@ double launch_tile_times(size_t tiles, size_t grid, bool split) {
 // Work of one 128 x 384 tile against a 256 x 256 one, and the rate of the
 // narrower tile (fewer MFMAs per barrier and per byte staged) against the
 // square one's, measured on MI355X in whole rounds (32768 x 1536 x 1536:
-// 124.7 us as 1024 wide tiles, 120.2 us as 768 square ones).
-constexpr double kWideWork = 0.75, kWideRate = 0.96;
+// 124.7 us as 1024 wide tiles, 120.2 us as 768 square ones).  A 256 x 288
+// tile is 1.125 square tiles of work at the square tile's rate per flop.
+constexpr double kWideWork = 0.75, kWideRate = 0.96, kTallWork = 1.125;
 
-// Whether a dense launch of M rows and Np packed columns runs faster as
-// 128 x 384 tiles than as 256 x 256 tiles with half-width tails, each on the
-// grid launch_bf16 gives it.
-bool dense_prefers_wide(size_t M, size_t Np, int cus) {
-  if (Np % Bf16Wide::BN != 0) return false;
+// Tile shape of a dense launch of M rows and Np packed columns: the one with
+// the fewest estimated square-tile-times on the grid launch_bf16 gives it
+// (0: 256 x 256 with half-width tails, 1: 128 x 384, 2: 256 x 288).
+int dense_tile_choice(size_t M, size_t Np, int cus) {
   const size_t sq = ((M + Bf16Down::BM - 1) / Bf16Down::BM) * (Np / Bf16Down::BN);
-  const size_t wd = ((M + Bf16Wide::BM - 1) / Bf16Wide::BM) * (Np / Bf16Wide::BN);
-  const double t_sq = launch_tile_times(sq, bf16_grid<Bf16Down, false>(M, 1, Np, cus), true);
-  const double t_wd = launch_tile_times(wd, bf16_grid<Bf16Wide, false>(M, 1, Np, cus), false) *
-                      kWideWork / kWideRate;
-  return t_wd < t_sq;
+  double best = launch_tile_times(sq, bf16_grid<Bf16Down, false>(M, 1, Np, cus), true);
+  int choice = 0;
+  if (Np % Bf16Wide::BN == 0) {
+    const size_t wd = ((M + Bf16Wide::BM - 1) / Bf16Wide::BM) * (Np / Bf16Wide::BN);
+    const double t = launch_tile_times(wd, bf16_grid<Bf16Wide, false>(M, 1, Np, cus), false) *
+                     kWideWork / kWideRate;
+    if (t < best) best = t, choice = 1;
+  }
+  if (Np % Bf16Tall::BN == 0) {
+    const size_t tl = ((M + Bf16Tall::BM - 1) / Bf16Tall::BM) * (Np / Bf16Tall::BN);
+    const double t =
+        launch_tile_times(tl, bf16_grid<Bf16Tall, false>(M, 1, Np, cus), false) * kTallWork;
+    if (t < best) best = t, choice = 2;
+  }
+  return choice;
 }
 
 template <bool GATEUP, int U, int SK>
@@ -1308,8 +1342,12 @@ int launch_grouped(bool gateup, const void *A, const int32_t *a_rows, int lda, c
     if (gateup)
       return launch_bf16<Bf16, true>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
                                      offsets, G, dense_m, max_rows, cus, s, pre);
-    if (offsets == nullptr && dense_prefers_wide((size_t)dense_m, (size_t)Np, cus))
+    const int shape = offsets == nullptr ? dense_tile_choice((size_t)dense_m, (size_t)Np, cus) : 0;
+    if (shape == 1)
       return launch_bf16<Bf16Wide, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
+                                          offsets, G, dense_m, max_rows, cus, s, nullptr);
+    if (shape == 2)
+      return launch_bf16<Bf16Tall, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
                                           offsets, G, dense_m, max_rows, cus, s, nullptr);
     return launch_bf16<Bf16Down, false>(A, a_rows, lda, B, b_stride, Np, K, Cp, ldc, n_store,
                                         offsets, G, dense_m, max_rows, cus, s, nullptr);

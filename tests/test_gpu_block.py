@@ -58,22 +58,32 @@ def _tile_times(tiles, grid, split):
 
 
 def _dense_cfg(M, N, cus):
-    """Mirror of the dense launcher's choice: ("wide" | "square", tail split).
-    Square = 256 x 256 tiles on a grid of min(2 (M/256 + 1) N/256, CUs) whose
-    last partial round of t tiles is split into half-width tiles when 2 t fits
-    the grid; wide = 128 x 384 tiles (N a multiple of 384) on min((M/128 + 1)
-    N/384, CUs), never split, each 0.75 of a square tile's work at 0.96 of its
-    rate.  The faster estimate wins."""
+    """Mirror of the dense launcher's choice: ("square" | "wide" | "tall", tail
+    split).  Square = 256 x 256 tiles on a grid of min(2 (M/256 + 1) N/256,
+    CUs) whose last partial round of t tiles is split into half-width tiles
+    when 2 t fits the grid; wide = 128 x 384 tiles (N a multiple of 384) on
+    min((M/128 + 1) N/384, CUs), never split, each 0.75 of a square tile's
+    work at 0.96 of its rate; tall = 256 x 288 tiles (N a multiple of 288) on
+    min((M/256 + 1) N/288, CUs), never split, 1.125 of a square tile's work.
+    The fastest estimate wins (ties keep the earlier shape)."""
     sq_tiles = -(-M // 256) * (N // 256)
     sq_grid = min(2 * (M // 256 + 1) * (N // 256), cus)
     tail = sq_tiles % sq_grid
     split = 0 < tail and 2 * tail <= sq_grid
+    best, cfg = _tile_times(sq_tiles, sq_grid, True), ("square", split)
     if N % 384 == 0:
         wd_tiles = -(-M // 128) * (N // 384)
         wd_grid = min((M // 128 + 1) * (N // 384), cus)
-        if _tile_times(wd_tiles, wd_grid, False) * 0.75 / 0.96 < _tile_times(sq_tiles, sq_grid, True):
-            return "wide", False
-    return "square", split
+        t = _tile_times(wd_tiles, wd_grid, False) * 0.75 / 0.96
+        if t < best:
+            best, cfg = t, ("wide", False)
+    if N % 288 == 0:
+        tl_tiles = -(-M // 256) * (N // 288)
+        tl_grid = min((M // 256 + 1) * (N // 288), cus)
+        t = _tile_times(tl_tiles, tl_grid, False) * 1.125
+        if t < best:
+            best, cfg = t, ("tall", False)
+    return cfg
 
 
 def test_gemm_tail_round_halves_bit_identical(cuda):
@@ -104,23 +114,28 @@ def test_gemm_tail_round_halves_bit_identical(cuda):
         assert ("square", True) in seen and ("wide", False) in seen, seen
 
 
-def test_dense_gemm_wide_tiles_qkv_shape(cuda, orc):
+def test_dense_gemm_qkv_shape_tiles(cuda, orc):
     """The block's q/k/v projection shape (8192 x 2304, K = 1536) runs as
-    128 x 384 tiles on 256 CUs: against the oracle's matmul_2d on a row slice
-    and bit-identical to the rows of a square-tile launch."""
+    256 x 288 tiles on 256 CUs (one round; 18 B blocks per stage dealt
+    unevenly over the 8 waves): against the oracle's matmul_2d on row slices,
+    and bit-identical to the rows of launches that pick 128 x 384 tiles (4096
+    rows) and 256 x 256 tiles with a half-width tail (2048 rows)."""
     M, K, N = 8192, 1536, 2304
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    say(f"dense gemm {M}x{N}x{K}: tiles {_dense_cfg(M, N, cus)[0]} on {cus} CUs")
+    cfgs = {m: _dense_cfg(m, N, cus)[0] for m in (M, 4096, 2048)}
+    say(f"dense gemm {N}x{K}: tiles by rows {cfgs} on {cus} CUs")
+    if cus == 256:
+        assert cfgs == {M: "tall", 4096: "wide", 2048: "square"}, cfgs
     rng = np.random.default_rng(5)
     a = synth.round_bf16(rng.standard_normal((M, K)))
     w = synth.round_bf16(0.05 * rng.standard_normal((K, N)))
     wp = ops.to_device_packed([ops.pack_weight(w, "bf16")], "bf16")
     c = host(ops.gemm(dev(a), wp, N))
-    ref = orc.matmul_2d(a[-256:], w)
-    assert rel_err(c[-256:], ref) <= 1e-2
-    M2 = 2048  # square tiles with a half-width tail
-    assert _dense_cfg(M2, N, cus)[0] == "square"
-    np.testing.assert_array_equal(host(ops.gemm(dev(a[:M2]), wp, N)), c[:M2])
+    for lo in (0, 4000, M - 256):
+        ref = orc.matmul_2d(a[lo:lo + 256], w)
+        assert rel_err(c[lo:lo + 256], ref) <= 1e-2, lo
+    for m2 in (4096, 2048):
+        np.testing.assert_array_equal(host(ops.gemm(dev(a[:m2]), wp, N)), c[:m2])
 
 
 def test_residual_add_bit_exact(cuda):

@@ -311,6 +311,37 @@ def test_decode_fused_permutation_other_experts(cuda, orc, E, k):
     layer.engine.close()
 
 
+# ------------------------------------------------ engine permutation reuse --
+@pytest.mark.parametrize("d,Ts", [(1536, [8192, 1000, 33, 8192, 4096]), (128, [8192, 700])],
+                         ids=["config2_dims", "d128"])
+def test_engine_permutation_across_batch_sizes(cuda, d, Ts):
+    # Consecutive forwards of different sizes on one engine (different router
+    # workgroup counts, so different histogram layouts in the reused
+    # buffers) must each give exactly the standalone router + permutation
+    # kernels' outputs.
+    E, k, f = 8, 2, 128
+    inp = synth.make_moe_inputs(T=max(Ts), d=d, f=f, E=E, k=k, dtype="bf16", seed=d,
+                                name=f"perm-d{d}")
+    say("engine permutation across batch sizes", d, Ts)
+    eng = moe.MoEEngine(d, f, E, k, 1, "bf16", max_tokens=max(Ts))
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    x = dev(inp.x, "bf16")
+    wr, rb = dev(inp.w_router), dev(inp.router_bias)
+    for T in Ts:
+        xs = x[:T].contiguous()
+        eng.forward(xs)
+        st = eng.stash()
+        _, idx, w, bc = ops.router_topk(xs, wr, rb, k)
+        off, rt, rw, tr = ops.permute(idx, w, bc, E)
+        torch.cuda.synchronize()
+        assert torch.equal(st["selected_experts"].view(-1), idx.view(-1)), T
+        assert torch.equal(st["offsets"], off), T
+        assert torch.equal(st["row_token"], rt), T
+        assert torch.equal(st["row_weight"].view(torch.int32), rw.view(torch.int32)), T
+        assert torch.equal(st["token_row"], tr), T
+    eng.close()
+
+
 # ------------------------------------------------------------ decode path --
 @pytest.mark.parametrize("T,E,k,concept", [(32, 8, 2, False), (17, 8, 2, True), (1, 8, 2, False),
                                            (5, 6, 3, False), (32, 5, 1, True)],
