@@ -693,15 +693,16 @@ COPY_BYTES = 1 << 30
 
 
 def copy_calibration():
-    """Three device-to-device copies of exactly COPY_BYTES (a plain copy kernel
-    whose FETCH_SIZE / WRITE_SIZE per dispatch should read COPY_BYTES)."""
+    """Three device-to-device copies of exactly COPY_BYTES with the library's
+    streaming copy kernel (prichs_hbm_copy: reads and writes each byte once,
+    so its FETCH_SIZE / WRITE_SIZE per dispatch should read COPY_BYTES)."""
     import torch
 
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     for _ in range(3):
-        dst.copy_(src)
+        _lib_copy(src, dst)
     torch.cuda.synchronize()
     log(f"bench: copy calibration, 3 x {COPY_BYTES} bytes")
     del src, dst

@@ -249,17 +249,20 @@ __device__ inline void router_quad_body(
 
   if (w_lds != nullptr) {
     // W^T already in the LDS layout [E][d + 4] (the engine keeps one): a
-    // straight copy, 8 float4 loads per thread in flight before their stores
-    // (E (d + 4) is a multiple of 4 since d % 128 == 0).
+    // straight copy, up to 16 float4 loads per thread in flight before their
+    // stores, so one round trip covers E (d + 4) <= 16384 floats (d = 1536,
+    // E = 8: 13 loads per thread; E (d + 4) is a multiple of 4 since
+    // d % 128 == 0).
+    constexpr int kWB = 16;
     const int n4 = E * ws / 4;
     const f32x4 *src = reinterpret_cast<const f32x4 *>(w_lds);
     f32x4 *dst = reinterpret_cast<f32x4 *>(wt_s);
-    for (int base = 0; base < n4; base += 8 * kRouterThreads) {
-      f32x4 v[8];
+    for (int base = 0; base < n4; base += kWB * kRouterThreads) {
+      f32x4 v[kWB];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = src[min(base + u * kRouterThreads + tid, n4 - 1)];
+      for (int u = 0; u < kWB; ++u) v[u] = src[min(base + u * kRouterThreads + tid, n4 - 1)];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kWB; ++u) {
         const int i = base + u * kRouterThreads + tid;
         if (i < n4) dst[i] = v[u];
       }
