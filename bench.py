@@ -432,15 +432,27 @@ def main():
         return b / (m[stage] / 1e3) / 1e9 if m[stage] > 0 else None
 
     kernel = "grouped gate/up GEMM + fused SwiGLU (bf16_gemm_kernel<Bf16Cfg<256,256,4,2>, Bf16Cfg<256,256,4,2>, true>)"
+    # The engine's decode path (bf16, 4 < E <= 8, one shared expert, T <= 32,
+    # d % 128 == 0, f % 64 == 0; config 4 meets it).
+    decode = (inp.dtype == "bf16" and S == 1 and 4 < E <= 8 and T <= 32 and d % 128 == 0
+              and f % 64 == 0)
     if T * k < 64 * E:  # fewer than 64 rows per routed expert on average
         # Decode shape: every touched expert's gate/up weights are streamed once
-        # for a handful of rows, so the launch is bound by HBM, not MFMA.
+        # for a handful of rows, so the launch is bound by HBM, not MFMA.  When
+        # one router workgroup covers the batch (T <= 32 here) the engine runs
+        # the router inside a gate/up launch over every token of every expert:
+        # all E + S experts' weights, x, and the activations of G T rows.
         sel = eng.stash()["selected_experts"].cpu().numpy()
         touched = len(set(sel.reshape(-1).tolist())) + S
-        gu_bytes = touched * d * 2 * f * es + rows * d * es + rows * f * es
+        if decode:
+            gu_bytes = (E + S) * d * 2 * f * es + T * d * es + (E + S) * T * f * es
+            kernel = ("router workgroup + dense gate/up GEMM + fused SwiGLU, decode launch "
+                      "(skinny::decode_gate_up_router_kernel<4>)")
+        else:
+            gu_bytes = touched * d * 2 * f * es + rows * d * es + rows * f * es
+            kernel = "grouped gate/up GEMM + fused SwiGLU, decode shape (skinny::skinny_gemm_kernel<true, 4, 1>)"
         bw = gu_bytes / t_gu / 1e9
-        kernel = "grouped gate/up GEMM + fused SwiGLU, decode shape (skinny::skinny_gemm_kernel<true, 4, 1>)"
-        tfile = "pmc_config4_skinny_traffic.txt"
+        tfile = "pmc_config4_decode_traffic.txt"
         roofline = {"kernel": kernel, "bound": "hbm", "achieved": bw, "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": bw / PEAK_HBM_GBPS,
                     "traffic": measured_traffic(tfile, "gate_up") if args.config == 4 else None,
@@ -509,6 +521,10 @@ def main():
         },
         "stage_ms": {kk: v for kk, v in ms.items() if kk != "n"},
         "stage_ms_flushed": {kk: v for kk, v in ms_cold.items() if kk != "n"},
+        **({"stage_note": "decode path: the router and the permutation run inside the gate/up "
+                          "launch (its first workgroup), so the router and permute intervals hold "
+                          "no kernel, only the gap between event records; gate_up times the "
+                          "router + gate/up launch"} if decode else {}),
         "inputs": inputs_record(f"config{args.config}", inp.digest()),
         "device": torch.cuda.get_device_name(0),
         "device_caps": device_caps(),
