@@ -387,6 +387,38 @@ def test_decode_path_bit_identical_to_routed_path(cuda, orc, T, E, k, concept):
     assert e_row <= TOL["bf16"], (worst, e_row)
 
 
+# ---------------------------------------------------- graph capture --
+def test_engine_forward_replays_in_a_hip_graph(cuda):
+    # The engine forward captured into a graph (router, permutation, gate/up,
+    # down, combine: no allocation, no memset node, no host synchronisation)
+    # and replayed three times, each after an eager forward of another size
+    # (which rewrites every intermediate) and a host synchronisation: every
+    # replay is bit-identical to the eager result.
+    inp = synth.config_inputs(2, T=4096)
+    say("case: engine forward graph replay T 4096")
+    eng = moe.MoEEngine(inp.d, inp.f, inp.E, inp.k, 1, "bf16", max_tokens=4096)
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    x = dev(inp.x, "bf16")
+    out = torch.empty((4096, inp.d), dtype=torch.bfloat16, device="cuda")
+    eng.forward(x, out=out)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eng.forward(x, out=out)
+    xs = x[:1500].contiguous()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        eng.forward(xs)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), rep
+        say(f"  replay {rep}: bit-identical")
+    del graph
+    eng.close()
+
+
 # ------------------------------------------------------------- full layer --
 @pytest.mark.parametrize("cfg", [1, 2, 4])
 def test_moe_layer_full_against_oracle(cuda, orc, cfg):
