@@ -332,6 +332,44 @@ def cpu_baseline(inp, target_s: float):
     }
 
 
+def cold_weights_pass(eng, inp, x, args, layers=4):
+    """The layer's rate when its weights are not resident in the 256 MB MALL:
+    `layers` engines with distinct weights (layer l: the same synthetic
+    tensors rolled by l along their columns, so equally distributed but held
+    apart in HBM; 4 x 106 MB at config 2) run one after another on the same
+    x, W + K such rounds timed as in the headline pass, after it.  Reported
+    beside `value`, not as it."""
+    import numpy as np
+    import torch
+
+    from prichs_amd import moe
+
+    log(f"bench: cold-weights pass, {layers} layers with distinct weights")
+    engines = [eng]
+    for l in range(1, layers):
+        e = moe.MoEEngine(inp.d, inp.f, inp.E, inp.k, inp.n_shared, inp.dtype, max_tokens=inp.T)
+        roll = lambda a: np.roll(a, l, axis=1)  # noqa: E731
+        e.upload(np.roll(inp.w_router, l, axis=0), inp.router_bias, [roll(a) for a in inp.gate],
+                 [roll(a) for a in inp.up], [roll(a) for a in inp.down])
+        engines.append(e)
+    outs = [torch.empty((inp.T, inp.d), dtype=x.dtype, device="cuda") for _ in engines]
+
+    def rounds():
+        for e, o in zip(engines, outs):
+            e.forward(x, out=o)
+
+    elapsed = timed_pass(rounds, args.steps, args.warmup)
+    for e in engines[1:]:
+        e.close()
+    per_layer = elapsed / args.steps / layers
+    return {"layers": layers, "tokens/s": inp.T / per_layer, "ms_per_layer": per_layer * 1e3,
+            "weights_MB_per_layer": round(sum(a.size for a in (*inp.gate, *inp.up, *inp.down))
+                                          * 2 / 1e6, 1),
+            "note": "each layer's weights evicted from the MALL by the other layers' between "
+                    "its forwards; layers 1.. use the same synthetic weights rolled along their "
+                    "columns (distinct tensors in HBM); x stays resident"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -412,6 +450,7 @@ def main():
            if inp.dtype == "bf16" and T * k >= 64 * E else None)
     log(f"bench: timing pass, {args.warmup} warmup + {args.steps} timed steps")
     elapsed = timed_pass(fwd, args.steps, args.warmup)
+    cold = cold_weights_pass(eng, inp, x, args) if T * k >= 64 * E else None
     log("bench: stage ms", json.dumps({kk: round(v, 4) for kk, v in ms.items()}))
     log("bench: stage ms (flushed)", json.dumps({kk: round(v, 4) for kk, v in ms_cold.items()}))
 
@@ -525,6 +564,7 @@ def main():
                           "launch (its first workgroup), so the router and permute intervals hold "
                           "no kernel, only the gap between event records; gate_up times the "
                           "router + gate/up launch"} if decode else {}),
+        **({"cold_weights": cold} if cold is not None else {}),
         "inputs": inputs_record(f"config{args.config}", inp.digest()),
         "device": torch.cuda.get_device_name(0),
         "device_caps": device_caps(),
