@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import rel_err
+from conftest import rel_err, row_rel_err
 from prichs_amd import block, ops, synth
 
 pytestmark = pytest.mark.gpu
@@ -293,6 +293,30 @@ def test_block_other_top_k(cuda, orc, k):
     inp = synth.make_block_inputs(batch=1, seq_len=64, k=k, name=f"block-1x64-k{k}")
     say("block top-k", k)
     _check_block(orc, inp)
+
+
+def test_block_decode_sized_residual_combine(cuda, orc):
+    # At 32 tokens the block's MoE takes the decode path, followed by the
+    # combine with the block's final residual add: out == x1 + moe_out bit
+    # for bit (f32 and bf16), routing bit-exact and moe_out within the bf16
+    # bar of the oracle on the GPU's own MoE input.
+    inp = synth.make_block_inputs(batch=1, seq_len=32, name="block-1x32")
+    say("block decode-sized", inp.batch, inp.seq_len)
+    blk = block.PrichsBlock.from_inputs(inp)
+    x = dev(inp.x)
+    out = host(blk.engine.forward(x, inp.batch, inp.seq_len, out_dtype=torch.float32))
+    st = {n: host(t) if t.dtype != torch.int32 else t.cpu().numpy()
+          for n, t in blk.engine.stash().items()}
+    np.testing.assert_array_equal(out, st["x1"] + st["moe_out"])
+    out_bf = host(blk.engine.forward(x, inp.batch, inp.seq_len, out_dtype=torch.bfloat16))
+    np.testing.assert_array_equal(out_bf, synth.round_bf16(st["x1"] + st["moe_out"]))
+    m = inp.moe
+    sub = synth.MoEInputs(**{**m.__dict__, "x": st["normed2"], "T": st["normed2"].shape[0]})
+    rm = orc.moe_forward(sub)
+    np.testing.assert_array_equal(st["selected_experts"], rm["sel"])
+    e_row, worst = row_rel_err(st["moe_out"], rm["out"])
+    assert e_row <= 2e-2, (worst, e_row)
+    blk.engine.close()
 
 
 def test_block_config5_full(cuda, orc):

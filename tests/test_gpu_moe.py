@@ -364,16 +364,27 @@ def test_decode_path_bit_identical_to_routed_path(cuda, orc, T, E, k, concept):
         cb_np[E - 1] = 0.5
         cb = dev(cb_np)
     x = dev(inp.x, "bf16")
-    outs, stashes = [], []
+    outs, outs32, stashes = [], [], []
     for backward in (False, True):
         eng = moe.MoEEngine(d, f, E, k, 1, "bf16", max_tokens=max(T, 32))
         if backward:
             eng.enable_backward()
         eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
         outs.append(eng.forward(x, concept_bias=cb).clone())
+        outs32.append(eng.forward(x, concept_bias=cb, out_dtype=torch.float32).clone())
         stashes.append(eng.stash())
+        if not backward:
+            # A misaligned output takes the combine's one-column-per-thread
+            # kernel instead of the 8-column one: same bits, bf16 and f32.
+            for dt, ref in ((torch.bfloat16, outs[0]), (torch.float32, outs32[0])):
+                buf = torch.empty(T * d + 8, dtype=dt, device="cuda")
+                mis = buf[1:1 + T * d].view(T, d)
+                eng.forward(x, concept_bias=cb, out=mis)
+                iv = torch.int16 if dt == torch.bfloat16 else torch.int32
+                assert torch.equal(mis.view(iv), ref.view(iv)), dt
         eng.close()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert torch.equal(outs32[0].view(torch.int32), outs32[1].view(torch.int32))
     for name in ("router_logits", "selected_experts", "gating_weights", "offsets", "row_token",
                  "row_weight", "token_row", "act", "y"):
         a, b = stashes[0][name], stashes[1][name]
@@ -410,6 +421,39 @@ def test_engine_forward_replays_in_a_hip_graph(cuda):
     for rep in range(3):
         out.fill_(float("nan"))
         eng.forward(xs)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), rep
+        say(f"  replay {rep}: bit-identical")
+    del graph
+    eng.close()
+
+
+def test_decode_forward_replays_in_a_hip_graph(cuda):
+    # The decode path (router and permutation inside the gate/up launch, the
+    # down GEMM gathering the routed rows) captured at T = 32 and replayed
+    # three times, each after eager forwards of other sizes on both paths:
+    # every replay is bit-identical.
+    inp = synth.config_inputs(4)
+    T = inp.T
+    say("case: decode forward graph replay T", T)
+    eng = moe.MoEEngine(inp.d, inp.f, inp.E, inp.k, 1, "bf16", max_tokens=256)
+    eng.upload(inp.w_router, inp.router_bias, inp.gate, inp.up, inp.down)
+    x = dev(inp.x, "bf16")
+    out = torch.empty((T, inp.d), dtype=torch.bfloat16, device="cuda")
+    eng.forward(x, out=out)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eng.forward(x, out=out)
+    x17 = x[:17].contiguous()
+    x_big = torch.cat([x] * 8).contiguous()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        eng.forward(x17)
+        eng.forward(x_big)
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
