@@ -22,12 +22,15 @@ constexpr int kRouterThreads = PRICHS_ROUTER_THREADS;  // >= PRICHS_MAX_EXPERTS
 // ---------------------------------------------------------------------------
 // Top-k gating of one token whose lpt lanes hold (raw, adj) of expert e = lane
 // index within the group (crates/prichs-core/src/ops.rs:219-248), then the
-// writes of idx / weights and the block's expert histogram.
+// writes of idx / weights and the block's expert histogram.  idx_l / w_l (may
+// be null): LDS copies of idx / weights at the same index, for a placement
+// by the same workgroup (which then needs no global round trip).
 // ---------------------------------------------------------------------------
 __device__ inline void topk_epilogue(float acc, float adj, bool valid, int e, int t, int T, int E,
                                      int k, int lpt, float *__restrict__ logits,
                                      int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
-                                     int *cnt_s) {
+                                     int *cnt_s, int32_t *idx_l = nullptr,
+                                     float *w_l = nullptr) {
 #pragma clang fp contract(off)
   if (valid && logits != nullptr) logits[(size_t)t * E + e] = acc;
 
@@ -122,8 +125,13 @@ __device__ inline void topk_epilogue(float acc, float adj, bool valid, int e, in
 #pragma unroll
     for (int s = 0; s < PRICHS_MAX_TOPK; ++s) {
       if (s < k && s == e) {
+        const float wv = ex[s] * inv;
         topk_idx[(size_t)t * k + s] = sel[s];
-        topk_w[(size_t)t * k + s] = ex[s] * inv;
+        topk_w[(size_t)t * k + s] = wv;
+        if (idx_l != nullptr) {
+          idx_l[t * k + s] = sel[s];
+          w_l[t * k + s] = wv;
+        }
         atomicAdd(&cnt_s[sel[s]], 1);  // integer histogram: order-free
       }
     }
@@ -363,14 +371,20 @@ __device__ inline void router_quad_body(
     adj = acc + bias[e];
     if (concept != nullptr && e < n_concept) adj = adj + concept[e];
   }
-  topk_epilogue(acc, adj, valid, e, t, T, E, k, 8, logits, topk_idx, topk_w, cnt_s);
+  // With a fused permutation this is the only workgroup (bid 0, t < kTpb):
+  // its selections also go to LDS for the placement below.
+  __shared__ int32_t idx_s[kTpb * PRICHS_MAX_TOPK];
+  __shared__ float wsel_s[kTpb * PRICHS_MAX_TOPK];
+  const bool fused = perm.offsets != nullptr;
+  topk_epilogue(acc, adj, valid, e, t, T, E, k, 8, logits, topk_idx, topk_w, cnt_s,
+                fused ? idx_s : nullptr, fused ? wsel_s : nullptr);
   __syncthreads();
   if (tid < E) block_counts[(size_t)bid * E + tid] = cnt_s[tid];
-  if (perm.offsets != nullptr) {
+  if (fused) {
     // The only workgroup: the histogram is the expert totals, the exclusive
     // scan gives the bases (as permute_kernel's block 0 computes them), and
-    // the block's entries (written above, visible after the barrier) are
-    // placed here.
+    // the block's entries (in LDS, visible after the barrier) are placed
+    // here.
     __shared__ int base_s[PRICHS_MAX_EXPERTS];
     if (tid == 0) {
       int run = 0;
@@ -383,7 +397,7 @@ __device__ inline void router_quad_body(
       perm.offsets[E + 1] = run + T;
     }
     __syncthreads();
-    place_entries(topk_idx, topk_w, 0, T, T, E, k, base_s, perm.row_token, perm.row_weight,
+    place_entries(idx_s, wsel_s, 0, T, T, E, k, base_s, perm.row_token, perm.row_weight,
                   perm.token_row, perm.dense_row);
   }
 }
