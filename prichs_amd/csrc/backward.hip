@@ -539,21 +539,36 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
   if ((int)threadIdx.x <= G) offs_s[threadIdx.x] = offsets[threadIdx.x];
   __syncthreads();
   if (threadIdx.x == 0) {
-    int n_items = 0x7fffffff;  // (without halves the walk below finds the end)
-    if (HALVES) {
-      n_items = 0;
-      for (int g = 0; g < G; ++g) {
-        const int m = offs_s[g + 1] - offs_s[g];
-        if (m <= 0) continue;
-        int L, nc;
-        wg_split(m, L, nc);
-        n_items += nc * tiles;
-      }
+    int n_items = 0;
+    for (int g = 0; g < G; ++g) {
+      const int m = offs_s[g + 1] - offs_s[g];
+      if (m <= 0) continue;
+      int L, nc;
+      wg_split(m, L, nc);
+      n_items += nc * tiles;
     }
     const int tail = HALVES && cus > 0 ? n_items % cus : 0;
     const bool halves = tail > 0 && 2 * tail <= cus;
     const int n_whole = halves ? n_items - tail : n_items;
+    // Block b runs on XCD b % 8.  The busy blocks (the grid is an upper bound)
+    // are renumbered so that each XCD takes a contiguous run of them,
+    // consecutive tiles that share operand panels in its L2: in each whole
+    // round of `cus` blocks XCD x takes [round start + x cus/8, + cus/8), and
+    // in a last partial round each XCD's run is its share of that round.
     int rest = (int)blockIdx.x, half = -1;
+    const int busy = halves ? n_whole + 2 * tail : n_items;
+    if (cus > 0 && cus % 8 == 0 && rest < busy) {
+      const int full = busy - busy % cus;
+      if (rest < full) {
+        const int r0 = rest - rest % cus, p = rest % cus;
+        rest = r0 + (p % 8) * (cus / 8) + p / 8;
+      } else {
+        const int q = rest - full, R = busy - full;
+        int pre = 0;
+        for (int y = 0; y < q % 8; ++y) pre += (R - y + 7) / 8;  // the blocks of XCD y
+        rest = full + pre + q / 8;
+      }
+    }
     if (rest >= n_whole) {
       const int u = rest - n_whole;
       rest = halves && u < 2 * tail ? n_whole + u / 2 : n_items;  // n_items: no item
