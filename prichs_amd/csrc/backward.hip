@@ -661,48 +661,66 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restri
     n_split = n;
   }
   __syncthreads();
-  // One (group, row) pair per workgroup step; threads walk the row's Q
-  // columns 4 at a time (no division per element).
+  // Each group's P x Q gradient as float4 units, grid-strided, two units per
+  // thread and step.  Chunk c's partial is read through a buffer resource of
+  // its own; chunks past the last have an empty range and read as zeros
+  // without touching memory, so every batch issues its 8 loads unconditionally
+  // and the in-order sum selects which to add.
   const long long PQ = (long long)P * Q;
-  const int q4n = Q / 4;
-  for (int idx = blockIdx.x; idx < n_split * P; idx += gridDim.x) {
-    const int s = idx / P, i = idx - s * P;
+  const int q4n = Q / 4, n4 = P * q4n;
+  const int stride = (int)gridDim.x * 256;
+  for (int s = 0; s < n_split; ++s) {
     const long long gbase = (long long)slot_of(sg[s], E) * slot_stride;
-    const float *prow = part + (long long)sps[s] * PQ + (long long)i * Q;
-    for (int c4 = threadIdx.x; c4 < q4n; c4 += 256) {
-      const int j = 4 * c4;
-      float *dst = wgrad_dst<GATEUP>(out0, out1, ldo, gbase, i, j, P, Q, f);
-      if (dst == nullptr) continue;
-      // Chunk loads in batches of 8 issued together (a runtime-length loop
-      // would wait for each load before the next); added in chunk order.
-      const int nc = snc[s];
-      float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int c0 = 0; c0 < nc; c0 += 8) {
-        float4 v[8];
+    const int nc = snc[s];
+    const float *p0 = part + (long long)sps[s] * PQ;
+    for (int u0 = (int)(blockIdx.x * 256 + threadIdx.x); u0 < n4; u0 += 2 * stride) {
+      float *dst[2];
+      uint32_t off[2];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          v[u] = *reinterpret_cast<const float4 *>(prow + (long long)min(c0 + u, nc - 1) * PQ + j);
+      for (int w = 0; w < 2; ++w) {
+        const int u = u0 + w * stride;
+        const int i = u / q4n, j = 4 * (u - i * q4n);
+        dst[w] = u < n4 ? wgrad_dst<GATEUP>(out0, out1, ldo, gbase, i, j, P, Q, f) : nullptr;
+        off[w] = u < n4 ? (uint32_t)(((long long)i * Q + j) * 4) : wgb::kOutOfRange;
+      }
+      f32x4 sum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      for (int c0 = 0; c0 < nc; c0 += 4) {
+        f32x4 v[4][2];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (c0 + u >= nc) break;
-          if (c0 + u == 0) {
-            sum = v[u];
-          } else {
-            sum.x = sum.x + v[u].x;
-            sum.y = sum.y + v[u].y;
-            sum.z = sum.z + v[u].z;
-            sum.w = sum.w + v[u].w;
-          }
+        for (int c = 0; c < 4; ++c) {
+          const bool have = c0 + c < nc;
+          const __amdgpu_buffer_rsrc_t r =
+              wg_rsrc(p0 + (have ? c0 + c : 0) * PQ, have ? (uint32_t)(PQ * 4) : 0u);
+#pragma unroll
+          for (int w = 0; w < 2; ++w)
+            v[c][w] = __builtin_bit_cast(f32x4,
+                                         __builtin_amdgcn_raw_buffer_load_b128(r, off[w], 0, 0));
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bool first = c0 + c == 0, use = c0 + c < nc;
+#pragma unroll
+          for (int w = 0; w < 2; ++w)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = sum[w][e] + v[c][w][e];
+              sum[w][e] = first ? v[c][w][e] : use ? a : sum[w][e];
+            }
         }
       }
-      if (beta != 0) {
-        const float4 d = *reinterpret_cast<const float4 *>(dst);
-        sum.x = d.x + sum.x;
-        sum.y = d.y + sum.y;
-        sum.z = d.z + sum.z;
-        sum.w = d.w + sum.w;
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        if (dst[w] == nullptr) continue;
+        float4 r = make_float4(sum[w][0], sum[w][1], sum[w][2], sum[w][3]);
+        if (beta != 0) {
+          const float4 d = *reinterpret_cast<const float4 *>(dst[w]);
+          r.x = d.x + r.x;
+          r.y = d.y + r.y;
+          r.z = d.z + r.z;
+          r.w = d.w + r.w;
+        }
+        *reinterpret_cast<float4 *>(dst[w]) = r;
       }
-      *reinterpret_cast<float4 *>(dst) = sum;
     }
   }
 }
@@ -1174,9 +1192,10 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
     // Every group's chunks: at most G + total_rows / kSplitRows per tile.
     const size_t items = (G + total_rows / wgb::kSplitRows) * (size_t)tiles;
     const size_t ab = total_rows * lda * 2, bb = total_rows * ldb * 2;
-    if (ab >= wgb::kOutOfRange || bb >= wgb::kOutOfRange)
-      return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: operands of %zu and %zu bytes exceed 2 GiB",
-                  ab, bb);
+    if (ab >= wgb::kOutOfRange || bb >= wgb::kOutOfRange || P * Q * 4 >= wgb::kOutOfRange)
+      return fail(PRICHS_ERR_UNSUPPORTED,
+                  "moe backward: operands of %zu and %zu bytes or a %zu x %zu gradient exceed 2 GiB",
+                  ab, bb, P, Q);
     if (items + (size_t)cus > (size_t)INT32_MAX)
       return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: too many tiles");
     auto kern = gateup ? wgrad_bf16_kernel<true, false> : wgrad_bf16_kernel<false, true>;
