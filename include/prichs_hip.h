@@ -520,8 +520,8 @@ int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
  * writes their AVERAGE milliseconds: [0] gate/up pre-activations (empty:
  * the forward's gate/up GEMM writes them once the backward is enabled), [1] rows
  * pass (dY, gathered x, router scalars), [2] dW_down, [3] dA = dY Wd^T,
- * [4] SwiGLU backward, [5] dW_gate / dW_up, [6] dX = [dG dU] [Wg Wu]^T,
- * [7] combine (router VJP, d_x), [8] dW_router, [9] whole backward. */
+ * [4] SwiGLU backward, [5] dX = [dG dU] [Wg Wu]^T, [6] combine (router
+ * VJP, d_x), [7] dW_gate / dW_up, [8] dW_router, [9] whole backward. */
 #define PRICHS_NUM_BWD_STAGES 10
 int prichs_moe_engine_backward_stage_ms(prichs_moe_engine *eng, float *ms_out,
                                         int *n_backwards);

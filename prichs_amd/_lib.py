@@ -29,8 +29,8 @@ MAX_EXPERTS = 64
 MAX_TOPK = 8
 NUM_STAGES = 6
 NUM_BWD_STAGES = 10
-BWD_STAGE_NAMES = ["gate_up", "rows", "dw_down", "d_act", "swiglu_bwd", "dw_gate_up", "d_x_gemm",
-                   "combine", "dw_router", "total"]
+BWD_STAGE_NAMES = ["gate_up", "rows", "dw_down", "d_act", "swiglu_bwd", "d_x_gemm", "combine",
+                   "dw_gate_up", "dw_router", "total"]
 STAGE_NAMES = ("router", "permute", "gate_up", "down", "combine", "total")
 
 
