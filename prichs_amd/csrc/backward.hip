@@ -470,48 +470,62 @@ __device__ __forceinline__ void wgrad_item(
 
   // acc[jb][ib] lane l holds out[i = 16 ib + l % 16][j = 16 jb + 4 (l / 16) + r]
   // of the wave's (BPT / 2) x 64 block.
+  //
+  // The tile leaves through the stage ring (idle after the last K-step), 128
+  // rows of 1 KiB at a time: the waves holding them write their fragments to
+  // LDS (float4 chunk c of row r at c ^ (r & 15), no bank conflicts either
+  // way), then each wave stores 16 whole rows, one 1 KiB row per
+  // instruction, instead of 16 rows x 64 bytes per instruction.
   const long long base = (long long)slot_of(g, E) * slot_stride;
-  if (pslot >= 0 || beta == 0) {
-    // Stores only: a chunk partial, or the gradient itself when beta = 0.
-    float *pbase = pslot >= 0 ? part + (long long)pslot * P * Q : nullptr;
+  float *const pbase = pslot >= 0 ? part + (long long)pslot * P * Q : nullptr;
+  const bool rmw = pslot < 0 && beta != 0;  // dW += tile (beta = 1, an unsplit group)
+  f32x4 *const st = reinterpret_cast<f32x4 *>(lds);
+  constexpr int kPasses = BPT / 128;
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
+  for (int h = 0; h < kPasses; ++h) {
+    if (kPasses == 1 || wp == h) {
 #pragma unroll
-      for (int ib = 0; ib < kIB; ++ib) {
-        const int i = i0 + wp * (BPT / 2) + ib * 16 + (lane & 15);
-        const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
-        const f32x4 a = acc[jb][ib];
-        float *dst = pbase != nullptr ? (i < P && j < Q ? pbase + (long long)i * Q + j : nullptr)
-                                      : wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
-        if (dst) *reinterpret_cast<float4 *>(dst) = make_float4(a[0], a[1], a[2], a[3]);
-      }
-    return;
-  }
-  // Read-modify-write in batches of 8: all loads of a batch are issued before
-  // its stores (a load cannot move past a store that may alias it).
+      for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb) {
-    float *dst[kIB];
-    float4 old[kIB];
-#pragma unroll
-    for (int ib = 0; ib < kIB; ++ib) {
-      const int i = i0 + wp * (BPT / 2) + ib * 16 + (lane & 15);
-      const int j = j0 + wq * 64 + jb * 16 + 4 * (lane >> 4);
-      dst[ib] = wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
-      old[ib] = dst[ib] ? *reinterpret_cast<const float4 *>(dst[ib]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int ib = 0; ib < kIB; ++ib) {
+          const int r = (kPasses == 1 ? wp * (BPT / 2) : 0) + ib * 16 + (lane & 15);
+          const int c = wq * 16 + jb * 4 + (lane >> 4);
+          st[r * 64 + (c ^ (r & 15))] = acc[jb][ib];
+        }
     }
+    __syncthreads();
+    // Rows in batches of 8: all loads of a batch (LDS, and the old values
+    // for a read-modify-write) are issued before its stores.
 #pragma unroll
-    for (int ib = 0; ib < kIB; ++ib) {
-      const f32x4 a = acc[jb][ib];
-      if (dst[ib]) {
-        float4 v = old[ib];
-        v.x = v.x + a[0];
-        v.y = v.y + a[1];
-        v.z = v.z + a[2];
-        v.w = v.w + a[3];
-        *reinterpret_cast<float4 *>(dst[ib]) = v;
+    for (int b = 0; b < 2; ++b) {
+      f32x4 v[8];
+      float *dst[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int r = wave * 16 + b * 8 + e;
+        const int i = i0 + h * 128 + r, j = j0 + 4 * lane;
+        v[e] = st[r * 64 + (lane ^ (r & 15))];
+        dst[e] = pbase != nullptr ? (i < P && j < Q ? pbase + (long long)i * Q + j : nullptr)
+                                  : wgrad_dst<GATEUP>(out0, out1, ldo, base, i, j, P, Q, f);
       }
+      if (rmw) {
+        float4 old[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          old[e] = dst[e] ? *reinterpret_cast<const float4 *>(dst[e]) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[e][0] = old[e].x + v[e][0];
+          v[e][1] = old[e].y + v[e][1];
+          v[e][2] = old[e].z + v[e][2];
+          v[e][3] = old[e].w + v[e][3];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (dst[e]) *reinterpret_cast<float4 *>(dst[e]) = make_float4(v[e][0], v[e][1], v[e][2], v[e][3]);
     }
+    if (h + 1 < kPasses) __syncthreads();  // the next pass reuses the LDS rows
   }
 }
 
