@@ -565,9 +565,35 @@ __device__ __forceinline__ void bf16_tile(
         if (ok1) *reinterpret_cast<u32x2 *>(row_ptr + col0 + 16) = v1;
       }
     };
-    if (P != nullptr) {
+    if (P != nullptr && stage_c) {
       // Training forward: the gate/up pre-activations too, [rows][Np] in
-      // packed column order (the backward's SwiGLU derivative needs them).
+      // packed column order (the backward's SwiGLU derivative needs them),
+      // through a row-major copy of the tile in LDS and written as whole
+      // 512-byte rows, as the down epilogue writes its tile.
+      constexpr int kS = Cf::kStgStride;
+      lds_barrier();  // every wave is done reading the ring
+      const int tcol = wn * WN + cq;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        bf16_t *srow = lds + (wm * WM + fr + 16 * i) * kS + tcol;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const f32x4 a = acc[i][j];
+          *reinterpret_cast<u32x2 *>(srow + 16 * j) =
+              u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+        }
+      }
+      lds_barrier();
+      constexpr int kChunksRow = BN / 8;  // 16-byte chunks per tile row
+#pragma unroll 4
+      for (int c = tid; c < BM * kChunksRow; c += Cf::kThreads) {
+        const int r = c / kChunksRow, ch = c - r * kChunksRow;
+        const int m = m0 + r;
+        if (m < mg)
+          *reinterpret_cast<u32x4 *>(P + (long long)(row0 + m) * Np + n0 + 8 * ch) =
+              *reinterpret_cast<const u32x4 *>(lds + r * kS + 8 * ch);
+      }
+    } else if (P != nullptr) {
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = lr + 16 * i;
