@@ -21,9 +21,11 @@
 // (no staging registers), 3 stages ahead of the MFMAs; the two halves of the
 // workgroup ping-pong, one wave per SIMD multiplying while the other reads
 // its fragments and issues loads.  Workgroups are persistent and walk an
-// XCD-aware tile order.  The down / dense epilogue stages the finished tile
-// in LDS and writes whole rows with 16-byte lanes; the gate/up epilogue
-// exchanges halves between lane pairs and writes 16 bytes per lane.
+// XCD-aware tile order.  The epilogues stage the finished tile in LDS and
+// write whole rows with 16-byte lanes (down / dense: the tile; gate/up: the
+// activations, or in the training forward the pre-activations, whose
+// activations then exchange halves between lane pairs and write 16 bytes per
+// lane).
 // f32 kernel: 128x128x16 tiles on v_mfma_f32_16x16x4_f32 (the fp32-checked
 // mode; accumulates in fp32 like the reference CPU path).
 #include <algorithm>
@@ -510,8 +512,7 @@ __device__ __forceinline__ void bf16_tile(
     // copy of the tile in LDS, then the workgroup writes whole rows with
     // 16-byte lanes (a wave store covers 8 full 128-byte lines instead of
     // 32-byte pieces of 16 rows).  C is 16-byte aligned and ldc, n_store
-    // are multiples of 8.  (The gate/up epilogue writes half as many
-    // columns and gains nothing from it.)
+    // are multiples of 8.
     constexpr int kS = Cf::kStgStride;
     lds_barrier();  // every wave is done reading the ring
     const int tcol = wn * WN + cq;
@@ -606,6 +607,42 @@ __device__ __forceinline__ void bf16_tile(
                      u32x2{pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])}, m < mg, m < mg);
         }
       }
+    }
+    if (stage_c && P == nullptr) {
+      // Inference: the activations through LDS, [BM][BN / 2 + 8], then whole
+      // 256-byte rows (config 2: 296.3 -> 293.7 us per layer; after the
+      // pre-activation copy of the training forward the extra barrier costs
+      // more than it gains there).
+      constexpr int kSa = BN / 2 + 8;
+      lds_barrier();  // every wave is done reading the ring
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        bf16_t *srow = lds + (wm * WM + fr + 16 * i) * kSa;
+#pragma unroll
+        for (int q = 0; q < NJ / (2 * kPieces); ++q) {
+#pragma unroll
+          for (int jj = 0; jj < kPieces; ++jj) {
+            const int j = 2 * kPieces * q + jj;
+            float h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              h[r] = PRICHS_BF16_SILU(acc[i][j][r]) * acc[i][j + kPieces][r];
+            *reinterpret_cast<u32x2 *>(srow + (wn * WN + 2 * Cf::kIl * q) / 2 + cq + 16 * jj) =
+                u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+          }
+        }
+      }
+      lds_barrier();
+      constexpr int kChunksRow = BN / 16;  // 16-byte chunks per activation row
+#pragma unroll 4
+      for (int c = tid; c < BM * kChunksRow; c += Cf::kThreads) {
+        const int r = c / kChunksRow, ch = c - r * kChunksRow;
+        const int m = m0 + r, col = n0 / 2 + 8 * ch;
+        if (m < mg && col < n_store)
+          *reinterpret_cast<u32x4 *>(C + (long long)(row0 + m) * ldc + col) =
+              *reinterpret_cast<const u32x4 *>(lds + r * kSa + 8 * ch);
+      }
+      return;
     }
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
