@@ -508,8 +508,8 @@ typedef struct prichs_moe_grads {
  * gradient carries the gate weight twice (its gather scales dY by w,
  * kernels.cu:926-944, and its scatter scales dX again, kernels.cu:971-991);
  * dx_weighting = 1 is the chain rule.  The weight gradients do not depend on
- * it.  The forward's stash is consumed (act is overwritten): one backward
- * per forward.  x, d_out and d_x are 16-byte aligned. */
+ * it.  The forward's stash is consumed (its buffers are reused): one
+ * backward per forward.  x, d_out and d_x are 16-byte aligned. */
 int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
                                const void *d_out, size_t T, void *d_x,
                                int d_x_dtype, const prichs_moe_grads *grads,
@@ -519,8 +519,9 @@ int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
  * records events in each of the next n backwards, and backward_stage_ms
  * writes their AVERAGE milliseconds: [0] gate/up pre-activations (empty:
  * the forward's gate/up GEMM writes them once the backward is enabled), [1] rows
- * pass (dY, gathered x, router scalars), [2] dW_down, [3] dA = dY Wd^T,
- * [4] SwiGLU backward, [5] dX = [dG dU] [Wg Wu]^T, [6] combine (router
+ * pass (dY, gathered x, router scalars), [2] dW_down, [3] dA = dY Wd^T
+ * (with the SwiGLU backward in its epilogue for bf16 at tiled sizes), [4]
+ * SwiGLU backward (then empty), [5] dX = [dG dU] [Wg Wu]^T, [6] combine (router
  * VJP, d_x), [7] dW_gate / dW_up, [8] dW_router, [9] whole backward. */
 #define PRICHS_NUM_BWD_STAGES 10
 int prichs_moe_engine_backward_stage_ms(prichs_moe_engine *eng, float *ms_out,

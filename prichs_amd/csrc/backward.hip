@@ -130,8 +130,7 @@ __global__ __launch_bounds__(256) void rows_kernel(const T *__restrict__ x,
 }
 
 // ------------------------------------------------------ SwiGLU backward --
-// kernels.cu:459-480 per element: sig = 1 / (1 + exp(-g)), silu = g sig,
-// dsilu = sig (1 + g (1 - sig)), dU = dA silu, dG = (dA u) dsilu.  gu holds
+// kernels.cu:459-480 per element (swiglu_bwd_elem).  gu holds
 // the packed pre-activations [rows, np] (block q: gate columns 32q.. at
 // 64q.., up at 64q + 32..) and receives dG, dU in the same places; padding
 // blocks (columns >= f) are cleared so the dX product sees zeros there.
@@ -161,14 +160,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(T *__restrict__ gu,
   V8<T>::load(up, u);
   V8<T>::load(da + (size_t)r * f + col, a);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float sig = 1.0f / (1.0f + expf(-g[j]));
-    const float silu = g[j] * sig;
-    const float dsilu = sig * (1.0f + g[j] * (1.0f - sig));
-    du[j] = a[j] * silu;
-    const float au = a[j] * u[j];
-    dg[j] = au * dsilu;
-  }
+  for (int j = 0; j < 8; ++j) swiglu_bwd_elem(g[j], u[j], a[j], dg[j], du[j]);
   V8<T>::store(gp, dg);
   V8<T>::store(up, du);
 }

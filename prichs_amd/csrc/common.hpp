@@ -110,6 +110,20 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, prichs_bf16x2));
 }
 
+// SwiGLU backward of one element (kernels.cu:459-480): sig = 1 / (1 + exp(-g)),
+// silu = g sig, dsilu = sig (1 + g (1 - sig)), dU = dA silu, dG = (dA u)
+// dsilu, each operation rounded on its own.  Shared by the SwiGLU backward
+// kernel and the dA GEMM epilogue that fuses it, so both give the same bits.
+__device__ __forceinline__ void swiglu_bwd_elem(float g, float u, float a, float &dg, float &du) {
+#pragma clang fp contract(off)
+  const float sig = 1.0f / (1.0f + expf(-g));
+  const float silu = g * sig;
+  const float dsilu = sig * (1.0f + g * (1.0f - sig));
+  du = a * silu;
+  const float au = a * u;
+  dg = au * dsilu;
+}
+
 // prichs_grouped_gate_up_swiglu / prichs_grouped_down with a tighter bound on
 // every group's row count (a caller that knows T passes T): decode-sized
 // groups then take the skinny weight-streaming kernel.  pre (may be null)
@@ -159,6 +173,16 @@ int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const vo
 int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *row_token,
              const float *row_weight, size_t rows, size_t routed_rows, size_t d, int dtype,
              void *dy, void *xg, float *scal, hipStream_t s);
+// dA = dY Wd^T (the down weights transposed, packed [G][np_f][d]) with the
+// SwiGLU backward in its epilogue: gu [rows][np] (the gate/up pre-activations,
+// packed) receives dG, dU in place and dA is never stored.  *fused = false
+// (nothing launched) where the tiled bf16 kernel does not apply (f32,
+// decode-sized groups, unaligned gu): the caller then runs grouped_gemm_rows
+// into a dA buffer and bwd_swiglu.
+int grouped_dact_swiglu_bwd(const void *dy, size_t d, const void *w_down_t, size_t b_group_stride,
+                            size_t np_f, void *gu, size_t np, size_t f, const int32_t *offsets,
+                            size_t G, size_t max_rows, size_t max_group_rows, int dtype,
+                            void *stream, bool *fused);
 int bwd_swiglu(void *gu, const void *da, size_t rows, size_t f, size_t np, int dtype,
                hipStream_t s);
 // part: bf16 split-K partials, bwd_wgrad_part_elems(rows, P, Q) floats.

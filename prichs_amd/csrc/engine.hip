@@ -13,9 +13,10 @@
 //
 // Backward (after enable_backward): on the forward's stash, whose gate/up
 // GEMM then also keeps the pre-activations,
-//   rows pass (dY, gathered x, router scalars) -> dW_down -> dA = dY Wd^T ->
-//   SwiGLU backward -> dX = [dG dU] [Wg Wu]^T -> combine (router VJP, d_x)
-//   -> dW_gate / dW_up -> dW_router (two passes)
+//   rows pass (dY, gathered x, router scalars) -> dW_down -> dA = dY Wd^T
+//   with the SwiGLU backward in its epilogue (bf16, tiled sizes; else two
+//   launches) -> dX = [dG dU] [Wg Wu]^T -> combine (router VJP, d_x) ->
+//   dW_gate / dW_up -> dW_router (two passes)
 // with the transposed weights packed at upload.
 #include <algorithm>
 #include <cstring>
@@ -650,12 +651,23 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
                  nullptr, d, grads->slot_stride, f, dt, eng->wpart, grads->beta, s);
   if (rc) return rc;
   PRICHS_BWD_MARK(3);
-  rc = grouped_gemm_rows(eng->dy, nullptr, d, eng->w_down_t, eng->dt_elems, np_f, d, eng->act, f,
-                         f, eng->offsets, G, rows, T, dt, stream);
+  // dA = dY Wd^T with the SwiGLU backward in its epilogue (dG, dU into gu in
+  // place; the SwiGLU interval then stays empty), or dA into act and the
+  // separate SwiGLU backward where the fused kernel does not apply.
+  bool fused = false;
+  rc = grouped_dact_swiglu_bwd(eng->dy, d, eng->w_down_t, eng->dt_elems, np_f, eng->gu, np, f,
+                               eng->offsets, G, rows, T, dt, stream, &fused);
   if (rc) return rc;
+  if (!fused) {
+    rc = grouped_gemm_rows(eng->dy, nullptr, d, eng->w_down_t, eng->dt_elems, np_f, d, eng->act,
+                           f, f, eng->offsets, G, rows, T, dt, stream);
+    if (rc) return rc;
+  }
   PRICHS_BWD_MARK(4);
-  rc = bwd_swiglu(eng->gu, eng->act, rows, f, np, dt, s);
-  if (rc) return rc;
+  if (!fused) {
+    rc = bwd_swiglu(eng->gu, eng->act, rows, f, np, dt, s);
+    if (rc) return rc;
+  }
   // dX, then the combine that reads it, then the weight gradients: each
   // reads what the launch before it wrote while that is still in the memory-
   // side cache (dX after dG/dU: 8 us faster than after dW_gate/up's partials

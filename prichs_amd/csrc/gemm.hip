@@ -319,7 +319,12 @@ constexpr int kBf16Threads = 64 * PRICHS_BF16_WGM * PRICHS_BF16_WGN;
 
 // One output tile of the grouped GEMM: M-tile mt (global over the groups of
 // tm) and N-tile nt of width Cf::BN, computed by the whole workgroup.
-template <class Cf, bool GATEUP>
+// DSW (down configurations only): the tile is dA of the MoE backward and its
+// epilogue is the SwiGLU backward: P is then the packed gate/up
+// pre-activations [rows][ldc] (ldc = their packed width Np_gu), updated in
+// place to dG, dU for the tile's activation columns (n_store = f valid ones;
+// those up to Np_gu / 2 beyond f are cleared), and C is not written.
+template <class Cf, bool GATEUP, bool DSW = false>
 __device__ __forceinline__ void bf16_tile(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
@@ -331,6 +336,7 @@ __device__ __forceinline__ void bf16_tile(
   constexpr int kInstPerStage = Cf::kInstPerStage, kStageElems = Cf::kStageElems;
   static_assert(Cf::kThreads == kBf16Threads, "launch bound of the bf16 kernels");
   static_assert(Cf::kWaves == 8, "ping-pong K loop: two groups of 4 waves, one of each per SIMD");
+  static_assert(!(GATEUP && DSW), "the SwiGLU-backward epilogue is a down / dense mode");
   static_assert(!GATEUP || (WN % (2 * Cf::kIl) == 0 && BN % (2 * Cf::kIl) == 0),
                 "whole [gate | up] blocks per wave; packed gate/up rows padded to BN");
 
@@ -507,7 +513,7 @@ __device__ __forceinline__ void bf16_tile(
   //                           [packed col n0 + wn*WN + 16j + 4*(lane >> 4) + r].
   const int lr = m0 + wm * WM + fr;
   const int cq = 4 * (lane >> 4);
-  if (!GATEUP && stage_c) {
+  if (!GATEUP && (stage_c || DSW)) {
     // Staged (down / dense): each lane's 8-byte pieces go to a row-major
     // copy of the tile in LDS, then the workgroup writes whole rows with
     // 16-byte lanes (a wave store covers 8 full 128-byte lines instead of
@@ -528,6 +534,65 @@ __device__ __forceinline__ void bf16_tile(
     }
     lds_barrier();
     constexpr int kChunksRow = BN / 8;  // 16-byte chunks per tile row
+    if constexpr (DSW) {
+      // SwiGLU backward on the staged (bf16-rounded) dA: chunk ch of row r
+      // is activation columns col .. col + 7, whose gate and up
+      // pre-activations are 8 contiguous values each at packed column
+      // (col / kIl) 2 kIl + col % kIl and kIl on.  Each thread's chunks go in
+      // batches of 8, all loads of a batch before its in-place stores;
+      // chunks outside the group's rows or past Np_gu / 2 load from the
+      // buffer's start and store nothing.
+      constexpr int kIl = Cf::kIl;
+      constexpr int kIters = BM * kChunksRow / Cf::kThreads;
+      constexpr int kBatch = kIters < 8 ? kIters : 8;
+      static_assert(BM * kChunksRow % Cf::kThreads == 0 && kIters % kBatch == 0,
+                    "whole batches of chunks per thread");
+      const int half_np = ldc / 2;
+#pragma unroll 1
+      for (int b0 = 0; b0 < kIters; b0 += kBatch) {
+        u32x4 gv[kBatch], uv[kBatch], av[kBatch];
+        bf16_t *gp[kBatch];
+        int col[kBatch];
+#pragma unroll
+        for (int e = 0; e < kBatch; ++e) {
+          const int c = tid + (b0 + e) * Cf::kThreads;
+          const int r = c / kChunksRow, ch = c - r * kChunksRow;
+          const int m = m0 + r;
+          col[e] = n0 + 8 * ch;
+          const bool ok = m < mg && col[e] < half_np;
+          gp[e] = ok ? P + (long long)(row0 + m) * ldc + (col[e] / kIl) * 2 * kIl + col[e] % kIl
+                     : nullptr;
+          const bf16_t *src = ok ? gp[e] : P;
+          gv[e] = *reinterpret_cast<const u32x4 *>(src);
+          uv[e] = *reinterpret_cast<const u32x4 *>(src + kIl);
+          av[e] = *reinterpret_cast<const u32x4 *>(lds + r * kS + 8 * ch);
+        }
+#pragma unroll
+        for (int e = 0; e < kBatch; ++e) {
+          if (gp[e] == nullptr) continue;
+          u32x4 dgv = {0u, 0u, 0u, 0u}, duv = {0u, 0u, 0u, 0u};
+          if (col[e] < n_store) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float dg[2], du[2];
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const uint32_t gb = h ? gv[e][i] & 0xffff0000u : gv[e][i] << 16;
+                const uint32_t ub = h ? uv[e][i] & 0xffff0000u : uv[e][i] << 16;
+                const uint32_t ab = h ? av[e][i] & 0xffff0000u : av[e][i] << 16;
+                swiglu_bwd_elem(__builtin_bit_cast(float, gb), __builtin_bit_cast(float, ub),
+                                __builtin_bit_cast(float, ab), dg[h], du[h]);
+              }
+              dgv[i] = pack_bf16x2(dg[0], dg[1]);
+              duv[i] = pack_bf16x2(du[0], du[1]);
+            }
+          }
+          *reinterpret_cast<u32x4 *>(gp[e]) = dgv;
+          *reinterpret_cast<u32x4 *>(gp[e] + kIl) = duv;
+        }
+      }
+      return;
+    }
 #pragma unroll 4
     for (int c = tid; c < BM * kChunksRow; c += Cf::kThreads) {
       const int r = c / kChunksRow, ch = c - r * kChunksRow;
@@ -692,7 +757,7 @@ __device__ __forceinline__ void bf16_tile(
 // Cf::BN / 2) on two workgroups, so that round takes about half as long.
 // Every output element is the same MFMA chain over K either way, so the
 // results are bit-identical.  CfT == Cf turns this off.
-template <class Cf, class CfT, bool GATEUP>
+template <class Cf, class CfT, bool GATEUP, bool DSW = false>
 __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
@@ -721,15 +786,15 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     int mt, nt;
     if (t < n_full) {
       tile_coords(t, m_tiles, n_tiles, mt, nt);
-      bf16_tile<Cf, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
-                            stage_c, P, lds, mt, nt);
+      bf16_tile<Cf, GATEUP, DSW>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
+                                 stage_c, P, lds, mt, nt);
     } else if constexpr (kSplit) {
       // Items 2u, 2u + 1 are the halves of tail tile n_full + u (consecutive
       // items run on one XCD, so both halves share the A panel in its L2).
       const int u = t - n_full;
       tile_coords(n_full + u / 2, m_tiles, n_tiles, mt, nt);
-      bf16_tile<CfT, GATEUP>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
-                             stage_c, P, lds, mt, 2 * nt + (u & 1));
+      bf16_tile<CfT, GATEUP, DSW>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
+                                  stage_c, P, lds, mt, 2 * nt + (u & 1));
     }
   }
 }
@@ -1260,7 +1325,7 @@ size_t bf16_grid(size_t max_rows, int G, int Np, int cus) {
   return std::max<size_t>(1, std::min<size_t>(ub, (size_t)gemm_cu_limit(cus)));
 }
 
-template <class Cf, bool GATEUP>
+template <class Cf, bool GATEUP, bool DSW = false>
 int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                 int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
                 int dense_m, size_t max_rows, int cus, hipStream_t s, void *pre) {
@@ -1268,7 +1333,7 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
   const int grid = (int)bf16_grid<Cf, GATEUP>(max_rows, G, Np, cus);
   static bool attr_set = false;
   if (!attr_set) {
-    PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&bf16_gemm_kernel<Cf, CfT, GATEUP>),
+    PRICHS_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&bf16_gemm_kernel<Cf, CfT, GATEUP, DSW>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)Cf::kLdsBytes),
                    "grouped gemm: set LDS size");
@@ -1282,7 +1347,10 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
                       reinterpret_cast<uintptr_t>(Cp) % 16 == 0 && ldc % 8 == 0 &&
                       n_store % 8 == 0 && reinterpret_cast<uintptr_t>(pre) % 16 == 0;
   static_assert(CfT::kLdsBytes <= Cf::kLdsBytes, "tail tiles fit the launch's LDS");
-  hipLaunchKernelGGL((bf16_gemm_kernel<Cf, CfT, GATEUP>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
+  if (DSW && !stage_c)
+    return fail(PRICHS_ERR_UNSUPPORTED,
+                "grouped gemm: the SwiGLU-backward epilogue needs 16-byte aligned pre-activations");
+  hipLaunchKernelGGL((bf16_gemm_kernel<Cf, CfT, GATEUP, DSW>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
                      b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G, dense_m,
                      stage_c, static_cast<bf16_t *>(pre));
@@ -1587,6 +1655,33 @@ int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const vo
   return launch_grouped(false, A, a_rows, (int)lda, B, (long long)b_group_stride, (int)Np,
                         (int)K, C, (int)ldc, (int)n_store, offsets, (int)G, 0, max_rows, dtype,
                         as_stream(stream), std::min(max_rows, max_group_rows));
+}
+
+int grouped_dact_swiglu_bwd(const void *dy, size_t d, const void *w_down_t, size_t b_group_stride,
+                            size_t np_f, void *gu, size_t np, size_t f, const int32_t *offsets,
+                            size_t G, size_t max_rows, size_t max_group_rows, int dtype,
+                            void *stream, bool *fused) {
+  *fused = false;
+  if (int rc = check_gemm_shape(np_f, d, dtype, "dA + SwiGLU backward")) return rc;
+  PRICHS_REQUIRE(dy && w_down_t && gu && offsets && G >= 1 && G <= (size_t)kMaxGroups,
+                 "dA + SwiGLU backward: null pointer or G=%zu", G);
+  // The tiled kernel's shapes (launch_grouped takes the skinny kernel for
+  // decode-sized groups), 16-byte aligned pre-activations of whole 8-column
+  // chunks, and a packed width whose activation columns the N-tiles cover.
+  const size_t mg = std::min(max_rows, max_group_rows);
+  const bool skinny = mg <= (size_t)skinny::kSkinnyRows && d % kBf16KMultiple == 0 &&
+                      np_f % skinny::BN == 0;
+  if (dtype != PRICHS_DTYPE_BF16 || skinny || reinterpret_cast<uintptr_t>(gu) % 16 != 0 ||
+      np % 8 != 0 || f % 8 != 0 || np / 2 > np_f || np_f % Bf16Down::BN != 0 ||
+      max_rows > (size_t)INT32_MAX || d > (size_t)INT32_MAX || np > (size_t)INT32_MAX)
+    return PRICHS_OK;
+  const int cus = device_cu_count();
+  if (cus <= 0) return fail(PRICHS_ERR_HIP, "dA + SwiGLU backward: cannot query the device");
+  *fused = true;
+  return launch_bf16<Bf16Down, false, true>(dy, nullptr, (int)d, w_down_t,
+                                            (long long)b_group_stride, (int)np_f, (int)d, nullptr,
+                                            (int)np, (int)f, offsets, (int)G, 0, max_rows, cus,
+                                            as_stream(stream), gu);
 }
 }  // namespace prichs
 
