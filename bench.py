@@ -688,7 +688,6 @@ def bench_backward(args):
     bwd_gemm_ms = sum(bms[kk] for kk in gemm_flops)
     bwd_gemm_tflops = sum(gemm_flops.values()) / (bwd_gemm_ms / 1e3) / 1e12
     es = 2
-    rows_bytes = rows * d * es * 4 + T * k * d * es + rows * 4 + T * k * 8
     swiglu_bytes = rows * np_gu * es * 2 + rows * f * es
     combine_bytes = rows * d * es + T * k * 16 + T * d * es + T * E * 4 + d * E * 4
 
@@ -696,8 +695,12 @@ def bench_backward(args):
         return b / (bms[stage] / 1e3) / 1e9 if bms[stage] > 0 else None
 
     # The SwiGLU backward runs inside the dA GEMM (bf16 at tiled sizes): its
-    # own interval then holds only its two events.
+    # own interval then holds only its two events.  The same condition makes
+    # the rows pass cover the routed rows only (the shared expert's dY and xg
+    # rows are d_out and x, read in place by their consumers).
     swiglu_fused = bms["swiglu_bwd"] < 0.2 * bms["d_act"]
+    rows_pass = T * k if swiglu_fused else rows
+    rows_bytes = rows_pass * d * es * 4 + T * k * d * es + rows_pass * 4 + T * k * 8
 
     res = {
         "metric": TRAIN_METRIC,

@@ -293,7 +293,7 @@ __device__ __forceinline__ void wgrad_item(
     const bf16_t *__restrict__ A, int lda, uint32_t a_bytes, const bf16_t *__restrict__ B,
     int ldb, uint32_t b_bytes, int E, int P, int Q, float *out0, float *out1, int ldo,
     long long slot_stride, int f, float *__restrict__ part, int beta, bf16_t *lds, int g,
-    int row_lo, int mg, int pslot, int i0, int j0) {
+    int a_row_lo, int b_row_lo, int mg, int pslot, int i0, int j0) {
   using namespace wgb;
   static_assert(BPT == 256 || BPT == 128, "whole or half tiles");
   // A tile: [BK][BPT] bf16 (rows of kRowA bytes); B tile: [BK][256].
@@ -338,7 +338,7 @@ __device__ __forceinline__ void wgrad_item(
     for (int i = 0; i < kInstA; ++i) {
       const int rr = kt * BK + a_row[i];
       const bool ok = rr < mg;
-      const uint32_t row = (uint32_t)(row_lo + rr);
+      const uint32_t row = (uint32_t)(a_row_lo + rr);
       wg_dma(ra, ok ? row * (uint32_t)lda * 2u + a_col[i] : kOutOfRange,
              sa + (BPT == 256 ? 4 * wave + 2 * i : 4 * wave) * BPT);
     }
@@ -346,7 +346,7 @@ __device__ __forceinline__ void wgrad_item(
     for (int i = 0; i < 2; ++i) {
       const int rr = kt * BK + b_row[i];
       const bool ok = rr < mg;
-      const uint32_t row = (uint32_t)(row_lo + rr);
+      const uint32_t row = (uint32_t)(b_row_lo + rr);
       wg_dma(rb, ok ? row * (uint32_t)ldb * 2u + b_col[i] : kOutOfRange,
              sb + (4 * wave + 2 * i) * BQ);
     }
@@ -536,7 +536,8 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
     const bf16_t *__restrict__ A, int lda, uint32_t a_bytes, const bf16_t *__restrict__ B,
     int ldb, uint32_t b_bytes, const int32_t *__restrict__ offsets, int G, int E, int P, int Q,
     int tiles_q, int tiles, float *out0, float *out1, int ldo, long long slot_stride, int f,
-    float *__restrict__ part, int beta, int cus) {
+    float *__restrict__ part, int beta, int cus, const bf16_t *__restrict__ A2, uint32_t a2_bytes,
+    const bf16_t *__restrict__ B2, uint32_t b2_bytes, int alt_g, int alt_row0) {
   using namespace wgb;
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   // The offsets come to LDS in one parallel load.
@@ -612,12 +613,20 @@ __global__ __launch_bounds__(wgb::kThreads) void wgrad_bf16_kernel(
   const int half = item[5];
   const int tp = tile / tiles_q;
   const int i0 = tp * BP, j0 = (tile - tp * tiles_q) * BQ;
+  // Group alt_g's rows may live in other buffers: its rows alt_row0.. of the
+  // row space are rows 0.. of A2 / B2 where those are given.
+  const bool alt_a = g == alt_g && A2 != nullptr, alt_b = g == alt_g && B2 != nullptr;
+  const bf16_t *const Ai = alt_a ? A2 : A;
+  const bf16_t *const Bi = alt_b ? B2 : B;
+  const uint32_t abi = alt_a ? a2_bytes : a_bytes, bbi = alt_b ? b2_bytes : b_bytes;
+  const int a_row_lo = alt_a ? row_lo - alt_row0 : row_lo;
+  const int b_row_lo = alt_b ? row_lo - alt_row0 : row_lo;
   if (half < 0) {
-    wgrad_item<GATEUP, 256>(A, lda, a_bytes, B, ldb, b_bytes, E, P, Q, out0, out1, ldo,
-                            slot_stride, f, part, beta, lds, g, row_lo, mg, pslot, i0, j0);
+    wgrad_item<GATEUP, 256>(Ai, lda, abi, Bi, ldb, bbi, E, P, Q, out0, out1, ldo, slot_stride, f,
+                            part, beta, lds, g, a_row_lo, b_row_lo, mg, pslot, i0, j0);
   } else if constexpr (HALVES) {
-    wgrad_item<GATEUP, 128>(A, lda, a_bytes, B, ldb, b_bytes, E, P, Q, out0, out1, ldo,
-                            slot_stride, f, part, beta, lds, g, row_lo, mg, pslot, i0 + 128 * half,
+    wgrad_item<GATEUP, 128>(Ai, lda, abi, Bi, ldb, bbi, E, P, Q, out0, out1, ldo, slot_stride, f,
+                            part, beta, lds, g, a_row_lo, b_row_lo, mg, pslot, i0 + 128 * half,
                             j0);
   }
 }
@@ -1188,7 +1197,7 @@ size_t bwd_wgrad_part_elems(size_t max_rows, size_t P, size_t Q) {
 int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb, size_t total_rows,
               const int32_t *offsets, size_t G, size_t E, size_t P, size_t Q, float *out0,
               float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, float *part,
-              int beta, hipStream_t s) {
+              int beta, hipStream_t s, const WgradAlt &alt) {
   if (total_rows == 0) return PRICHS_OK;
   const int cus = device_cu_count();
   const unsigned rgrid = (unsigned)std::max(1, 4 * cus);
@@ -1198,7 +1207,9 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
     // Every group's chunks: at most G + total_rows / kSplitRows per tile.
     const size_t items = (G + total_rows / wgb::kSplitRows) * (size_t)tiles;
     const size_t ab = total_rows * lda * 2, bb = total_rows * ldb * 2;
-    if (ab >= wgb::kOutOfRange || bb >= wgb::kOutOfRange || P * Q * 4 >= wgb::kOutOfRange)
+    const size_t ab2 = alt.A ? alt.rows * lda * 2 : 0, bb2 = alt.B ? alt.rows * ldb * 2 : 0;
+    if (ab >= wgb::kOutOfRange || bb >= wgb::kOutOfRange || ab2 >= wgb::kOutOfRange ||
+        bb2 >= wgb::kOutOfRange || P * Q * 4 >= wgb::kOutOfRange)
       return fail(PRICHS_ERR_UNSUPPORTED,
                   "moe backward: operands of %zu and %zu bytes or a %zu x %zu gradient exceed 2 GiB",
                   ab, bb, P, Q);
@@ -1222,7 +1233,10 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
                        static_cast<const bf16_t *>(A), (int)lda, (uint32_t)ab,
                        static_cast<const bf16_t *>(B), (int)ldb, (uint32_t)bb, offsets, (int)G,
                        (int)E, (int)P, (int)Q, tiles_q, tiles, out0, out1, (int)ldo,
-                       (long long)slot_stride, (int)f, part, beta, cus);
+                       (long long)slot_stride, (int)f, part, beta, cus,
+                       static_cast<const bf16_t *>(alt.A), (uint32_t)ab2,
+                       static_cast<const bf16_t *>(alt.B), (uint32_t)bb2,
+                       alt.A || alt.B ? (int)alt.g : -1, (int)alt.row0);
     PRICHS_LAUNCH_CHECK("moe backward: weight gradient");
     // Some group may have been split, or (beta = 0) may have no rows.
     if (total_rows > (size_t)wgb::kSplitRows || beta == 0) {
@@ -1233,6 +1247,8 @@ int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb,
     }
     return PRICHS_OK;
   }
+  if (alt.A || alt.B)
+    return fail(PRICHS_ERR_UNSUPPORTED, "moe backward: alternate row buffers need bf16");
   const int tiles_q = (int)cdiv(Q, wg::BQ);
   const int tiles = (int)cdiv(P, wg::BP) * tiles_q;
   const unsigned grid = (unsigned)(8 * cdiv((size_t)tiles, 8) * G);

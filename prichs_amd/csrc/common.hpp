@@ -177,20 +177,31 @@ int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *row
 // SwiGLU backward in its epilogue: gu [rows][np] (the gate/up pre-activations,
 // packed) receives dG, dU in place and dA is never stored.  *fused = false
 // (nothing launched) where the tiled bf16 kernel does not apply (f32,
-// decode-sized groups, unaligned gu): the caller then runs grouped_gemm_rows
-// into a dA buffer and bwd_swiglu.
+// decode-sized groups, unaligned gu; dact_swiglu_bwd_fusable): the caller
+// then runs grouped_gemm_rows into a dA buffer and bwd_swiglu.  a2 (may be
+// null): group a2_g's rows a2_row0.. of dY are rows 0.. of a2 (same pitch).
+bool dact_swiglu_bwd_fusable(size_t d, size_t np_f, const void *gu, size_t np, size_t f,
+                             size_t max_rows, size_t max_group_rows, int dtype);
 int grouped_dact_swiglu_bwd(const void *dy, size_t d, const void *w_down_t, size_t b_group_stride,
                             size_t np_f, void *gu, size_t np, size_t f, const int32_t *offsets,
                             size_t G, size_t max_rows, size_t max_group_rows, int dtype,
-                            void *stream, bool *fused);
+                            void *stream, bool *fused, const void *a2 = nullptr, size_t a2_g = 0,
+                            size_t a2_row0 = 0);
 int bwd_swiglu(void *gu, const void *da, size_t rows, size_t f, size_t np, int dtype,
                hipStream_t s);
 // part: bf16 split-K partials, bwd_wgrad_part_elems(rows, P, Q) floats.
 size_t bwd_wgrad_part_elems(size_t max_rows, size_t P, size_t Q);
+// Group g's rows row0 .. row0 + rows - 1 of the row space read from A / B
+// (bf16, same row pitch) instead, where those are set: the shared expert's
+// rows are x and d_out themselves, which the rows pass then need not copy.
+struct WgradAlt {
+  const void *A = nullptr, *B = nullptr;
+  size_t g = 0, row0 = 0, rows = 0;
+};
 int bwd_wgrad(bool gateup, const void *A, size_t lda, const void *B, size_t ldb, size_t total_rows,
               const int32_t *offsets, size_t G, size_t E, size_t P, size_t Q, float *out0,
               float *out1, size_t ldo, size_t slot_stride, size_t f, int dtype, float *part,
-              int beta, hipStream_t s);
+              int beta, hipStream_t s, const WgradAlt &alt = WgradAlt());
 int bwd_combine(const void *dX, const float *scal, const int32_t *topk_idx, const float *topk_w,
                 const int32_t *token_row, const float *wrt, size_t T, size_t d, size_t k,
                 int weighting, int dtype, float *dlr, void *d_x, int dx_dtype, hipStream_t s);

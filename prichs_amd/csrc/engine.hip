@@ -642,13 +642,26 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   PRICHS_BWD_MARK(0);
   // (Stage 0, the gate/up pre-activations, is written by the forward's
   // gate/up GEMM when the backward is enabled; its interval stays empty.)
+  // The shared expert's rows of dY and xg are d_out and x themselves (weight
+  // 1, rows in token order).  Where the bf16 tiled kernels run (the fused dA
+  // + SwiGLU backward applies), dW_down, dA and dW_gate/up read those rows
+  // from d_out and x directly and the rows pass covers the routed rows only.
+  const bool lean = eng->S == 1 && dact_swiglu_bwd_fusable(d, np_f, eng->gu, np, f, rows, T, dt);
+  WgradAlt alt_dy, alt_x;
+  if (lean) {
+    alt_dy.B = d_out;
+    alt_x.A = x;
+    alt_dy.g = alt_x.g = E;
+    alt_dy.row0 = alt_x.row0 = routed;
+    alt_dy.rows = alt_x.rows = T;
+  }
   PRICHS_BWD_MARK(1);
-  rc = bwd_rows(x, d_out, eng->y, eng->row_token, eng->row_weight, rows, routed, d, dt, eng->dy,
-                eng->xg, eng->scal, s);
+  rc = bwd_rows(x, d_out, eng->y, eng->row_token, eng->row_weight, lean ? routed : rows, routed, d,
+                dt, eng->dy, eng->xg, eng->scal, s);
   if (rc) return rc;
   PRICHS_BWD_MARK(2);
   rc = bwd_wgrad(false, eng->act, f, eng->dy, d, rows, eng->offsets, G, E, f, d, grads->d_down,
-                 nullptr, d, grads->slot_stride, f, dt, eng->wpart, grads->beta, s);
+                 nullptr, d, grads->slot_stride, f, dt, eng->wpart, grads->beta, s, alt_dy);
   if (rc) return rc;
   PRICHS_BWD_MARK(3);
   // dA = dY Wd^T with the SwiGLU backward in its epilogue (dG, dU into gu in
@@ -656,8 +669,11 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   // separate SwiGLU backward where the fused kernel does not apply.
   bool fused = false;
   rc = grouped_dact_swiglu_bwd(eng->dy, d, eng->w_down_t, eng->dt_elems, np_f, eng->gu, np, f,
-                               eng->offsets, G, rows, T, dt, stream, &fused);
+                               eng->offsets, G, rows, T, dt, stream, &fused,
+                               lean ? d_out : nullptr, E, routed);
   if (rc) return rc;
+  if (lean && !fused)
+    return fail(PRICHS_ERR_STATE, "engine_backward: the dA launch did not take the shared rows");
   if (!fused) {
     rc = grouped_gemm_rows(eng->dy, nullptr, d, eng->w_down_t, eng->dt_elems, np_f, d, eng->act,
                            f, f, eng->offsets, G, rows, T, dt, stream);
@@ -682,7 +698,7 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   if (rc) return rc;
   PRICHS_BWD_MARK(7);
   rc = bwd_wgrad(true, eng->xg, d, eng->gu, np, rows, eng->offsets, G, E, d, np, grads->d_gate,
-                 grads->d_up, f, grads->slot_stride, f, dt, eng->wpart, grads->beta, s);
+                 grads->d_up, f, grads->slot_stride, f, dt, eng->wpart, grads->beta, s, alt_x);
   if (rc) return rc;
   PRICHS_BWD_MARK(8);
   rc = bwd_router_wgrad(eng->xg, eng->dlr, eng->offsets, T, k, d, E, dt, eng->rpart,

@@ -317,6 +317,14 @@ using Bf16Tall = Bf16Cfg<256, 288, 4, 2>;
 // substitute in the host pass).
 constexpr int kBf16Threads = 64 * PRICHS_BF16_WGM * PRICHS_BF16_WGN;
 
+// Group g's A rows row0.. read from A + delta (elements) instead: the MoE
+// backward's dA takes the shared expert's rows of dY from d_out itself.
+// g = -1: none.
+struct A2Rows {
+  long long delta = 0;
+  int g = -1, row0 = 0;
+};
+
 // One output tile of the grouped GEMM: M-tile mt (global over the groups of
 // tm) and N-tile nt of width Cf::BN, computed by the whole workgroup.
 // DSW (down configurations only): the tile is dA of the MoE backward and its
@@ -329,7 +337,7 @@ __device__ __forceinline__ void bf16_tile(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
     bf16_t *__restrict__ C, int ldc, int n_store, const WaveTileMap &tm, int stage_c,
-    bf16_t *__restrict__ P, bf16_t *lds, int mt, int nt) {
+    bf16_t *__restrict__ P, bf16_t *lds, int mt, int nt, const A2Rows &a2) {
   constexpr int BM = Cf::BM, BN = Cf::BN, BK = Cf::BK, kStages = Cf::kStages;
   constexpr int WGN = Cf::WGN, WM = Cf::WM, WN = Cf::WN, MI = Cf::MI, NJ = Cf::NJ;
   constexpr int kRowsPerInst = Cf::kRowsPerInst, kInstA = Cf::kInstA, kInstB = Cf::kInstB;
@@ -381,7 +389,8 @@ __device__ __forceinline__ void bf16_tile(
     lr = lr < mg ? lr : mg - 1;  // rows past the group repeat its last row
     const int vr = row0 + lr;
     const int src = a_rows ? a_rows[vr] : vr;
-    a_goff[i] = (long long)src * lda + dma_chunk * 8;
+    a_goff[i] = g == a2.g ? a2.delta + (long long)(vr - a2.row0) * lda + dma_chunk * 8
+                          : (long long)src * lda + dma_chunk * 8;
   }
 #pragma unroll
   for (int i = 0; i < kInstB; ++i) {
@@ -762,7 +771,7 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     const bf16_t *__restrict__ A, const int32_t *__restrict__ a_rows, int lda,
     const bf16_t *__restrict__ B, long long b_group_stride, int Np, int K,
     bf16_t *__restrict__ C, int ldc, int n_store, const int32_t *__restrict__ offsets,
-    int G, int dense_m, int stage_c, bf16_t *__restrict__ P) {
+    int G, int dense_m, int stage_c, bf16_t *__restrict__ P, A2Rows a2) {
   constexpr bool kSplit = !std::is_same<Cf, CfT>::value;
   static_assert(!kSplit || (CfT::BM == Cf::BM && 2 * CfT::BN == Cf::BN && !GATEUP),
                 "tail tiles are the two column halves of a down / dense tile");
@@ -787,14 +796,14 @@ __global__ __launch_bounds__(kBf16Threads) void bf16_gemm_kernel(
     if (t < n_full) {
       tile_coords(t, m_tiles, n_tiles, mt, nt);
       bf16_tile<Cf, GATEUP, DSW>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
-                                 stage_c, P, lds, mt, nt);
+                                 stage_c, P, lds, mt, nt, a2);
     } else if constexpr (kSplit) {
       // Items 2u, 2u + 1 are the halves of tail tile n_full + u (consecutive
       // items run on one XCD, so both halves share the A panel in its L2).
       const int u = t - n_full;
       tile_coords(n_full + u / 2, m_tiles, n_tiles, mt, nt);
       bf16_tile<CfT, GATEUP, DSW>(A, a_rows, lda, B, b_group_stride, Np, K, C, ldc, n_store, tm,
-                                  stage_c, P, lds, mt, 2 * nt + (u & 1));
+                                  stage_c, P, lds, mt, 2 * nt + (u & 1), a2);
     }
   }
 }
@@ -1328,7 +1337,8 @@ size_t bf16_grid(size_t max_rows, int G, int Np, int cus) {
 template <class Cf, bool GATEUP, bool DSW = false>
 int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, long long b_stride,
                 int Np, int K, void *Cp, int ldc, int n_store, const int32_t *offsets, int G,
-                int dense_m, size_t max_rows, int cus, hipStream_t s, void *pre) {
+                int dense_m, size_t max_rows, int cus, hipStream_t s, void *pre,
+                A2Rows a2 = A2Rows()) {
   using CfT = TailCfg<Cf, GATEUP>;
   const int grid = (int)bf16_grid<Cf, GATEUP>(max_rows, G, Np, cus);
   static bool attr_set = false;
@@ -1353,7 +1363,7 @@ int launch_bf16(const void *A, const int32_t *a_rows, int lda, const void *B, lo
   hipLaunchKernelGGL((bf16_gemm_kernel<Cf, CfT, GATEUP, DSW>), dim3(grid), dim3(Cf::kThreads), Cf::kLdsBytes, s,
                      static_cast<const bf16_t *>(A), a_rows, lda, static_cast<const bf16_t *>(B),
                      b_stride, Np, K, static_cast<bf16_t *>(Cp), ldc, n_store, offsets, G, dense_m,
-                     stage_c, static_cast<bf16_t *>(pre));
+                     stage_c, static_cast<bf16_t *>(pre), a2);
   PRICHS_LAUNCH_CHECK("grouped gemm launch");
   return PRICHS_OK;
 }
@@ -1657,31 +1667,44 @@ int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const vo
                         as_stream(stream), std::min(max_rows, max_group_rows));
 }
 
-int grouped_dact_swiglu_bwd(const void *dy, size_t d, const void *w_down_t, size_t b_group_stride,
-                            size_t np_f, void *gu, size_t np, size_t f, const int32_t *offsets,
-                            size_t G, size_t max_rows, size_t max_group_rows, int dtype,
-                            void *stream, bool *fused) {
-  *fused = false;
-  if (int rc = check_gemm_shape(np_f, d, dtype, "dA + SwiGLU backward")) return rc;
-  PRICHS_REQUIRE(dy && w_down_t && gu && offsets && G >= 1 && G <= (size_t)kMaxGroups,
-                 "dA + SwiGLU backward: null pointer or G=%zu", G);
+bool dact_swiglu_bwd_fusable(size_t d, size_t np_f, const void *gu, size_t np, size_t f,
+                             size_t max_rows, size_t max_group_rows, int dtype) {
   // The tiled kernel's shapes (launch_grouped takes the skinny kernel for
   // decode-sized groups), 16-byte aligned pre-activations of whole 8-column
   // chunks, and a packed width whose activation columns the N-tiles cover.
   const size_t mg = std::min(max_rows, max_group_rows);
   const bool skinny = mg <= (size_t)skinny::kSkinnyRows && d % kBf16KMultiple == 0 &&
                       np_f % skinny::BN == 0;
-  if (dtype != PRICHS_DTYPE_BF16 || skinny || reinterpret_cast<uintptr_t>(gu) % 16 != 0 ||
-      np % 8 != 0 || f % 8 != 0 || np / 2 > np_f || np_f % Bf16Down::BN != 0 ||
-      max_rows > (size_t)INT32_MAX || d > (size_t)INT32_MAX || np > (size_t)INT32_MAX)
+  return dtype == PRICHS_DTYPE_BF16 && !skinny && reinterpret_cast<uintptr_t>(gu) % 16 == 0 &&
+         np % 8 == 0 && f % 8 == 0 && np / 2 <= np_f && np_f % Bf16Down::BN == 0 &&
+         max_rows <= (size_t)INT32_MAX && d <= (size_t)INT32_MAX && np <= (size_t)INT32_MAX;
+}
+
+int grouped_dact_swiglu_bwd(const void *dy, size_t d, const void *w_down_t, size_t b_group_stride,
+                            size_t np_f, void *gu, size_t np, size_t f, const int32_t *offsets,
+                            size_t G, size_t max_rows, size_t max_group_rows, int dtype,
+                            void *stream, bool *fused, const void *a2, size_t a2_g,
+                            size_t a2_row0) {
+  *fused = false;
+  if (int rc = check_gemm_shape(np_f, d, dtype, "dA + SwiGLU backward")) return rc;
+  PRICHS_REQUIRE(dy && w_down_t && gu && offsets && G >= 1 && G <= (size_t)kMaxGroups,
+                 "dA + SwiGLU backward: null pointer or G=%zu", G);
+  if (!dact_swiglu_bwd_fusable(d, np_f, gu, np, f, max_rows, max_group_rows, dtype))
     return PRICHS_OK;
   const int cus = device_cu_count();
   if (cus <= 0) return fail(PRICHS_ERR_HIP, "dA + SwiGLU backward: cannot query the device");
+  A2Rows alt;
+  if (a2 != nullptr) {
+    // Element distance from dy to a2 (both bf16, so exact).
+    alt.delta = (long long)(reinterpret_cast<intptr_t>(a2) - reinterpret_cast<intptr_t>(dy)) / 2;
+    alt.g = (int)a2_g;
+    alt.row0 = (int)a2_row0;
+  }
   *fused = true;
   return launch_bf16<Bf16Down, false, true>(dy, nullptr, (int)d, w_down_t,
                                             (long long)b_group_stride, (int)np_f, (int)d, nullptr,
                                             (int)np, (int)f, offsets, (int)G, 0, max_rows, cus,
-                                            as_stream(stream), gu);
+                                            as_stream(stream), gu, alt);
 }
 }  // namespace prichs
 
