@@ -646,7 +646,13 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
   // 1, rows in token order).  Where the bf16 tiled kernels run (the fused dA
   // + SwiGLU backward applies), dW_down, dA and dW_gate/up read those rows
   // from d_out and x directly and the rows pass covers the routed rows only.
-  const bool lean = eng->S == 1 && dact_swiglu_bwd_fusable(d, np_f, eng->gu, np, f, rows, T, dt);
+  // (dW_gate/up reads x after the combine has written d_x, so not when d_x
+  // shares memory with x; d_out is read before the combine.)
+  const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), dx0 = reinterpret_cast<uintptr_t>(d_x);
+  const bool dx_overlaps_x =
+      dx0 < x0 + T * d * dtype_size(dt) && x0 < dx0 + T * d * dtype_size(d_x_dtype);
+  const bool lean = eng->S == 1 && !dx_overlaps_x &&
+                    dact_swiglu_bwd_fusable(d, np_f, eng->gu, np, f, rows, T, dt);
   WgradAlt alt_dy, alt_x;
   if (lean) {
     alt_dy.B = d_out;

@@ -163,6 +163,29 @@ def test_backward_deterministic_accumulating_and_flat_layout(cuda, T):
     assert torch.equal(flat[:, 2].reshape(G, f, d), g1["d_down"])
 
 
+@pytest.mark.parametrize("T", [512, 3000])
+def test_backward_d_x_in_place_of_x(cuda, T):
+    # d_x may be written over x.  The shared expert's rows of x are otherwise
+    # read in place after the combine has written d_x, so the engine then
+    # copies them as for the routed rows: both routes give the same bits.
+    inp, d_out = inputs(T, 256, 128, 8, 2, "bf16", seed=23)
+    eng = make_engine(inp)
+    say("separate d_x", T)
+    x = dev(inp.x, "bf16")
+    eng.forward(x)
+    g1 = zero_grads(inp)
+    dx1 = eng.backward(x, dev(d_out, "bf16"), g1, dx_weighting=2, d_x_dtype=torch.bfloat16)
+    say("d_x over x", T)
+    x2 = dev(inp.x, "bf16")
+    eng.forward(x2)
+    g2 = zero_grads(inp)
+    eng.backward(x2, dev(d_out, "bf16"), g2, dx_weighting=2, d_x=x2)
+    torch.cuda.synchronize()
+    assert torch.equal(x2, dx1)
+    for key in g1:
+        assert torch.equal(g1[key], g2[key]), key
+
+
 def test_backward_modes_share_weight_gradients(cuda):
     inp, d_out = inputs(256, 128, 128, 8, 2, "bf16", seed=5)
     eng = make_engine(inp)
