@@ -1034,23 +1034,27 @@ __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(const float *_
   __shared__ int offs_s[PRICHS_MAX_EXPERTS + 1];
   if ((int)threadIdx.x <= E) offs_s[threadIdx.x] = offsets[threadIdx.x];
   __syncthreads();
+  // Column-fastest (a wave's loads of one chunk row are contiguous), the
+  // chunks of the column's group added in order, 16 loads in flight.
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= d * E) return;
-  const int c = i / E, e = i - c * E;
+  const int e = i / d, c = i - e * d;
   int first = 0;
   for (int g = 0; g < e; ++g)
     first += (offs_s[g + 1] - offs_s[g] + kRouterChunk - 1) / kRouterChunk;
   const int n = (offs_s[e + 1] - offs_s[e] + kRouterChunk - 1) / kRouterChunk;
   float s = 0.f;
-  for (int ch = 0; ch < n; ch += 8) {
-    float v[8];
+  for (int ch = 0; ch < n; ch += 16) {
+    float v[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      v[u] = ch + u < n ? part[(size_t)(first + ch + u) * d + c] : 0.f;
+    for (int u = 0; u < 16; ++u)
+      v[u] = part[(size_t)(first + min(ch + u, n - 1)) * d + c];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s = s + v[u];
+    for (int u = 0; u < 16; ++u)
+      if (ch + u < n) s = s + v[u];
   }
-  dw[i] = beta != 0 ? dw[i] + s : s;
+  const size_t o = (size_t)c * E + e;
+  dw[o] = beta != 0 ? dw[o] + s : s;
 }
 
 unsigned blocks_for(long long n, int per = 256) { return (unsigned)((n + per - 1) / per); }
