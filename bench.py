@@ -699,8 +699,10 @@ def bench_backward(args):
     # the rows pass cover the routed rows only (the shared expert's dY and xg
     # rows are d_out and x, read in place by their consumers).
     swiglu_fused = bms["swiglu_bwd"] < 0.2 * bms["d_act"]
+    # One wave per token: d_out[t] and x[t] read once; dY and xg written and
+    # (routed) y read per row.
     rows_pass = T * k if swiglu_fused else rows
-    rows_bytes = rows_pass * d * es * 4 + T * k * d * es + rows_pass * 4 + T * k * 8
+    rows_bytes = T * d * es * 2 + rows_pass * d * es * 2 + T * k * d * es + T * k * 8
 
     res = {
         "metric": TRAIN_METRIC,

@@ -82,50 +82,74 @@ __device__ inline float wave_sum(float v) {
 }
 
 // ------------------------------------------------------------- rows pass --
-// One wave per row r of the row space (routed rows, then the shared rows):
-// dY[r] = w_r * d_out[t] (kernels.cu:926-944; w = 1 on shared rows, whose
-// gradient the reference feeds straight to the shared expert, engine.rs:
-// 2513-2703), xg[r] = x[t] (the gathered expert input of the weight
-// gradients), and for routed rows s_r = sum_c y[r][c] * d_out[t][c]
-// (kernels.cu:946-969: the dot of the unweighted expert output with the
-// layer's output gradient).
-template <typename T>
+// One wave per token t, over its k routed rows r_s = token_row[t k + s]
+// (and, with `shared`, its shared row T k + t): dY[r] = w_r * d_out[t]
+// (kernels.cu:926-944; w = 1 on the shared row, whose gradient the reference
+// feeds straight to the shared expert, engine.rs:2513-2703), xg[r] = x[t]
+// (the gathered expert input of the weight gradients), and for routed rows
+// s_r = sum_c y[r][c] * d_out[t][c] (kernels.cu:946-969: the dot of the
+// unweighted expert output with the layer's output gradient), each lane
+// summing its columns in order and the wave by a fixed butterfly.  d_out[t]
+// and x[t] are read once for all of the token's rows.
+template <typename T, int KC>
 __global__ __launch_bounds__(256) void rows_kernel(const T *__restrict__ x,
                                                    const T *__restrict__ d_out,
                                                    const T *__restrict__ y,
-                                                   const int32_t *__restrict__ row_token,
-                                                   const float *__restrict__ row_weight, int rows,
-                                                   int routed_rows, int d, T *__restrict__ dy,
+                                                   const int32_t *__restrict__ token_row,
+                                                   const float *__restrict__ row_weight, int T_,
+                                                   int k_rt, int d, int shared, T *__restrict__ dy,
                                                    T *__restrict__ xg, float *__restrict__ scal) {
 #pragma clang fp contract(off)
+  constexpr int kMax = KC > 0 ? KC : PRICHS_MAX_TOPK;
+  const int k = KC > 0 ? KC : k_rt;
   const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-  if (r >= rows) return;
-  const int t = row_token[r];
-  const bool routed = r < routed_rows;
-  const float w = routed ? row_weight[r] : 1.0f;
+  const int t = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+  if (t >= T_) return;
+  int rr[kMax];
+  float w[kMax], sacc[kMax];
+#pragma unroll
+  for (int sl = 0; sl < kMax; ++sl) {
+    rr[sl] = sl < k ? token_row[(size_t)t * k + sl] : 0;
+    w[sl] = sl < k ? row_weight[rr[sl]] : 0.f;
+    sacc[sl] = 0.f;
+  }
+  const size_t rsh = (size_t)T_ * k + t;  // the shared row
   const T *go = d_out + (size_t)t * d;
-  float s = 0.f;
+  const T *xr = x + (size_t)t * d;
+  // x[t] is copied as raw bits (8 elements: 16 bytes in bf16, 32 in f32).
+  using XRaw = typename std::conditional<sizeof(T) == 2, u32x4, u32x4[2]>::type;
   for (int c = lane * 8; c < d; c += 64 * 8) {
-    float g[8], o[8];
+    float g[8];
     V8<T>::load(go + c, g);
-    V8<T>::copy(x + (size_t)t * d + c, xg + (size_t)r * d + c);
+    XRaw xv;
+    __builtin_memcpy(&xv, xr + c, sizeof(XRaw));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = w * g[j];
-    V8<T>::store(dy + (size_t)r * d + c, o);
-    if (routed) {
-      float yv[8];
-      V8<T>::load(y + (size_t)r * d + c, yv);
+    for (int sl = 0; sl < kMax; ++sl) {
+      if (sl < k) {
+        float o[8], yv[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p = yv[j] * g[j];
-        s = s + p;
+        for (int j = 0; j < 8; ++j) o[j] = w[sl] * g[j];
+        V8<T>::store(dy + (size_t)rr[sl] * d + c, o);
+        __builtin_memcpy(xg + (size_t)rr[sl] * d + c, &xv, sizeof(XRaw));
+        V8<T>::load(y + (size_t)rr[sl] * d + c, yv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = yv[j] * g[j];
+          sacc[sl] = sacc[sl] + p;
+        }
       }
     }
+    if (shared) {
+      V8<T>::store(dy + rsh * d + c, g);
+      __builtin_memcpy(xg + rsh * d + c, &xv, sizeof(XRaw));
+    }
   }
-  if (routed) {
-    s = wave_sum(s);
-    if (lane == 0) scal[r] = s;
+#pragma unroll
+  for (int sl = 0; sl < kMax; ++sl) {
+    if (sl < k) {
+      const float sr = wave_sum(sacc[sl]);
+      if (lane == 0) scal[rr[sl]] = sr;
+    }
   }
 }
 
@@ -1154,23 +1178,31 @@ __global__ __launch_bounds__(256) void legacy_scatter_add_grad_kernel(
 }  // namespace
 
 // ---------------------------------------------------------------- launchers --
-int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *row_token,
-             const float *row_weight, size_t rows, size_t routed_rows, size_t d, int dtype,
+int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *token_row,
+             const float *row_weight, size_t T, size_t k, bool shared, size_t d, int dtype,
              void *dy, void *xg, float *scal, hipStream_t s) {
-  if (rows == 0) return PRICHS_OK;
-  const unsigned grid = (unsigned)cdiv(rows, 4);
+  if (T == 0) return PRICHS_OK;
+  const unsigned grid = (unsigned)cdiv(T, 4);  // one wave per token
+#define PRICHS_ROWS_K(TT, KC)                                                                    \
+  hipLaunchKernelGGL((rows_kernel<TT, KC>), dim3(grid), dim3(256), 0, s,                        \
+                     static_cast<const TT *>(x), static_cast<const TT *>(d_out),                \
+                     static_cast<const TT *>(y), token_row, row_weight, (int)T, (int)k, (int)d, \
+                     shared ? 1 : 0, static_cast<TT *>(dy), static_cast<TT *>(xg), scal)
+#define PRICHS_ROWS(TT)          \
+  do {                           \
+    if (k == 2)                  \
+      PRICHS_ROWS_K(TT, 2);      \
+    else if (k == 1)             \
+      PRICHS_ROWS_K(TT, 1);      \
+    else                         \
+      PRICHS_ROWS_K(TT, 0);      \
+  } while (0)
   if (dtype == PRICHS_DTYPE_BF16)
-    hipLaunchKernelGGL(rows_kernel<bf16_t>, dim3(grid), dim3(256), 0, s,
-                       static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(d_out),
-                       static_cast<const bf16_t *>(y), row_token, row_weight, (int)rows,
-                       (int)routed_rows, (int)d, static_cast<bf16_t *>(dy),
-                       static_cast<bf16_t *>(xg), scal);
+    PRICHS_ROWS(bf16_t);
   else
-    hipLaunchKernelGGL(rows_kernel<float>, dim3(grid), dim3(256), 0, s,
-                       static_cast<const float *>(x), static_cast<const float *>(d_out),
-                       static_cast<const float *>(y), row_token, row_weight, (int)rows,
-                       (int)routed_rows, (int)d, static_cast<float *>(dy),
-                       static_cast<float *>(xg), scal);
+    PRICHS_ROWS(float);
+#undef PRICHS_ROWS
+#undef PRICHS_ROWS_K
   PRICHS_LAUNCH_CHECK("moe backward: rows");
   return PRICHS_OK;
 }

@@ -170,8 +170,8 @@ int grouped_gemm_rows(const void *A, const int32_t *a_rows, size_t lda, const vo
                       size_t max_group_rows, int dtype, void *stream);
 
 // MoE backward stages (backward.hip); the engine sequences them.
-int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *row_token,
-             const float *row_weight, size_t rows, size_t routed_rows, size_t d, int dtype,
+int bwd_rows(const void *x, const void *d_out, const void *y, const int32_t *token_row,
+             const float *row_weight, size_t T, size_t k, bool shared, size_t d, int dtype,
              void *dy, void *xg, float *scal, hipStream_t s);
 // dA = dY Wd^T (the down weights transposed, packed [G][np_f][d]) with the
 // SwiGLU backward in its epilogue: gu [rows][np] (the gate/up pre-activations,

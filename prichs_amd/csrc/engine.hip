@@ -662,8 +662,8 @@ extern "C" int prichs_moe_engine_backward(prichs_moe_engine *eng, const void *x,
     alt_dy.rows = alt_x.rows = T;
   }
   PRICHS_BWD_MARK(1);
-  rc = bwd_rows(x, d_out, eng->y, eng->row_token, eng->row_weight, lean ? routed : rows, routed, d,
-                dt, eng->dy, eng->xg, eng->scal, s);
+  rc = bwd_rows(x, d_out, eng->y, eng->token_row, eng->row_weight, T, k, !lean, d, dt, eng->dy,
+                eng->xg, eng->scal, s);
   if (rc) return rc;
   PRICHS_BWD_MARK(2);
   rc = bwd_wgrad(false, eng->act, f, eng->dy, d, rows, eng->offsets, G, E, f, d, grads->d_down,
