@@ -44,6 +44,16 @@ template <> struct V8<float> {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
   }
+  __device__ static void load_nt(const float *p, float v[8]) {
+    typedef float f4_t __attribute__((ext_vector_type(4)));
+    const f4_t a = __builtin_nontemporal_load(reinterpret_cast<const f4_t *>(p));
+    const f4_t b = __builtin_nontemporal_load(reinterpret_cast<const f4_t *>(p + 4));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
   __device__ static void store(float *p, const float v[8]) {
     *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
     *reinterpret_cast<float4 *>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
@@ -56,6 +66,15 @@ template <> struct V8<float> {
 template <> struct V8<bf16_t> {
   __device__ static void load(const bf16_t *p, float v[8]) {
     const u32x4 u = *reinterpret_cast<const u32x4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __builtin_bit_cast(float, u[i] << 16);
+      v[2 * i + 1] = __builtin_bit_cast(float, u[i] & 0xffff0000u);
+    }
+  }
+  // Non-temporal (streaming) load, for data read for the last time.
+  __device__ static void load_nt(const bf16_t *p, float v[8]) {
+    const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v[2 * i] = __builtin_bit_cast(float, u[i] << 16);
@@ -704,7 +723,11 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restri
   // thread and step.  Chunk c's partial is read through a buffer resource of
   // its own; chunks past the last have an empty range and read as zeros
   // without touching memory, so every batch issues its 8 loads unconditionally
-  // and the in-order sum selects which to add.
+  // and the in-order sum selects which to add.  The partials are read once and
+  // are dead afterwards, so the loads are non-temporal (cache policy 2): they
+  // leave the caches to the operands of the kernels that follow (dW_gate/up
+  // 222.7 -> 218.9 us with its reduce, training step -2.6 us; same bits).
+  constexpr int kStreamingLoad = 2;
   const long long PQ = (long long)P * Q;
   const int q4n = Q / 4, n4 = P * q4n;
   const int stride = (int)gridDim.x * 256;
@@ -733,7 +756,7 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restri
 #pragma unroll
           for (int w = 0; w < 2; ++w)
             v[c][w] = __builtin_bit_cast(f32x4,
-                                         __builtin_amdgcn_raw_buffer_load_b128(r, off[w], 0, 0));
+                                         __builtin_amdgcn_raw_buffer_load_b128(r, off[w], 0, kStreamingLoad));
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -894,6 +917,8 @@ __global__ __launch_bounds__(wg::kThreads) void wgrad_f32_kernel(
 // comes transposed, wrt [E, d], so a selection's 8 columns are one vector
 // load.  The thread of column 0 also writes d_logit_j at the row of each
 // selection (dlr [T*k], in row-space order) for the router's weight gradient.
+// dX is read here for the last time, so its loads are non-temporal (training
+// step -1.5 us: they leave the caches to dW_gate/up's operands).
 // KC: the top-k as a compile-time constant (k = 1, 2), or 0 for k at run time.
 template <typename T, typename OT, int KC>
 __global__ __launch_bounds__(256) void combine_kernel(
@@ -956,7 +981,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
   for (int s = 0; s < kMax; ++s) {
     if (s < k) {
-      V8<T>::load(dX + (size_t)rows[s] * d + c, v);
+      V8<T>::load_nt(dX + (size_t)rows[s] * d + c, v);
       const float wx = weighting == 2 ? wt[s] : 1.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -965,7 +990,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
       }
     }
   }
-  V8<T>::load(dX + ((size_t)T_ * k + t) * d + c, v);
+  V8<T>::load_nt(dX + ((size_t)T_ * k + t) * d + c, v);
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = acc[j] + v[j];
   float rs[8];

@@ -258,11 +258,17 @@ int router_topk_lds(const void *x, int x_dtype, const float *w_router, const flo
 size_t router_lds_layout_elems(size_t d, size_t E);
 void router_lds_layout(const float *w_router, size_t d, size_t E, float *out);
 
+// prichs_moe_combine; y_last_use: no later kernel reads y, so its loads are
+// non-temporal (the same results; elementwise.hip).
+int moe_combine(const void *y, int y_dtype, const int32_t *topk_idx, const float *topk_w,
+                const int32_t *token_row, size_t T, size_t d, size_t k, int has_shared, void *out,
+                int out_dtype, void *stream, bool y_last_use);
 // moe_out = the MoE combine (bf16) and out = res + moe_out (the block's final
-// residual add) in one kernel (elementwise.hip).
+// residual add) in one kernel (elementwise.hip); y_last_use as above.
 int moe_combine_residual(const void *y, const int32_t *topk_idx, const float *topk_w,
                          const int32_t *token_row, size_t T, size_t d, size_t k, int has_shared,
-                         void *moe_out, const float *res, void *out, int out_dtype, void *stream);
+                         void *moe_out, const float *res, void *out, int out_dtype, void *stream,
+                         bool y_last_use = false);
 // prichs_moe_engine_forward whose combine also adds the f32 residual:
 // moe_out gets the layer output (bf16), out = residual + moe_out (engine.hip).
 int moe_engine_forward_residual(prichs_moe_engine *eng, const void *x, size_t T,

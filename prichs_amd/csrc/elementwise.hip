@@ -36,6 +36,38 @@ __device__ inline V8 ld8(const bf16_t *p) {
   }
   return r;
 }
+// ld8 with a non-temporal load (streaming cache policy): for data read for
+// the last time, so that it leaves the caches to data that is read again.
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+__device__ inline V8 ld8_nt(const float *p) {
+  V8 r;
+  const nt_f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4 *>(p));
+  const nt_f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4 *>(p + 4));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r.v[i] = a[i];
+    r.v[4 + i] = b[i];
+  }
+  return r;
+}
+__device__ inline V8 ld8_nt(const bf16_t *p) {
+  V8 r;
+  const nt_u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4 *>(p));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r.v[2 * i] = __uint_as_float(a[i] << 16);
+    r.v[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+  }
+  return r;
+}
+template <bool NT, typename T> __device__ inline V8 ld8y(const T *p) {
+  if constexpr (NT)
+    return ld8_nt(p);
+  else
+    return ld8(p);
+}
+
 __device__ inline void st8(float *p, const V8 &r) {
   *reinterpret_cast<float4 *>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
   *reinterpret_cast<float4 *>(p + 4) = make_float4(r.v[4], r.v[5], r.v[6], r.v[7]);
@@ -63,8 +95,8 @@ template <typename T> bool aligned16(const T *p) {
 // out = out + w * y[row]  (crates/prichs-model/src/moe.rs:146, 149, 177-184).
 // KC is the top-k as a compile-time constant (the common k = 1, 2 keep the
 // index loads and the ordering to a few instructions); KC = 0 takes k at run
-// time (k <= PRICHS_MAX_TOPK).
-template <typename YT, typename OT, bool VEC, int KC>
+// time (k <= PRICHS_MAX_TOPK).  NT: y is read for the last time (see ld8_nt).
+template <typename YT, typename OT, bool VEC, int KC, bool NT = false>
 __global__ __launch_bounds__(256) void combine_kernel(
     const YT *__restrict__ y, const int32_t *__restrict__ topk_idx,
     const float *__restrict__ topk_w, const int32_t *__restrict__ token_row, int T, int d,
@@ -108,7 +140,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
   if (VEC) {
     V8 acc;
     if (has_shared) {
-      acc = ld8(y + shared_row * d + c);
+      acc = ld8y<NT>(y + shared_row * d + c);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc.v[j] = 0.f;
@@ -116,7 +148,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
     for (int s = 0; s < kMax; ++s) {
       if (s < k) {
-        const V8 yv = ld8(y + (size_t)rows[s] * d + c);
+        const V8 yv = ld8y<NT>(y + (size_t)rows[s] * d + c);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float p = wt[s] * yv.v[j];
@@ -140,7 +172,8 @@ __global__ __launch_bounds__(256) void combine_kernel(
 // to bf16 into moe_out, the sub-layer output), then out = res + moe with res
 // the f32 residual x1, rounded to OT -- the arithmetic of combine_kernel
 // followed by add_kernel, so both outputs are bit-identical to that pair.
-template <typename OT, int KC>
+// NT: y is read for the last time (see ld8_nt).
+template <typename OT, int KC, bool NT = false>
 __global__ __launch_bounds__(256) void combine_residual_kernel(
     const bf16_t *__restrict__ y, const int32_t *__restrict__ topk_idx,
     const float *__restrict__ topk_w, const int32_t *__restrict__ token_row, int T, int d,
@@ -179,7 +212,7 @@ __global__ __launch_bounds__(256) void combine_residual_kernel(
       }
   V8 acc;
   if (has_shared) {
-    acc = ld8(y + ((size_t)T * k + t) * d + c);
+    acc = ld8y<NT>(y + ((size_t)T * k + t) * d + c);
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc.v[j] = 0.f;
@@ -187,7 +220,7 @@ __global__ __launch_bounds__(256) void combine_residual_kernel(
 #pragma unroll
   for (int s = 0; s < kMax; ++s) {
     if (s < k) {
-      const V8 yv = ld8(y + (size_t)rows[s] * d + c);
+      const V8 yv = ld8y<NT>(y + (size_t)rows[s] * d + c);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float p = wt[s] * yv.v[j];
@@ -456,13 +489,17 @@ void launch_rmsnorm_t(const void *x, const float *w, void *out, float *rstd, siz
 
 template <typename YT, typename OT>
 void launch_combine_t(const void *y, const int32_t *idx, const float *w, const int32_t *tr,
-                      size_t T, size_t d, size_t k, int has_shared, void *out, hipStream_t s) {
+                      size_t T, size_t d, size_t k, int has_shared, void *out, hipStream_t s,
+                      bool y_last_use) {
   const bool vec =
       d % 8 == 0 && aligned16(static_cast<const YT *>(y)) && aligned16(static_cast<OT *>(out));
   const size_t n = T * (vec ? d / 8 : d);
-  auto kern = vec ? (k == 2   ? combine_kernel<YT, OT, true, 2>
-                     : k == 1 ? combine_kernel<YT, OT, true, 1>
-                              : combine_kernel<YT, OT, true, 0>)
+  auto kern = vec ? (y_last_use ? (k == 2   ? combine_kernel<YT, OT, true, 2, true>
+                                   : k == 1 ? combine_kernel<YT, OT, true, 1, true>
+                                            : combine_kernel<YT, OT, true, 0, true>)
+                                : (k == 2   ? combine_kernel<YT, OT, true, 2>
+                                   : k == 1 ? combine_kernel<YT, OT, true, 1>
+                                            : combine_kernel<YT, OT, true, 0>))
                   : combine_kernel<YT, OT, false, 0>;
   hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(256), 0, s, static_cast<const YT *>(y), idx, w,
                      tr, (int)T, (int)d, (int)k, has_shared, static_cast<OT *>(out));
@@ -495,10 +532,10 @@ void launch_rope_t(void *qk, size_t ld, const float *cs, const float *sn, size_t
 using namespace prichs;
 
 // ------------------------------------------------------------ entry points --
-extern "C" int prichs_moe_combine(const void *y, int y_dtype, const int32_t *topk_idx,
-                                  const float *topk_w, const int32_t *token_row, size_t T,
-                                  size_t d, size_t k, int has_shared, void *out, int out_dtype,
-                                  void *stream) {
+namespace prichs {
+int moe_combine(const void *y, int y_dtype, const int32_t *topk_idx, const float *topk_w,
+                const int32_t *token_row, size_t T, size_t d, size_t k, int has_shared, void *out,
+                int out_dtype, void *stream, bool y_last_use) {
   PRICHS_REQUIRE(dtype_ok(y_dtype) && dtype_ok(out_dtype), "combine: bad dtype");
   PRICHS_REQUIRE(k >= 1 && k <= PRICHS_MAX_TOPK, "combine: k=%zu outside [1, %d]", k,
                  PRICHS_MAX_TOPK);
@@ -510,17 +547,30 @@ extern "C" int prichs_moe_combine(const void *y, int y_dtype, const int32_t *top
   const int hs = has_shared ? 1 : 0;
   if (y_dtype == PRICHS_DTYPE_BF16) {
     if (out_dtype == PRICHS_DTYPE_BF16)
-      launch_combine_t<bf16_t, bf16_t>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+      launch_combine_t<bf16_t, bf16_t>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s,
+                                        y_last_use);
     else
-      launch_combine_t<bf16_t, float>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+      launch_combine_t<bf16_t, float>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s,
+                                        y_last_use);
   } else {
     if (out_dtype == PRICHS_DTYPE_BF16)
-      launch_combine_t<float, bf16_t>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+      launch_combine_t<float, bf16_t>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s,
+                                        y_last_use);
     else
-      launch_combine_t<float, float>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s);
+      launch_combine_t<float, float>(y, topk_idx, topk_w, token_row, T, d, k, hs, out, s,
+                                        y_last_use);
   }
   PRICHS_LAUNCH_CHECK("combine launch");
   return PRICHS_OK;
+}
+}  // namespace prichs
+
+extern "C" int prichs_moe_combine(const void *y, int y_dtype, const int32_t *topk_idx,
+                                  const float *topk_w, const int32_t *token_row, size_t T,
+                                  size_t d, size_t k, int has_shared, void *out, int out_dtype,
+                                  void *stream) {
+  return moe_combine(y, y_dtype, topk_idx, topk_w, token_row, T, d, k, has_shared, out,
+                     out_dtype, stream, false);
 }
 
 extern "C" int prichs_rmsnorm_forward(const void *x, int x_dtype, const float *w, void *out,
@@ -659,7 +709,7 @@ namespace prichs {
 int moe_combine_residual(const void *y, const int32_t *topk_idx, const float *topk_w,
                          const int32_t *token_row, size_t T, size_t d, size_t k, int has_shared,
                          void *moe_out, const float *res, void *out, int out_dtype,
-                         void *stream) {
+                         void *stream, bool y_last_use) {
   PRICHS_REQUIRE(dtype_ok(out_dtype), "combine_residual: bad out dtype");
   PRICHS_REQUIRE(k >= 1 && k <= PRICHS_MAX_TOPK, "combine_residual: bad k=%zu", k);
   if (T == 0) return PRICHS_OK;
@@ -669,29 +719,37 @@ int moe_combine_residual(const void *y, const int32_t *topk_idx, const float *to
                      ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(moe_out) |
                        reinterpret_cast<uintptr_t>(res) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
   if (!fused) {
-    int rc = prichs_moe_combine(y, PRICHS_DTYPE_BF16, topk_idx, topk_w, token_row, T, d, k,
-                                has_shared, moe_out, PRICHS_DTYPE_BF16, stream);
+    int rc = moe_combine(y, PRICHS_DTYPE_BF16, topk_idx, topk_w, token_row, T, d, k, has_shared,
+                         moe_out, PRICHS_DTYPE_BF16, stream, y_last_use);
     if (rc) return rc;
     return prichs_add(res, PRICHS_DTYPE_F32, moe_out, PRICHS_DTYPE_BF16, out, out_dtype, T * d,
                       stream);
   }
   hipStream_t s = as_stream(stream);
   const unsigned grid = grid_for(T * (d / 8));
-#define PRICHS_COMBINE_RES(OT_, KC_)                                                          \
-  hipLaunchKernelGGL((combine_residual_kernel<OT_, KC_>), dim3(grid), dim3(256), 0, s,        \
+#define PRICHS_COMBINE_RES(OT_, KC_, NT_)                                                     \
+  hipLaunchKernelGGL((combine_residual_kernel<OT_, KC_, NT_>), dim3(grid), dim3(256), 0, s,   \
                      static_cast<const bf16_t *>(y), topk_idx, topk_w, token_row, (int)T,     \
                      (int)d, (int)k, has_shared, static_cast<bf16_t *>(moe_out), res,         \
                      static_cast<OT_ *>(out))
   if (out_dtype == PRICHS_DTYPE_BF16) {
-    if (k == 2)
-      PRICHS_COMBINE_RES(bf16_t, 2);
-    else
-      PRICHS_COMBINE_RES(bf16_t, 0);
+    if (k == 2) {
+      if (y_last_use)
+        PRICHS_COMBINE_RES(bf16_t, 2, true);
+      else
+        PRICHS_COMBINE_RES(bf16_t, 2, false);
+    } else {
+      PRICHS_COMBINE_RES(bf16_t, 0, false);
+    }
   } else {
-    if (k == 2)
-      PRICHS_COMBINE_RES(float, 2);
-    else
-      PRICHS_COMBINE_RES(float, 0);
+    if (k == 2) {
+      if (y_last_use)
+        PRICHS_COMBINE_RES(float, 2, true);
+      else
+        PRICHS_COMBINE_RES(float, 2, false);
+    } else {
+      PRICHS_COMBINE_RES(float, 0, false);
+    }
   }
 #undef PRICHS_COMBINE_RES
   PRICHS_LAUNCH_CHECK("combine_residual launch");

@@ -487,19 +487,28 @@ static int moe_forward_impl(prichs_moe_engine *eng, const void *x, size_t T,
 static int moe_finish(prichs_moe_engine *eng, size_t T, void *out, int out_dtype, void *stream,
                       const float *residual, void *moe_out, bool tm, hipEvent_t *ev) {
   hipStream_t s = as_stream(stream);
+  // Without the backward nothing reads y after the combine, so the combine
+  // streams it (non-temporal loads): the 75 MB of y at config 2 then no longer
+  // push the layer's weights out of the memory-side cache between forwards
+  // (repeated config-2 forwards: 5-11 us less per layer by box, although the
+  // combine itself takes 2 us more; with flushed caches 3 us more).  With the
+  // backward enabled the rows pass reads y again, and streaming it cost 2 us
+  // per training step.
+  const bool y_last_use = !eng->bwd;
   int rc;
   if (residual != nullptr && eng->dtype == PRICHS_DTYPE_BF16) {
     rc = moe_combine_residual(eng->y, eng->topk_idx, eng->topk_w, eng->token_row, T, eng->d,
-                              eng->k, (int)eng->S, moe_out, residual, out, out_dtype, stream);
+                              eng->k, (int)eng->S, moe_out, residual, out, out_dtype, stream,
+                              y_last_use);
   } else if (residual != nullptr) {
-    rc = prichs_moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T,
-                            eng->d, eng->k, (int)eng->S, moe_out, PRICHS_DTYPE_BF16, stream);
+    rc = moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T, eng->d,
+                     eng->k, (int)eng->S, moe_out, PRICHS_DTYPE_BF16, stream, y_last_use);
     if (!rc)
       rc = prichs_add(residual, PRICHS_DTYPE_F32, moe_out, PRICHS_DTYPE_BF16, out, out_dtype,
                       T * eng->d, stream);
   } else {
-    rc = prichs_moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T,
-                            eng->d, eng->k, (int)eng->S, out, out_dtype, stream);
+    rc = moe_combine(eng->y, eng->dtype, eng->topk_idx, eng->topk_w, eng->token_row, T, eng->d,
+                     eng->k, (int)eng->S, out, out_dtype, stream, y_last_use);
   }
   if (rc) return rc;
   if (tm) PRICHS_HIP_TRY(hipEventRecord(ev[5], s), "engine_forward: event");
