@@ -558,7 +558,16 @@ __device__ __forceinline__ void wgrad_item(
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (dst[e]) *reinterpret_cast<float4 *>(dst[e]) = make_float4(v[e][0], v[e][1], v[e][2], v[e][3]);
+        if (dst[e]) {
+          // The gradients go back to the caller and nothing in the step reads
+          // them again: non-temporal stores keep their 211 MB (config 2) out
+          // of the memory-side cache (training step -15 us).  Split-K
+          // partials are read right after by the reduce pass: plain stores.
+          if (pbase == nullptr)
+            __builtin_nontemporal_store(v[e], reinterpret_cast<f32x4 *>(dst[e]));
+          else
+            *reinterpret_cast<float4 *>(dst[e]) = make_float4(v[e][0], v[e][1], v[e][2], v[e][3]);
+        }
     }
     if (h + 1 < kPasses) __syncthreads();  // the next pass reuses the LDS rows
   }
@@ -781,7 +790,8 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float *__restri
           r.z = d.z + r.z;
           r.w = d.w + r.w;
         }
-        *reinterpret_cast<float4 *>(dst[w]) = r;
+        // The finished gradient: non-temporal, as in the tile kernel.
+        __builtin_nontemporal_store(f32x4{r.x, r.y, r.z, r.w}, reinterpret_cast<f32x4 *>(dst[w]));
       }
     }
   }

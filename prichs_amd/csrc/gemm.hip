@@ -644,7 +644,11 @@ __device__ __forceinline__ void bf16_tile(
       // Training forward: the gate/up pre-activations too, [rows][Np] in
       // packed column order (the backward's SwiGLU derivative needs them),
       // through a row-major copy of the tile in LDS and written as whole
-      // 512-byte rows, as the down epilogue writes its tile.
+      // 512-byte rows, as the down epilogue writes its tile.  Nothing reads
+      // them until the backward's dA epilogue, so the stores are
+      // non-temporal: the 126 MB at config 2 leave the memory-side cache to
+      // the forward's weights and activations (training forward 335.5 ->
+      // 328.8 us, step -6.9 us).
       constexpr int kS = Cf::kStgStride;
       lds_barrier();  // every wave is done reading the ring
       const int tcol = wn * WN + cq;
@@ -665,8 +669,9 @@ __device__ __forceinline__ void bf16_tile(
         const int r = c / kChunksRow, ch = c - r * kChunksRow;
         const int m = m0 + r;
         if (m < mg)
-          *reinterpret_cast<u32x4 *>(P + (long long)(row0 + m) * Np + n0 + 8 * ch) =
-              *reinterpret_cast<const u32x4 *>(lds + r * kS + 8 * ch);
+          __builtin_nontemporal_store(
+              *reinterpret_cast<const u32x4 *>(lds + r * kS + 8 * ch),
+              reinterpret_cast<u32x4 *>(P + (long long)(row0 + m) * Np + n0 + 8 * ch));
       }
     } else if (P != nullptr) {
 #pragma unroll
