@@ -557,7 +557,9 @@ def main():
                         "bytes": combine_bytes, **copy_ref["combine"]},
             "peak_GB/s": PEAK_HBM_GBPS,
             "note": "flushed = L2 and MALL overwritten (512 MiB) before each forward, outside the "
-                    "stage intervals; the combine reads y right after the down GEMM wrote it; "
+                    "stage intervals; the combine reads y right after the down GEMM wrote it, with "
+                    "non-temporal loads (y is dead afterwards, so it leaves the caches to the "
+                    "weights of the next forward; the combine itself is slower for it); "
                     "copy_same_bytes* = the library's streaming copy (prichs_hbm_copy) of the "
                     "stage's bytes, timed the same way; frac_of_copy = copy ms / stage ms",
         },
