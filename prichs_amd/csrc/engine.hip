@@ -490,7 +490,7 @@ static int moe_finish(prichs_moe_engine *eng, size_t T, void *out, int out_dtype
   // Without the backward nothing reads y after the combine, so the combine
   // streams it (non-temporal loads): the 75 MB of y at config 2 then no longer
   // push the layer's weights out of the memory-side cache between forwards
-  // (repeated config-2 forwards: 5-11 us less per layer by box, although the
+  // (repeated config-2 forwards: 2-11 us less per layer by box, although the
   // combine itself takes 2 us more; with flushed caches 3 us more).  With the
   // backward enabled the rows pass reads y again, and streaming it cost 2 us
   // per training step.
